@@ -1,0 +1,118 @@
+/*
+ * vocalarc_hip.h -- harness C-ABI of the MI355X (gfx950) VocalArc provider.
+ *
+ * The reference host reaches the GPU only through native_gpu.h (declared in
+ * this directory as well).  That ABI is bound to the host's compile-time
+ * shape (dim 256, 90 bands, hop 512, GELU) and never sees the STFT, iSTFT or
+ * band split.  These entry points expose the same device path with the shape
+ * as data, so the benchmark configurations (dim 384, 62 bands, hop 441,
+ * GELU-GLU, chunked 5-minute input) run through the same kernels.  Each
+ * function names the reference function whose computation it performs.
+ *
+ * Conventions: plain pointers and sizes only.  Pointers documented as
+ * "device" are device memory owned by the caller; the library allocates its
+ * own scratch.  Work is issued on the context's stream (default: the null
+ * stream; see vh_set_stream) and is complete when vh_synchronize returns.
+ * Functions return 1 on success and 0 on failure (message: vh_last_error).
+ */
+#ifndef VOCALARC_HIP_H
+#define VOCALARC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VH_MAX_BANDS 256
+
+/* Model shape; the reference fixes these at compile time
+   (native/vocalarc_separation.c:33-57).  Same field order as the oracle's. */
+typedef struct {
+    int dim, depth, bands, heads, dim_head, ff_dim;
+    int ffn_glu;      /* 0: Linear->GELU (reference FFN), 1: GELU-GLU   */
+    int gated;        /* 1: per-head sigmoid gates (reference)           */
+    int mask_hidden;  /* mask-estimator hidden width (reference: FF_DIM) */
+    int n_fft, hop, channels;
+    int band_widths[VH_MAX_BANDS];
+} vh_dims;
+
+typedef struct vh_context vh_context;
+typedef struct vh_model vh_model;
+
+/* ---- context ----------------------------------------------------------- */
+vh_context *vh_create(void);
+void vh_destroy(vh_context *ctx);
+int vh_set_stream(vh_context *ctx, void *hip_stream);
+int vh_synchronize(vh_context *ctx);
+const char *vh_last_error(void);
+const char *vh_device_name(vh_context *ctx);
+
+/* ---- isolated kernels on device buffers --------------------------------- */
+/* RMSNorm rows: y = x * sqrt(dim)/sqrt(sum x^2 + 1e-12) * gamma
+   (native/vocalarc_separation.c:419-424, native/native_simd.c:98-121). */
+int vh_rmsnorm(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, float *y);
+/* Row softmax over [rows][len] (native/native_gpu_cuda.cu:357-381). */
+int vh_softmax_rows(vh_context *ctx, int64_t rows, int len, const float *in, float *out);
+/* Rotary embedding in place on [bh][len][dim_head] with base 10000
+   (native/vocalarc_separation.c:692-744). dim_head must be 64. */
+int vh_rope_bhld(vh_context *ctx, int64_t bh, int len, int dim_head, float *x);
+/* GELU-GLU: in[rows][2*width] = [value|gate] -> out[rows][width]. */
+int vh_geglu(vh_context *ctx, int64_t rows, int width, const float *in, float *out);
+/* x[n] += r[n] (native/vocalarc_separation.c:820-834). */
+int vh_residual_add(vh_context *ctx, int64_t n, float *x, const float *r);
+/* C[M][N] (op)= A[M][K] * W[N][K]^T (+bias): the token-wise linear
+   (native/vocalarc_separation.c:631-636).  epilogue: 0 store, 1 GELU,
+   2 tanh, 3 residual (C +=), 4 GELU-GLU on interleaved columns. */
+int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const float *W, int ldw,
+            const float *bias, float *C, int ldc, int epilogue);
+/* Fused attention core over qkv[S*L][3*H*64] (rotary applied here):
+   native/vocalarc_separation.c:692-793.  out[S*L][H*64]. */
+int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, float *out,
+                 int apply_rotary);
+
+/* ---- model -------------------------------------------------------------- */
+/* Upload a VSCNAT01 pack (native/vocalarc_separation.c:528-589) laid out for
+   `dims` from host memory.  Returns NULL on a malformed pack. */
+vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const void *pack, size_t bytes);
+void vh_model_free(vh_model *model);
+/* One axial transformer (native/vocalarc_separation.c:836-873) in place on
+   device x[S][L][dim]; axis 0 = time weights, 1 = band weights. */
+int vh_transformer(vh_context *ctx, vh_model *model, int layer, int axis, float *x, int sequences, int length);
+/* STFT (native/vocalarc_separation.c:1044-1072): device audio[C][length] ->
+   device source[F][C][T][2], T = length/hop + 1. */
+int vh_stft(vh_context *ctx, vh_model *model, const float *audio, int length, float *source);
+/* Complex mask multiply + iSTFT + overlap-add
+   (native/vocalarc_separation.c:1084-1136) -> device audio[C][length]. */
+int vh_istft(vh_context *ctx, vh_model *model, const float *source, const float *mask, int length, float *audio);
+/* Band split (native/vocalarc_separation.c:887-926): device source -> device
+   time_sequences[B][T][dim]. */
+int vh_band_split(vh_context *ctx, vh_model *model, const float *source, int frames, float *time_sequences);
+/* Mask estimator (native/vocalarc_separation.c:1316-1340, all bands) on
+   final-normed device features[T][B][dim] -> device mask[F][C][T][2]. */
+int vh_mask_estimate(vh_context *ctx, vh_model *model, const float *features, int frames, float *mask);
+/* Whole forward of one window (native/vocalarc_separation.c:1342-1445):
+   device audio[C][length] -> device vocals[C][length]. */
+int vh_forward(vh_context *ctx, vh_model *model, const float *audio, int length, float *vocals);
+/* Chunked separation of a long device audio[C][length]: windows of `chunk`
+   samples every `step` samples (zero-padded at the end), `batch` windows per
+   device pass, linear cross-fade over the overlap normalised by the summed
+   fade weights.  No reference counterpart (the reference host runs the whole
+   file as one window, native/vocalarc_separation.c:1344). */
+int vh_separate(vh_context *ctx, vh_model *model, const float *audio, int length, int chunk, int step, int batch,
+                float *vocals);
+
+/* ---- measurement --------------------------------------------------------- */
+/* Per-kernel-class timing with HIP events on the context stream. */
+int vh_timing_enable(vh_context *ctx, int enable);
+int vh_timing_reset(vh_context *ctx);
+/* Total milliseconds and launch count of a kernel class since the last reset
+   (after vh_synchronize).  Returns 0 if the class never ran. */
+int vh_timing_get(vh_context *ctx, const char *name, double *total_ms, int64_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

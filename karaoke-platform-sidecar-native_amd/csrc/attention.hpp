@@ -1,0 +1,221 @@
+// Fused axial attention on CDNA4 fp32 matrix cores.
+//
+// Computes, for every (sequence, head, query), the softmax-weighted sum over
+// all keys of one axial sequence, with the rotary embedding applied to q and
+// k as they are loaded and the per-head sigmoid gate applied at the store.
+// This is the whole of native/vocalarc_separation.c:692-818 (rotary,
+// attention_heads, apply_gates) for one transformer in one launch; the
+// reference CUDA provider spends 5 launches and a materialised score matrix
+// on it (native/native_gpu_cuda.cu:497-538).
+//
+// Layout: q, k, v and the gate logits live in one row per token of the fused
+// QKV(+gate) projection (q at column 0, k at `inner`, v at 2*inner, gates at
+// `gate_col`).  A token of sequence s at position p sits in row
+//   (s / group) * group_stride + (s % group) * seq_stride + p * pos_stride,
+// so the same kernel reads the time axis and the band axis of one physical
+// [frames][bands] activation tensor without a transpose.
+//
+// Per wavefront: 32 queries.  For each block of 32 keys the wave computes
+// S^T = K * Q^T with v_mfma_f32_32x32x2f32, which leaves every lane holding
+// 16 scores of ONE query (rows = keys).  The online-softmax statistics are
+// therefore lane-local plus one exchange with the partner half-wave, and the
+// probabilities are already in the B-operand layout of O^T += V^T * P^T: step
+// s of that MFMA consumes register s.  V is staged transposed in LDS so its
+// A operand is one ds_read_b128 per four MFMAs.
+#pragma once
+
+#include "common.hpp"
+
+namespace vh {
+
+struct AttnArgs {
+    const float *qkv;  // fused projection rows
+    int ld;            // row pitch of qkv (floats)
+    float *out;        // [rows][ld_out], head h at column h*64
+    int ld_out;
+    const float *rope_cos;  // [L][32], may be null (no rotary)
+    const float *rope_sin;
+    int S, L, H;
+    int group, group_stride, seq_stride, pos_stride;
+    int inner;      // H * 64
+    int gate_col;   // < 0: no gates
+    float scale;    // 1/sqrt(64)
+};
+
+constexpr int ATT_DH = 64;
+constexpr int ATT_KB = 32;             // keys per block
+constexpr int ATT_KPITCH = ATT_DH + 4; // K tile row pitch
+constexpr int ATT_VPITCH = ATT_KB + 4; // V^T tile row pitch
+
+VH_DEVICE int attn_row(const AttnArgs &a, int s, int p) {
+    return (s / a.group) * a.group_stride + (s % a.group) * a.seq_stride + p * a.pos_stride;
+}
+
+// Rotate the two interleaved pairs of a float4 that starts at dimension d0.
+VH_DEVICE floatx4 rope4(floatx4 v, const float *cs, const float *sn, int pos, int d0) {
+    if (cs == nullptr) return v;
+    const int pi = pos * (ATT_DH / 2) + (d0 >> 1);
+    float c0 = cs[pi], s0 = sn[pi], c1 = cs[pi + 1], s1 = sn[pi + 1];
+    floatx4 r;
+    r[0] = v[0] * c0 - v[1] * s0;
+    r[1] = v[0] * s0 + v[1] * c0;
+    r[2] = v[2] * c1 - v[3] * s1;
+    r[3] = v[2] * s1 + v[3] * c1;
+    return r;
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attention_kernel(AttnArgs a) {
+    constexpr int NT = 64 * WAVES;
+    constexpr int KV_F4 = ATT_KB * ATT_DH / 4;             // float4s per K (or V) tile
+    constexpr int PER_T = (KV_F4 + NT - 1) / NT;           // per thread
+    __shared__ __attribute__((aligned(16))) float Ks[2][ATT_KB][ATT_KPITCH];
+    __shared__ __attribute__((aligned(16))) float Vt[2][ATT_DH][ATT_VPITCH];
+
+    const int qgroups = (a.L + 32 * WAVES - 1) / (32 * WAVES);
+    const int task = (int)blockIdx.x;
+    const int qg = task % qgroups;
+    const int sh = task / qgroups;
+    const int h = sh % a.H;
+    const int s = sh / a.H;
+
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int q0 = (qg * WAVES + wave) * 32;
+    const bool wave_active = q0 < a.L;
+
+    const int kcol = a.inner + h * ATT_DH;
+    const int vcol = 2 * a.inner + h * ATT_DH;
+
+    // Q for query q0+li, dims 8g + 4lh .. +3, rotated and pre-scaled (the
+    // scale 1/8 is a power of two, so this is exact).
+    floatx4 qr[8];
+    {
+        const int q = min(q0 + li, a.L - 1);
+        const float *qp = a.qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int d0 = 8 * g + 4 * lh;
+            floatx4 v = rope4(ld4(qp + d0), a.rope_cos, a.rope_sin, q, d0);
+            qr[g] = v * a.scale;
+        }
+    }
+
+    floatx4 kreg[PER_T], vreg[PER_T];
+    auto load = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) {
+            const int e = tid + NT * i;
+            if (e < KV_F4) {
+                const int kk = e >> 4, d0 = 4 * (e & 15);
+                const int p = kb * ATT_KB + kk;
+                if (p < a.L) {
+                    const size_t row = (size_t)attn_row(a, s, p) * a.ld;
+                    kreg[i] = rope4(ld4(a.qkv + row + kcol + d0), a.rope_cos, a.rope_sin, p, d0);
+                    vreg[i] = ld4(a.qkv + row + vcol + d0);
+                } else {
+                    kreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    vreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) {
+            const int e = tid + NT * i;
+            if (e < KV_F4) {
+                const int kk = e >> 4, d0 = 4 * (e & 15);
+                st4(&Ks[buf][kk][d0], kreg[i]);
+                Vt[buf][d0 + 0][kk] = vreg[i][0];
+                Vt[buf][d0 + 1][kk] = vreg[i][1];
+                Vt[buf][d0 + 2][kk] = vreg[i][2];
+                Vt[buf][d0 + 3][kk] = vreg[i][3];
+            }
+        }
+    };
+
+    floatx16 o[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[t][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int nkb = (a.L + ATT_KB - 1) / ATT_KB;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb++) {
+        const int buf = kb & 1;
+        if (kb + 1 < nkb) load(kb + 1);
+        if (wave_active) {
+            floatx16 sc;
+#pragma unroll
+            for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                floatx4 kf = ld4(&Ks[buf][li][8 * g + 4 * lh]);
+#pragma unroll
+                for (int r = 0; r < 4; r++) sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[r], qr[g][r], sc, 0, 0, 0);
+            }
+            // sc[r]: score of key kb*32 + 8*(r/4) + 4*lh + r%4 for query q0+li
+            const int valid = a.L - kb * ATT_KB;
+            float mb = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (key >= valid) sc[r] = -INFINITY;
+                mb = fmaxf(mb, sc[r]);
+            }
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+            const float m_new = fmaxf(m_run, mb);
+            const float alpha = fast_exp_dev(m_run - m_new);
+            float ls = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                sc[r] = fast_exp_dev(sc[r] - m_new);
+                ls += sc[r];
+            }
+            l_run = l_run * alpha + ls;
+            m_run = m_new;
+#pragma unroll
+            for (int t = 0; t < 2; t++) o[t] *= alpha;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++) {
+                    floatx4 vf = ld4(&Vt[buf][32 * t + li][8 * qq + 4 * lh]);
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[r], sc[4 * qq + r], o[t], 0, 0, 0);
+                }
+        }
+        if (kb + 1 < nkb) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (!wave_active) return;
+    // Both half-waves hold partial row sums of the same query; combine them
+    // while every lane of the wave is still active.
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const int q = q0 + li;
+    if (q >= a.L) return;
+    const float inv = 1.0f / l_tot;
+    const int row = attn_row(a, s, q);
+    float gate = 1.0f;
+    if (a.gate_col >= 0) gate = sigmoid_dev(a.qkv[(size_t)row * a.ld + a.gate_col + h]);
+    float *op = a.out + (size_t)row * a.ld_out + h * ATT_DH;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            floatx4 v;
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = (o[t][4 * rq + r] * inv) * gate;
+            st4(op + 32 * t + 8 * rq + 4 * lh, v);
+        }
+}
+
+}  // namespace vh

@@ -1,0 +1,57 @@
+// Shared device helpers for the gfx950 kernels of the VocalArc HIP provider.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+#define VH_DEVICE __device__ __forceinline__
+
+// 64-lane wavefront reductions through cross-lane permutes.
+VH_DEVICE float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+VH_DEVICE float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// exp(x) through the hardware base-2 exponential.
+VH_DEVICE float fast_exp_dev(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+VH_DEVICE float sigmoid_dev(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+VH_DEVICE float gelu_dev(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865475f)); }
+
+VH_DEVICE floatx4 ld4(const float *p) { return *reinterpret_cast<const floatx4 *>(p); }
+VH_DEVICE void st4(float *p, floatx4 v) { *reinterpret_cast<floatx4 *>(p) = v; }
+
+// Non-temporal streaming variants for data touched exactly once.
+VH_DEVICE floatx4 ld4_stream(const float *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(p));
+}
+VH_DEVICE void st4_stream(float *p, floatx4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(p));
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X
+// (workgroup i runs on XCD i % 8).  Remapping the linear id so that each XCD
+// owns a contiguous range of tiles keeps neighbouring tiles (which share
+// operand rows) in the same L2.
+VH_DEVICE int xcd_swizzle(int id, int count) {
+    const int xcds = 8;
+    int per = count / xcds;
+    int rem = count % xcds;
+    int xcd = id % xcds;
+    int local = id / xcds;
+    // XCDs [0, rem) own per+1 tiles, the rest own per tiles.
+    int base = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
+    int mine = xcd < rem ? per + 1 : per;
+    return local < mine ? base + local : id;  // tail ids (never produced when count % 8 == 0) keep their id
+}

@@ -1,0 +1,269 @@
+// Bandwidth-bound kernels: one pass over HBM each, 16-byte accesses,
+// wave64 shuffle reductions (no LDS round trips for row statistics).
+#pragma once
+
+#include "common.hpp"
+
+namespace vh {
+
+// ---------------------------------------------------------------- RMSNorm
+// y = x * (sqrt(d) / sqrt(sum(x^2) + 1e-12)) * gamma
+// (native/vocalarc_separation.c:419-424, native/native_simd.c:98-121).
+// One wavefront per row, the row held in registers between the two passes.
+template <int MAXV>
+static __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, int ldx,
+                                                      const float *__restrict__ gamma,
+                                                      float *__restrict__ y, int ldy, int rows, int dim) {
+    const int row = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
+    const int lane = (int)threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + (size_t)row * ldx;
+    float *yr = y + (size_t)row * ldy;
+    const int nv = dim >> 2;
+    floatx4 v[MAXV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) {
+        const int c = lane + 64 * i;
+        if (c < nv) {
+            v[i] = ld4(xr + 4 * c);
+            ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = sqrtf((float)dim) / sqrtf(ss + 1.0e-12f);
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) {
+        const int c = lane + 64 * i;
+        if (c < nv) st4(yr + 4 * c, (v[i] * inv) * ld4(gamma + 4 * c));
+    }
+}
+
+// ------------------------------------------------------------ row softmax
+// Materialised softmax of score rows (max, exp, sum, divide), the
+// decomposition of native/native_gpu_cuda.cu:357-381.  Rows need not be
+// 16-byte aligned (801-float rows), so accesses are 4-byte and coalesced.
+template <int MAXN>
+static __global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restrict__ in,
+                                                           float *__restrict__ out, int64_t rows, int len) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
+    const int lane = (int)threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = in + row * len;
+    float *yr = out + row * len;
+    float v[MAXN];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MAXN; i++) {
+        const int c = lane + 64 * i;
+        v[i] = c < len ? __builtin_nontemporal_load(xr + c) : -INFINITY;
+        m = fmaxf(m, v[i]);
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXN; i++) {
+        v[i] = fast_exp_dev(v[i] - m);
+        s += v[i];
+    }
+    s = wave_sum(s);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < MAXN; i++) {
+        const int c = lane + 64 * i;
+        if (c < len) __builtin_nontemporal_store(v[i] * inv, yr + c);
+    }
+}
+
+// --------------------------------------------------------- rotary [BH][L][64]
+// Interleaved-pair rotation (native/vocalarc_separation.c:692-711) with the
+// host-built cos/sin table [L][32] (native/vocalarc_separation.c:726-731).
+static __global__ __launch_bounds__(256) void rope_bhld_kernel(float *__restrict__ x, const float *__restrict__ cs,
+                                                        const float *__restrict__ sn, int64_t n4, int len) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n4) return;
+    const int c4 = (int)(e & 15);           // float4 within the 64-wide head row
+    const int pos = (int)((e >> 4) % len);  // position
+    float *p = x + 4 * e;
+    floatx4 v = ld4(p);
+    const int pi = pos * 32 + 2 * c4;
+    const float c0 = cs[pi], s0 = sn[pi], c1 = cs[pi + 1], s1 = sn[pi + 1];
+    floatx4 r;
+    r[0] = v[0] * c0 - v[1] * s0;
+    r[1] = v[0] * s0 + v[1] * c0;
+    r[2] = v[2] * c1 - v[3] * s1;
+    r[3] = v[2] * s1 + v[3] * c1;
+    st4(p, r);
+}
+
+// ------------------------------------------------------------- GELU-GLU
+// in[rows][2w] = [value | gate] -> out[rows][w] = value * gelu(gate)
+static __global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ in, float *__restrict__ out,
+                                                    int64_t rows, int width) {
+    const int w4 = width >> 2;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= rows * w4) return;
+    const int64_t r = e / w4;
+    const int c = (int)(e % w4);
+    const float *ir = in + r * 2 * width;
+    floatx4 v = ld4_stream(ir + 4 * c);
+    floatx4 g = ld4_stream(ir + width + 4 * c);
+    floatx4 o;
+#pragma unroll
+    for (int k = 0; k < 4; k++) o[k] = v[k] * gelu_dev(g[k]);
+    st4_stream(out + r * width + 4 * c, o);
+}
+
+// ----------------------------------------------------------- residual add
+// x += r (native/vocalarc_separation.c:820-834)
+static __global__ __launch_bounds__(256) void residual_add_kernel(float *__restrict__ x, const float *__restrict__ r,
+                                                           int64_t n4) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n4) return;
+    st4_stream(x + 4 * e, ld4_stream(x + 4 * e) + ld4_stream(r + 4 * e));
+}
+
+// ------------------------------------------------------------ GELU (in place)
+static __global__ __launch_bounds__(256) void gelu_kernel(float *__restrict__ x, int64_t n) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e < n) x[e] = gelu_dev(x[e]);
+}
+
+// --------------------------------------------------------- weight unpack
+// Packed layout (native/vocalarc_separation.c:428-457: full 32-wide output
+// tiles [in][32], then the out%32 tail [in][tail]) -> [row][in] rows of the
+// destination.  mode 0: row = dst_row0 + o.  mode 1 (GELU-GLU interleave):
+// value output c (o < out/2) and gate output c (o >= out/2) go to rows
+// (c/32)*64 + c%32 and (c/32)*64 + 32 + c%32, so a 64-column GEMM tile holds
+// 32 values and their 32 gates.
+static __global__ __launch_bounds__(256) void unpack_weight_kernel(const float *__restrict__ packed, int in, int out,
+                                                            float *__restrict__ dst, int ldd, int dst_row0,
+                                                            int mode) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)in * out) return;
+    const int i = (int)(e % in);
+    const int o = (int)(e / in);
+    const int full = (out / 32) * 32;
+    float v;
+    if (o < full) v = packed[(size_t)(o / 32) * in * 32 + (size_t)i * 32 + (o % 32)];
+    else v = packed[(size_t)full * in + (size_t)i * (out - full) + (o - full)];
+    int row = o;
+    if (mode == 1) {
+        const int half = out / 2;
+        const int g = o >= half ? 1 : 0;
+        const int c = o - g * half;
+        row = (c / 32) * 64 + 32 * g + (c % 32);
+    }
+    dst[(size_t)(dst_row0 + row) * ldd + i] = v;
+}
+
+// Vector permutation matching mode 1 of unpack_weight_kernel.
+static __global__ __launch_bounds__(256) void interleave_glu_bias_kernel(const float *__restrict__ src, float *__restrict__ dst,
+                                                                  int out) {
+    const int o = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (o >= out) return;
+    const int half = out / 2;
+    const int g = o >= half ? 1 : 0;
+    const int c = o - g * half;
+    dst[(c / 32) * 64 + 32 * g + (c % 32)] = src[o];
+}
+
+// ------------------------------------------------- token-row transposes
+// [outer][a][b][D] -> [outer][b][a][D]: whole D-float rows move, so reads and
+// writes are both contiguous 16-byte streams.
+static __global__ __launch_bounds__(256) void transpose_rows_kernel(const float *__restrict__ src, float *__restrict__ dst,
+                                                             int outer, int a, int b, int d4) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)outer * a * b * d4;
+    if (e >= total) return;
+    const int c = (int)(e % d4);
+    const int64_t tok = e / d4;            // source token index within outer: (i, j)
+    const int j = (int)(tok % b);
+    const int64_t t2 = tok / b;
+    const int i = (int)(t2 % a);
+    const int64_t ot = t2 / a;
+    const int64_t dt = (ot * b + j) * a + i;
+    st4(dst + dt * 4 * d4 + 4 * c, ld4(src + tok * 4 * d4 + 4 * c));
+}
+
+// --------------------------------------------------------- band split gather
+// For band b and spectrogram row m (= chunk*T + t) gather the band's bins from
+// source[chunk][F][C][T][2] in (frequency, channel, re/im) order, RMS-normalise
+// with the band gamma and write row m of the band's input matrix
+// (native/vocalarc_separation.c:887-912).
+struct BandTable {
+    int first_freq[256];
+    int width[256];
+    int64_t in_offset[256];  // float offset of the band's [M][4w] input matrix
+    const float *gamma[256];
+};
+
+static __global__ __launch_bounds__(256) void band_gather_norm_kernel(const float *__restrict__ source,
+                                                               const BandTable *__restrict__ tab,
+                                                               float *__restrict__ bandin, int M, int T, int F,
+                                                               int C) {
+    const int b = (int)blockIdx.y;
+    const int m = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
+    const int lane = (int)threadIdx.x & 63;
+    if (m >= M) return;
+    const int chunk = m / T, t = m % T;
+    const int w = tab->width[b], ff = tab->first_freq[b];
+    const int in_dim = w * C * 2;
+    const int pairs = w * C;
+    const float *src = source + (size_t)chunk * F * C * T * 2;
+    float *dst = bandin + tab->in_offset[b] + (size_t)m * in_dim;
+    const float *gamma = tab->gamma[b];
+    constexpr int MAXP = 5;  // up to 320 (frequency, channel) pairs per band
+    float2 v[MAXP];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXP; k++) {
+        const int j = lane + 64 * k;
+        if (j < pairs) {
+            const int f = j / C, c = j % C;
+            v[k] = *reinterpret_cast<const float2 *>(src + (((size_t)(ff + f) * C + c) * T + t) * 2);
+            ss += v[k].x * v[k].x + v[k].y * v[k].y;
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = sqrtf((float)in_dim) / sqrtf(ss + 1.0e-12f);
+#pragma unroll
+    for (int k = 0; k < MAXP; k++) {
+        const int j = lane + 64 * k;
+        if (j < pairs) {
+            float2 o;
+            o.x = (v[k].x * inv) * gamma[2 * j];
+            o.y = (v[k].y * inv) * gamma[2 * j + 1];
+            *reinterpret_cast<float2 *>(dst + 2 * j) = o;
+        }
+    }
+}
+
+// ------------------------------------------------------ mask GLU + scatter
+// proj_b[m][2*dim] (bias included) -> mask[chunk][F][C][T][2]:
+// m_i = p_i * sigmoid(p_{dim+i}), i -> (frequency i/(2C), channel (i/2)%C,
+// component i%2) (native/vocalarc_separation.c:1330-1338).
+struct MaskTable {
+    int first_freq[256];
+    int dim[256];            // 4w
+    int64_t proj_offset[256];
+};
+
+static __global__ __launch_bounds__(256) void mask_glu_scatter_kernel(const float *__restrict__ proj,
+                                                               const MaskTable *__restrict__ tab,
+                                                               float *__restrict__ mask, int M, int T, int F,
+                                                               int C) {
+    const int b = (int)blockIdx.y;
+    const int dim = tab->dim[b];
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)M * dim) return;
+    const int m = (int)(e / dim), i = (int)(e % dim);
+    const int chunk = m / T, t = m % T;
+    const float *p = proj + tab->proj_offset[b] + (size_t)m * 2 * dim;
+    const float val = p[i] * (1.0f / (1.0f + __expf(-p[dim + i])));
+    const int f = tab->first_freq[b] + i / (2 * C);
+    const int c = (i / 2) % C, comp = i & 1;
+    mask[(size_t)chunk * F * C * T * 2 + (((size_t)f * C + c) * T + t) * 2 + comp] = val;
+}
+
+}  // namespace vh

@@ -1,0 +1,402 @@
+// Launchers, buffers, weight upload and the device transformer block.
+#include "runtime.hpp"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+
+#include "attention.hpp"
+#include "elementwise.hpp"
+#include "gemm.hpp"
+
+namespace vh {
+
+// ----------------------------------------------------------------- errors
+static std::mutex g_err_mu;
+static char g_err[1024] = "";
+
+void set_error(const char *fmt, ...) {
+    std::lock_guard<std::mutex> lock(g_err_mu);
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+const char *last_error() { return g_err; }
+
+bool check(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_error("%s failed: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+bool debug_enabled() {
+    static int on = -1;
+    if (on < 0) on = getenv("VOCALARC_GPU_DEBUG") != nullptr;
+    return on != 0;
+}
+
+// After each launch: pick up launch errors; in debug mode synchronise and log
+// (native/native_gpu_cuda.cu:487-495 offers the same switch).
+bool sync_debug(hipStream_t s, const char *what) {
+    if (!check(hipGetLastError(), what)) return false;
+    if (!debug_enabled()) return true;
+    bool ok = check(hipStreamSynchronize(s), what);
+    fprintf(stderr, "vocalarc-hip: %s %s\n", what, ok ? "ok" : last_error());
+    return ok;
+}
+
+// ---------------------------------------------------------------- buffers
+bool DeviceBuffer::ensure(size_t need, const char *what) {
+    if (need <= bytes && ptr != nullptr) return true;
+    release();
+    if (need == 0) need = 16;
+    if (!check(hipMalloc(&ptr, need), what)) {
+        ptr = nullptr;
+        return false;
+    }
+    bytes = need;
+    return true;
+}
+
+void DeviceBuffer::release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+// ----------------------------------------------------------------- timing
+void KernelTimer::begin(hipStream_t s, const char *, hipEvent_t *a) {
+    (void)hipEventCreate(a);
+    (void)hipEventRecord(*a, s);
+}
+
+void KernelTimer::end(hipStream_t s, const char *name, hipEvent_t a) {
+    hipEvent_t b;
+    (void)hipEventCreate(&b);
+    (void)hipEventRecord(b, s);
+    pending.push_back({name, a, b});
+}
+
+void KernelTimer::collect() {
+    for (auto &p : pending) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(p.b) == hipSuccess && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            auto &t = totals[p.name];
+            t.first += ms;
+            t.second += 1;
+        }
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    pending.clear();
+}
+
+void KernelTimer::reset() {
+    collect();
+    totals.clear();
+}
+
+// --------------------------------------------------------------- launchers
+static inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+static bool gemm_ok(const GemmArgs &g) {
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0) return false;
+    if (g.K % 4 || g.lda % 4 || g.ldb % 4) return false;
+    if (((uintptr_t)g.A | (uintptr_t)g.B) & 15) return false;
+    if (g.M > INT32_MAX / 2) return false;
+    return true;
+}
+
+template <int EPI>
+static void launch_epi(hipStream_t s, const GemmDesc *single, const GemmBatch *batch, unsigned tiles, unsigned n) {
+    if (single) hipLaunchKernelGGL(gemm_f32_kernel<EPI>, dim3(tiles), dim3(GEMM_THREADS), 0, s, *single);
+    else hipLaunchKernelGGL(gemm_f32_batched_kernel<EPI>, dim3(tiles, 1, n), dim3(GEMM_THREADS), 0, s, *batch);
+}
+
+static bool launch_gemm(hipStream_t s, int epi, const GemmDesc *single, const GemmBatch *batch, unsigned tiles,
+                        unsigned n) {
+    switch (epi) {
+        case EPI_STORE: launch_epi<EPI_STORE>(s, single, batch, tiles, n); break;
+        case EPI_GELU: launch_epi<EPI_GELU>(s, single, batch, tiles, n); break;
+        case EPI_TANH: launch_epi<EPI_TANH>(s, single, batch, tiles, n); break;
+        case EPI_RESIDUAL: launch_epi<EPI_RESIDUAL>(s, single, batch, tiles, n); break;
+        case EPI_GEGLU: launch_epi<EPI_GEGLU>(s, single, batch, tiles, n); break;
+        default: set_error("unknown GEMM epilogue %d", epi); return false;
+    }
+    return sync_debug(s, "gemm_f32_kernel");
+}
+
+static GemmDesc to_desc(const GemmArgs &g) {
+    GemmDesc d;
+    d.A = g.A; d.B = g.B; d.bias = g.bias; d.C = g.C;
+    d.M = (int)g.M; d.N = g.N; d.K = g.K;
+    d.lda = g.lda; d.ldb = g.ldb; d.ldc = g.ldc;
+    return d;
+}
+
+static int64_t tiles_of(const GemmArgs &g) {
+    return ((g.M + GEMM_BM - 1) / GEMM_BM) * ((g.N + GEMM_BN - 1) / GEMM_BN);
+}
+
+bool gemm(hipStream_t s, const GemmArgs &g, int epilogue, KernelTimer *t, const char *name) {
+    if (!gemm_ok(g)) {
+        set_error("gemm: unsupported shape M=%lld N=%d K=%d lda=%d ldb=%d", (long long)g.M, g.N, g.K, g.lda, g.ldb);
+        return false;
+    }
+    if (epilogue == EPI_GEGLU && g.N % 64) {
+        set_error("gemm: GELU-GLU needs N %% 64 == 0 (N=%d)", g.N);
+        return false;
+    }
+    GemmDesc d = to_desc(g);
+    Scope sc(t, s, name);
+    return launch_gemm(s, epilogue, &d, nullptr, (unsigned)tiles_of(g), 1);
+}
+
+bool gemm_batched(hipStream_t s, const std::vector<GemmArgs> &gs, int epilogue, KernelTimer *t, const char *name) {
+    Scope sc(t, s, name);
+    for (size_t first = 0; first < gs.size(); first += GEMM_MAX_BATCH) {
+        const size_t count = std::min(gs.size() - first, (size_t)GEMM_MAX_BATCH);
+        GemmBatch b;
+        memset(&b, 0, sizeof(b));
+        int64_t max_tiles = 0;
+        for (size_t i = 0; i < count; i++) {
+            const GemmArgs &g = gs[first + i];
+            if (!gemm_ok(g) || (epilogue == EPI_GEGLU && g.N % 64)) {
+                set_error("gemm_batched: unsupported shape M=%lld N=%d K=%d", (long long)g.M, g.N, g.K);
+                return false;
+            }
+            b.d[i] = to_desc(g);
+            max_tiles = std::max(max_tiles, tiles_of(g));
+        }
+        if (!launch_gemm(s, epilogue, nullptr, &b, (unsigned)max_tiles, (unsigned)count)) return false;
+    }
+    return true;
+}
+
+bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
+             KernelTimer *t) {
+    if (dim % 4 || dim > 2048 || rows <= 0) {
+        set_error("rmsnorm: unsupported dim %d", dim);
+        return false;
+    }
+    Scope sc(t, s, "rmsnorm");
+    const unsigned grid = blocks_for(rows, 4);
+    const int nv = dim / 4;
+    if (nv <= 64) hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    else if (nv <= 128) hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    else if (nv <= 256) hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    else hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    return sync_debug(s, "rmsnorm_kernel");
+}
+
+bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int len, KernelTimer *t) {
+    if (len <= 0 || len > 64 * 32) {
+        set_error("softmax_rows: unsupported length %d", len);
+        return false;
+    }
+    Scope sc(t, s, "softmax");
+    const unsigned grid = blocks_for(rows, 4);
+    const int per = (len + 63) / 64;
+    if (per <= 2) hipLaunchKernelGGL(softmax_rows_kernel<2>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else if (per <= 4) hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else if (per <= 8) hipLaunchKernelGGL(softmax_rows_kernel<8>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else if (per <= 13) hipLaunchKernelGGL(softmax_rows_kernel<13>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else if (per <= 16) hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else hipLaunchKernelGGL(softmax_rows_kernel<32>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    return sync_debug(s, "softmax_rows_kernel");
+}
+
+bool rope_bhld(hipStream_t s, float *x, const float *cs, const float *sn, int64_t bh, int len, KernelTimer *t) {
+    const int64_t n4 = bh * len * 16;
+    Scope sc(t, s, "rope");
+    hipLaunchKernelGGL(rope_bhld_kernel, dim3(blocks_for(n4, 256)), dim3(256), 0, s, x, cs, sn, n4, len);
+    return sync_debug(s, "rope_bhld_kernel");
+}
+
+bool geglu(hipStream_t s, const float *in, float *out, int64_t rows, int width, KernelTimer *t) {
+    if (width % 4) {
+        set_error("geglu: width %% 4 != 0");
+        return false;
+    }
+    Scope sc(t, s, "geglu");
+    hipLaunchKernelGGL(geglu_kernel, dim3(blocks_for(rows * (width / 4), 256)), dim3(256), 0, s, in, out, rows, width);
+    return sync_debug(s, "geglu_kernel");
+}
+
+bool residual_add(hipStream_t s, float *x, const float *r, int64_t n, KernelTimer *t) {
+    if (n % 4) {
+        set_error("residual_add: n %% 4 != 0");
+        return false;
+    }
+    Scope sc(t, s, "residual");
+    hipLaunchKernelGGL(residual_add_kernel, dim3(blocks_for(n / 4, 256)), dim3(256), 0, s, x, r, n / 4);
+    return sync_debug(s, "residual_add_kernel");
+}
+
+bool unpack_weight(hipStream_t s, const float *packed_dev, int in, int out, float *dst, int ldd, int row0, int mode) {
+    hipLaunchKernelGGL(unpack_weight_kernel, dim3(blocks_for((int64_t)in * out, 256)), dim3(256), 0, s, packed_dev, in,
+                       out, dst, ldd, row0, mode);
+    return sync_debug(s, "unpack_weight_kernel");
+}
+
+bool interleave_glu_bias(hipStream_t s, const float *src, float *dst, int out) {
+    hipLaunchKernelGGL(interleave_glu_bias_kernel, dim3(blocks_for(out, 256)), dim3(256), 0, s, src, dst, out);
+    return sync_debug(s, "interleave_glu_bias_kernel");
+}
+
+bool transpose_rows(hipStream_t s, const float *src, float *dst, int outer, int a, int b, int dim) {
+    if (dim % 4) {
+        set_error("transpose_rows: dim %% 4 != 0");
+        return false;
+    }
+    const int64_t n = (int64_t)outer * a * b * (dim / 4);
+    hipLaunchKernelGGL(transpose_rows_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, src, dst, outer, a, b, dim / 4);
+    return sync_debug(s, "transpose_rows_kernel");
+}
+
+bool attention(hipStream_t s, const float *qkv, int ld, float *out, int ld_out, const float *rope_cos,
+               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t) {
+    if (lay.S <= 0 || lay.L <= 0 || ld % 4 || ld_out % 4) {
+        set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
+        return false;
+    }
+    AttnArgs a;
+    a.qkv = qkv; a.ld = ld; a.out = out; a.ld_out = ld_out;
+    a.rope_cos = rope_cos; a.rope_sin = rope_sin;
+    a.S = lay.S; a.L = lay.L; a.H = heads;
+    a.group = lay.group; a.group_stride = lay.group_stride; a.seq_stride = lay.seq_stride; a.pos_stride = lay.pos_stride;
+    a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
+    Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
+    if (lay.L <= 64) {
+        const int64_t grid = (int64_t)lay.S * heads * ((lay.L + 63) / 64);
+        hipLaunchKernelGGL(attention_kernel<2>, dim3((unsigned)grid), dim3(128), 0, s, a);
+    } else {
+        const int64_t grid = (int64_t)lay.S * heads * ((lay.L + 127) / 128);
+        hipLaunchKernelGGL(attention_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, a);
+    }
+    return sync_debug(s, "attention_kernel");
+}
+
+// ------------------------------------------------------------------- dims
+Dims dims_from(const vh_dims &d) {
+    Dims o;
+    o.dim = d.dim; o.depth = d.depth; o.bands = d.bands; o.heads = d.heads; o.dim_head = d.dim_head;
+    o.ff_dim = d.ff_dim; o.ffn_glu = d.ffn_glu; o.gated = d.gated; o.mask_hidden = d.mask_hidden;
+    o.n_fft = d.n_fft; o.hop = d.hop; o.channels = d.channels;
+    for (int i = 0; i < VH_MAX_BANDS; i++) o.band_widths[i] = i < d.bands ? d.band_widths[i] : 0;
+    return o;
+}
+
+bool Dims::valid(char *why, size_t n) const {
+    if (dim_head != 64) { snprintf(why, n, "dim_head must be 64 (got %d)", dim_head); return false; }
+    if (dim <= 0 || dim % 4 || dim > 2048) { snprintf(why, n, "dim must be a multiple of 4 up to 2048"); return false; }
+    if (heads <= 0 || bands <= 0 || bands > VH_MAX_BANDS || depth < 0) { snprintf(why, n, "bad heads/bands/depth"); return false; }
+    if (ffn_glu && (ff_dim % 32)) { snprintf(why, n, "GELU-GLU needs ff_dim %% 32 == 0"); return false; }
+    if (ff_dim % 4 || mask_hidden % 4 || mask_hidden <= 0) { snprintf(why, n, "ff_dim/mask_hidden must be multiples of 4"); return false; }
+    if (n_fft <= 0 || (n_fft & (n_fft - 1)) || n_fft > 4096 || hop <= 0) { snprintf(why, n, "n_fft must be a power of two <= 4096"); return false; }
+    if (channels <= 0 || channels > 8) { snprintf(why, n, "bad channel count"); return false; }
+    int sum = 0;
+    for (int b = 0; b < bands; b++) {
+        if (band_widths[b] <= 0 || band_widths[b] * channels > 320) { snprintf(why, n, "band %d too wide", b); return false; }
+        sum += band_widths[b];
+    }
+    if (sum != freq_bins()) { snprintf(why, n, "band widths sum to %d, expected %d", sum, freq_bins()); return false; }
+    return true;
+}
+
+// ------------------------------------------------------------------ rotary
+bool RopeCache::get(int length, int dim_head, hipStream_t s, const float **cs, const float **sn) {
+    auto it = tables.find(length);
+    if (it == tables.end()) {
+        const int pairs = dim_head / 2;
+        std::vector<float> freq(pairs), hc((size_t)length * pairs), hs((size_t)length * pairs);
+        for (int i = 0; i < pairs; i++) freq[i] = 1.0f / powf(10000.0f, (float)(2 * i) / (float)dim_head);
+        for (int p = 0; p < length; p++)
+            for (int k = 0; k < pairs; k++) {
+                float angle = (float)p * freq[k];
+                hc[(size_t)p * pairs + k] = cosf(angle);
+                hs[(size_t)p * pairs + k] = sinf(angle);
+            }
+        float *dc = nullptr, *ds = nullptr;
+        size_t bytes = hc.size() * sizeof(float);
+        if (!check(hipMalloc((void **)&dc, bytes), "hipMalloc(rope cos)")) return false;
+        if (!check(hipMalloc((void **)&ds, bytes), "hipMalloc(rope sin)")) { (void)hipFree(dc); return false; }
+        if (!check(hipMemcpyAsync(dc, hc.data(), bytes, hipMemcpyHostToDevice, s), "hipMemcpy(rope cos)") ||
+            !check(hipMemcpyAsync(ds, hs.data(), bytes, hipMemcpyHostToDevice, s), "hipMemcpy(rope sin)") ||
+            !check(hipStreamSynchronize(s), "hipStreamSynchronize(rope)")) {
+            (void)hipFree(dc); (void)hipFree(ds);
+            return false;
+        }
+        it = tables.emplace(length, std::make_pair(dc, ds)).first;
+    }
+    *cs = it->second.first;
+    *sn = it->second.second;
+    return true;
+}
+
+void RopeCache::release() {
+    for (auto &kv : tables) {
+        (void)hipFree(kv.second.first);
+        (void)hipFree(kv.second.second);
+    }
+    tables.clear();
+}
+
+// --------------------------------------------------------------- block
+bool BlockScratch::ensure(const Dims &d, int64_t tokens) {
+    const size_t t = (size_t)tokens;
+    return normed.ensure(t * d.dim * sizeof(float), "hipMalloc(normed)") &&
+           qkvg.ensure(t * d.qkvg_dim() * sizeof(float), "hipMalloc(qkv)") &&
+           attn.ensure(t * d.inner() * sizeof(float), "hipMalloc(attention)") &&
+           hidden.ensure(t * d.ff_dim * sizeof(float), "hipMalloc(ffn hidden)");
+}
+
+bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, float *x, int64_t tokens,
+                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t) {
+    if (!scr.ensure(d, tokens)) return false;
+    const float *cs = nullptr, *sn = nullptr;
+    if (!rope.get(lay.L, d.dim_head, s, &cs, &sn)) return false;
+    const int D = d.dim, inner = d.inner(), nq = d.qkvg_dim();
+    float *normed = scr.normed.f(), *qkvg = scr.qkvg.f(), *attn = scr.attn.f(), *hid = scr.hidden.f();
+    // pre-norm -> fused QKV (+gate logits with their bias)
+    if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
+    if (!gemm(s, {normed, D, w.wqkvg, D, w.bqkvg, qkvg, nq, tokens, nq, D}, EPI_STORE, t, "gemm_qkv")) return false;
+    // rotary + attention + gates
+    if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, d.gated ? d.qkv_dim() : -1, t)) return false;
+    // out projection added to the residual stream
+    if (!gemm(s, {attn, inner, w.wout, inner, nullptr, x, D, tokens, D, inner}, EPI_RESIDUAL, t, "gemm_out")) return false;
+    // FFN
+    if (!rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
+    if (!gemm(s, {normed, D, w.w1, D, w.b1, hid, d.ff_dim, tokens, d.ff1_out(), D}, d.ffn_glu ? EPI_GEGLU : EPI_GELU, t,
+              "gemm_ff1"))
+        return false;
+    if (!gemm(s, {hid, d.ff_dim, w.w2, d.ff_dim, w.b2, x, D, tokens, D, d.ff_dim}, EPI_RESIDUAL, t, "gemm_ff2"))
+        return false;
+    return true;
+}
+
+// ---------------------------------------------------------------- upload
+bool upload_weight(hipStream_t s, const float *host_packed, int in, int out, float *dst, int ldd, int row0, int mode,
+                   DeviceBuffer &staging) {
+    const size_t bytes = (size_t)in * out * sizeof(float);
+    if (!staging.ensure(bytes, "hipMalloc(weight staging)")) return false;
+    if (!check(hipMemcpyAsync(staging.ptr, host_packed, bytes, hipMemcpyHostToDevice, s), "hipMemcpy(weight)"))
+        return false;
+    if (!unpack_weight(s, staging.f(), in, out, dst, ldd, row0, mode)) return false;
+    // The staging buffer is reused by the next upload: wait for the unpack.
+    return check(hipStreamSynchronize(s), "hipStreamSynchronize(weight)");
+}
+
+bool upload_vector(hipStream_t s, const float *host, size_t count, float *dst) {
+    if (!check(hipMemcpyAsync(dst, host, count * sizeof(float), hipMemcpyHostToDevice, s), "hipMemcpy(vector)"))
+        return false;
+    return check(hipStreamSynchronize(s), "hipStreamSynchronize(vector)");
+}
+
+}  // namespace vh

@@ -1,0 +1,161 @@
+// Host-side runtime of the VocalArc HIP provider: device buffers, the
+// per-shape launchers of the gfx950 kernels, weight upload and the
+// device-resident transformer block shared by the native_gpu.h provider and
+// the vocalarc_hip.h harness API.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/vocalarc_hip.h"
+
+namespace vh {
+
+// ----------------------------------------------------------------- errors
+// Every HIP call goes through check(); the first failure is remembered (for
+// vh_last_error) and printed once with the operation name.
+bool check(hipError_t e, const char *what);
+void set_error(const char *fmt, ...);
+const char *last_error();
+bool debug_enabled();
+bool sync_debug(hipStream_t s, const char *what);
+
+// ---------------------------------------------------------------- buffers
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    bool ensure(size_t need, const char *what);
+    void release();
+    float *f() const { return static_cast<float *>(ptr); }
+    ~DeviceBuffer() { release(); }
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer &) = delete;
+    DeviceBuffer &operator=(const DeviceBuffer &) = delete;
+};
+
+// --------------------------------------------------------------- kernel timing
+// Optional per-kernel-class timing with HIP events recorded on the launch
+// stream around each launch of a named class (e.g. "gemm_ff1").
+struct KernelTimer {
+    bool enabled = false;
+    struct Pending { std::string name; hipEvent_t a, b; };
+    std::vector<Pending> pending;
+    std::map<std::string, std::pair<double, int64_t>> totals;  // ms, count
+    void begin(hipStream_t s, const char *name, hipEvent_t *a);
+    void end(hipStream_t s, const char *name, hipEvent_t a);
+    void collect();  // after a stream sync
+    void reset();
+};
+
+struct Scope {
+    KernelTimer *t;
+    hipStream_t s;
+    const char *name;
+    hipEvent_t a = nullptr;
+    Scope(KernelTimer *t_, hipStream_t s_, const char *n) : t(t_), s(s_), name(n) {
+        if (t && t->enabled) t->begin(s, name, &a);
+    }
+    ~Scope() {
+        if (t && t->enabled) t->end(s, name, a);
+    }
+};
+
+// --------------------------------------------------------------- launchers
+// GEMM epilogues (what the store does with acc + bias).
+enum Epilogue : int {
+    EPI_STORE = 0,     // C = acc + bias
+    EPI_GELU = 1,      // C = gelu(acc + bias)
+    EPI_TANH = 2,      // C = tanh(acc + bias)
+    EPI_RESIDUAL = 3,  // C += acc + bias
+    EPI_GEGLU = 4,     // columns come in (32 value, 32 gate) pairs: C[:, n/2] = v * gelu(g)
+};
+
+struct GemmArgs {
+    const float *A; int lda;
+    const float *B; int ldb;  // [N][K] rows
+    const float *bias;
+    float *C; int ldc;
+    int64_t M; int N, K;
+};
+bool gemm(hipStream_t s, const GemmArgs &g, int epilogue, KernelTimer *t = nullptr, const char *name = "gemm");
+// Batched/ragged: one descriptor per problem, launched together.
+bool gemm_batched(hipStream_t s, const std::vector<GemmArgs> &g, int epilogue, KernelTimer *t = nullptr,
+                  const char *name = "gemm_batched");
+
+bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
+             KernelTimer *t = nullptr);
+bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int len, KernelTimer *t = nullptr);
+bool rope_bhld(hipStream_t s, float *x, const float *cs, const float *sn, int64_t bh, int len,
+               KernelTimer *t = nullptr);
+bool geglu(hipStream_t s, const float *in, float *out, int64_t rows, int width, KernelTimer *t = nullptr);
+bool residual_add(hipStream_t s, float *x, const float *r, int64_t n, KernelTimer *t = nullptr);
+bool unpack_weight(hipStream_t s, const float *packed_dev, int in, int out, float *dst, int ldd, int row0,
+                   int mode);
+bool interleave_glu_bias(hipStream_t s, const float *src, float *dst, int out);
+bool transpose_rows(hipStream_t s, const float *src, float *dst, int outer, int a, int b, int dim);
+
+struct AttnLayout {
+    int S, L;
+    int group, group_stride, seq_stride, pos_stride;
+};
+bool attention(hipStream_t s, const float *qkv, int ld, float *out, int ld_out, const float *rope_cos,
+               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t = nullptr);
+
+// ------------------------------------------------------------------- dims
+struct Dims {
+    int dim, depth, bands, heads, dim_head, ff_dim, ffn_glu, gated, mask_hidden, n_fft, hop, channels;
+    int band_widths[VH_MAX_BANDS];
+    int freq_bins() const { return n_fft / 2 + 1; }
+    int inner() const { return heads * dim_head; }
+    int qkv_dim() const { return 3 * inner(); }
+    int ff1_out() const { return ffn_glu ? 2 * ff_dim : ff_dim; }
+    // fused QKV + gate projection width (gates padded to a 32-column tile)
+    int qkvg_dim() const { return qkv_dim() + (gated ? 32 : 0); }
+    int in_dim(int b) const { return band_widths[b] * channels * 2; }
+    int frames(int length) const { return length / hop + 1; }
+    bool valid(char *why, size_t n) const;
+};
+Dims dims_from(const vh_dims &d);
+
+// ------------------------------------------------------- device weights
+struct LayerWeights {
+    float *gamma = nullptr, *ff_gamma = nullptr;
+    float *wqkvg = nullptr, *bqkvg = nullptr;  // [qkvg_dim][D], bias (0 on q/k/v columns)
+    float *wout = nullptr;                     // [D][inner]
+    float *w1 = nullptr, *b1 = nullptr;        // [ff1_out][D] (value/gate interleaved for GLU)
+    float *w2 = nullptr, *b2 = nullptr;        // [D][ff_dim]
+};
+
+// Rotary cos/sin tables per sequence length, built on the host with the
+// reference's float expressions (native/vocalarc_separation.c:726-731,1312).
+struct RopeCache {
+    std::map<int, std::pair<float *, float *>> tables;
+    bool get(int length, int dim_head, hipStream_t s, const float **cs, const float **sn);
+    void release();
+    ~RopeCache() { release(); }
+};
+
+// Scratch for one transformer pass over `tokens` tokens.
+struct BlockScratch {
+    DeviceBuffer normed, qkvg, attn, hidden;
+    bool ensure(const Dims &d, int64_t tokens);
+};
+
+// One axial transformer block on device-resident activations x
+// (native/vocalarc_separation.c:836-873).  Rows of x are tokens; `lay` maps
+// (sequence, position) to rows.
+bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, float *x, int64_t tokens,
+                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t = nullptr);
+
+// Host packed weight (reference layout) -> device [out][in] rows, through a
+// staging buffer.  mode as unpack_weight.
+bool upload_weight(hipStream_t s, const float *host_packed, int in, int out, float *dst, int ldd, int row0, int mode,
+                   DeviceBuffer &staging);
+bool upload_vector(hipStream_t s, const float *host, size_t count, float *dst);
+
+}  // namespace vh

@@ -1,0 +1,587 @@
+// vocalarc_hip.h: the shape-generic device path (isolated kernels, model
+// upload, STFT -> band split -> axial stack -> mask -> iSTFT, chunked
+// separation).
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "dsp.hpp"
+#include "elementwise.hpp"
+#include "runtime.hpp"
+
+using namespace vh;
+
+// Physical activation layout of the device pipeline: [chunk][T][B][D] (one
+// row per (frame, band) token).  The time axis reads it with pos_stride B, the
+// band axis with pos_stride 1, so neither axis needs a transpose.
+static AttnLayout time_axis_layout(int chunks, int T, int B) {
+    return {chunks * B, T, B, T * B, 1, B};
+}
+static AttnLayout band_axis_layout(int chunks, int T, int B) {
+    return {chunks * T, B, 1, B, 0, 1};
+}
+static AttnLayout contiguous_layout(int S, int L) { return {S, L, 1, L, 0, 1}; }
+
+struct vh_context {
+    hipStream_t stream = nullptr;
+    int device = 0;
+    char name[256] = "";
+    KernelTimer timer;
+    RopeCache rope;
+    BlockScratch scratch;
+    DeviceBuffer staging;
+};
+
+struct vh_model {
+    vh_context *ctx = nullptr;
+    Dims d;
+    DeviceBuffer weights;
+    std::vector<LayerWeights> layers;  // [depth][2]
+    std::vector<float *> band_gamma, band_w, band_b;
+    float *final_gamma = nullptr;
+    std::vector<float *> mask_w1, mask_b1, mask_w2, mask_b2;
+    std::vector<int> first_freq;
+    // DSP constants
+    DeviceBuffer window, twiddle;
+    // pipeline scratch (grown on demand)
+    DeviceBuffer source, x, normed, mask, bandin, mhidden, proj, frames, chunk_out, starts, tables;
+    int64_t band_in_total = 0;   // sum over bands of 4w (floats per spectrogram row)
+    int64_t proj_total = 0;      // sum over bands of 8w
+};
+
+// ------------------------------------------------------------------ context
+extern "C" vh_context *vh_create(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        set_error("no HIP device");
+        return nullptr;
+    }
+    vh_context *ctx = new vh_context();
+    if (!check(hipSetDevice(0), "hipSetDevice")) {
+        delete ctx;
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) == hipSuccess) snprintf(ctx->name, sizeof(ctx->name), "%s (%s)", prop.name, prop.gcnArchName);
+    return ctx;
+}
+
+extern "C" void vh_destroy(vh_context *ctx) {
+    if (!ctx) return;
+    (void)hipStreamSynchronize(ctx->stream);
+    ctx->timer.reset();
+    delete ctx;
+}
+
+extern "C" int vh_set_stream(vh_context *ctx, void *s) {
+    if (!ctx) return 0;
+    ctx->stream = (hipStream_t)s;
+    return 1;
+}
+
+extern "C" int vh_synchronize(vh_context *ctx) {
+    if (!ctx) return 0;
+    bool ok = check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    ctx->timer.collect();
+    return ok ? 1 : 0;
+}
+
+extern "C" const char *vh_last_error(void) { return last_error(); }
+extern "C" const char *vh_device_name(vh_context *ctx) { return ctx ? ctx->name : ""; }
+
+// --------------------------------------------------------- isolated kernels
+extern "C" int vh_rmsnorm(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, float *y) {
+    if (!ctx) return 0;
+    return rmsnorm(ctx->stream, x, dim, gamma, y, dim, rows, dim, &ctx->timer) ? 1 : 0;
+}
+
+extern "C" int vh_softmax_rows(vh_context *ctx, int64_t rows, int len, const float *in, float *out) {
+    if (!ctx) return 0;
+    return softmax_rows(ctx->stream, in, out, rows, len, &ctx->timer) ? 1 : 0;
+}
+
+extern "C" int vh_rope_bhld(vh_context *ctx, int64_t bh, int len, int dim_head, float *x) {
+    if (!ctx || dim_head != 64) {
+        set_error("vh_rope_bhld: dim_head must be 64");
+        return 0;
+    }
+    const float *cs, *sn;
+    if (!ctx->rope.get(len, dim_head, ctx->stream, &cs, &sn)) return 0;
+    return rope_bhld(ctx->stream, x, cs, sn, bh, len, &ctx->timer) ? 1 : 0;
+}
+
+extern "C" int vh_geglu(vh_context *ctx, int64_t rows, int width, const float *in, float *out) {
+    if (!ctx) return 0;
+    return geglu(ctx->stream, in, out, rows, width, &ctx->timer) ? 1 : 0;
+}
+
+extern "C" int vh_residual_add(vh_context *ctx, int64_t n, float *x, const float *r) {
+    if (!ctx) return 0;
+    return residual_add(ctx->stream, x, r, n, &ctx->timer) ? 1 : 0;
+}
+
+extern "C" int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const float *W, int ldw,
+                       const float *bias, float *C, int ldc, int epilogue) {
+    if (!ctx) return 0;
+    return gemm(ctx->stream, {A, lda, W, ldw, bias, C, ldc, M, N, K}, epilogue, &ctx->timer, "gemm") ? 1 : 0;
+}
+
+extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, float *out,
+                            int apply_rotary) {
+    if (!ctx) return 0;
+    const float *cs = nullptr, *sn = nullptr;
+    if (apply_rotary && !ctx->rope.get(length, 64, ctx->stream, &cs, &sn)) return 0;
+    const int inner = heads * 64;
+    return attention(ctx->stream, qkv, 3 * inner, out, inner, cs, sn, contiguous_layout(sequences, length), heads, -1,
+                     &ctx->timer)
+               ? 1
+               : 0;
+}
+
+// -------------------------------------------------------------------- model
+namespace {
+
+struct PackReader {
+    const unsigned char *cur, *end;
+    const float *next(uint64_t expect) {
+        if ((size_t)(end - cur) < 8) return nullptr;
+        uint64_t n;
+        memcpy(&n, cur, 8);
+        cur += 8;
+        if (n != expect || (size_t)(end - cur) < n * sizeof(float)) return nullptr;
+        const float *r = reinterpret_cast<const float *>(cur);
+        cur += n * sizeof(float);
+        return r;
+    }
+};
+
+// Bump allocator over the model's single weight allocation (256-byte aligned).
+struct Arena {
+    size_t used = 0;
+    char *base = nullptr;
+    float *take(size_t floats) {
+        float *p = reinterpret_cast<float *>(base + used);
+        used += (floats * sizeof(float) + 255) & ~(size_t)255;
+        return p;
+    }
+};
+
+size_t model_weight_bytes(const Dims &d) {
+    auto r = [](size_t floats) { return (floats * sizeof(float) + 255) & ~(size_t)255; };
+    size_t b = 0;
+    const size_t D = d.dim;
+    for (int l = 0; l < d.depth * 2; l++) {
+        b += 2 * r(D);
+        b += r((size_t)d.qkvg_dim() * D) + r(d.qkvg_dim());
+        b += r(D * d.inner());
+        b += r((size_t)d.ff1_out() * D) + r(d.ff1_out());
+        b += r(D * d.ff_dim) + r(D);
+    }
+    for (int k = 0; k < d.bands; k++) b += r(d.in_dim(k)) + r(D * d.in_dim(k)) + r(D);
+    b += r(D);
+    for (int k = 0; k < d.bands; k++)
+        b += r((size_t)d.mask_hidden * D) + r(d.mask_hidden) + r((size_t)2 * d.in_dim(k) * d.mask_hidden) +
+             r(2 * d.in_dim(k));
+    return b;
+}
+
+bool upload_pack(vh_model *m, const void *pack, size_t bytes) {
+    const Dims &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    if (bytes < 64 || memcmp(pack, "VSCNAT01", 8) != 0) {
+        set_error("pack: bad magic");
+        return false;
+    }
+    uint32_t f[14];
+    memcpy(f, (const char *)pack + 8, sizeof(f));
+    if (f[0] != 1 || f[1] != (uint32_t)d.dim || f[2] != (uint32_t)d.depth || f[3] != (uint32_t)d.bands ||
+        f[4] != (uint32_t)d.heads || f[5] != (uint32_t)d.dim_head || f[6] != (uint32_t)d.freq_bins() ||
+        f[7] != (uint32_t)d.channels || f[8] != (uint32_t)d.n_fft || f[9] != (uint32_t)d.hop) {
+        set_error("pack: header does not match the model shape");
+        return false;
+    }
+    if (!m->weights.ensure(model_weight_bytes(d), "hipMalloc(model weights)")) return false;
+    if (!check(hipMemsetAsync(m->weights.ptr, 0, m->weights.bytes, s), "hipMemset(model weights)")) return false;
+    Arena ar;
+    ar.base = static_cast<char *>(m->weights.ptr);
+    PackReader rd{(const unsigned char *)pack + 64, (const unsigned char *)pack + bytes};
+    const int D = d.dim, H = d.heads, inner = d.inner(), nq = d.qkvg_dim();
+    DeviceBuffer &stg = m->ctx->staging;
+    std::vector<float> zeros;
+    m->layers.resize((size_t)d.depth * 2);
+    for (int l = 0; l < d.depth * 2; l++) {
+        LayerWeights &w = m->layers[l];
+        w.gamma = ar.take(D);
+        w.wqkvg = ar.take((size_t)nq * D);
+        w.bqkvg = ar.take(nq);
+        w.wout = ar.take((size_t)D * inner);
+        w.ff_gamma = ar.take(D);
+        w.w1 = ar.take((size_t)d.ff1_out() * D);
+        w.b1 = ar.take(d.ff1_out());
+        w.w2 = ar.take((size_t)D * d.ff_dim);
+        w.b2 = ar.take(D);
+        const float *gamma = rd.next(D), *qkv = rd.next((uint64_t)3 * inner * D), *gw = rd.next((uint64_t)H * D),
+                    *gb = rd.next(H), *wo = rd.next((uint64_t)D * inner), *fg = rd.next(D),
+                    *w1 = rd.next((uint64_t)d.ff1_out() * D), *b1 = rd.next(d.ff1_out()),
+                    *w2 = rd.next((uint64_t)D * d.ff_dim), *b2 = rd.next(D);
+        if (!gamma || !qkv || !gw || !gb || !wo || !fg || !w1 || !b1 || !w2 || !b2) {
+            set_error("pack: truncated or mis-sized transformer tensor (layer %d axis %d)", l / 2, l % 2);
+            return false;
+        }
+        if (!upload_vector(s, gamma, D, w.gamma) || !upload_vector(s, fg, D, w.ff_gamma)) return false;
+        if (!upload_weight(s, qkv, D, 3 * inner, w.wqkvg, D, 0, 0, stg)) return false;
+        if (d.gated) {
+            if (!upload_weight(s, gw, D, H, w.wqkvg, D, 3 * inner, 0, stg)) return false;
+            if (!upload_vector(s, gb, H, w.bqkvg + 3 * inner)) return false;
+        }
+        if (!upload_weight(s, wo, inner, D, w.wout, inner, 0, 0, stg)) return false;
+        if (!upload_weight(s, w1, D, d.ff1_out(), w.w1, D, 0, d.ffn_glu ? 1 : 0, stg)) return false;
+        if (d.ffn_glu) {
+            if (!stg.ensure((size_t)d.ff1_out() * sizeof(float), "hipMalloc(staging)")) return false;
+            if (!upload_vector(s, b1, d.ff1_out(), stg.f())) return false;
+            if (!interleave_glu_bias(s, stg.f(), w.b1, d.ff1_out())) return false;
+            if (!check(hipStreamSynchronize(s), "sync")) return false;
+        } else if (!upload_vector(s, b1, d.ff1_out(), w.b1)) {
+            return false;
+        }
+        if (!upload_weight(s, w2, d.ff_dim, D, w.w2, d.ff_dim, 0, 0, stg)) return false;
+        if (!upload_vector(s, b2, D, w.b2)) return false;
+    }
+    for (int k = 0; k < d.bands; k++) {
+        const int in = d.in_dim(k);
+        const float *g = rd.next(in), *w = rd.next((uint64_t)D * in), *b = rd.next(D);
+        if (!g || !w || !b) {
+            set_error("pack: truncated band-split tensor (band %d)", k);
+            return false;
+        }
+        m->band_gamma.push_back(ar.take(in));
+        m->band_w.push_back(ar.take((size_t)D * in));
+        m->band_b.push_back(ar.take(D));
+        if (!upload_vector(s, g, in, m->band_gamma.back()) || !upload_weight(s, w, in, D, m->band_w.back(), in, 0, 0, stg) ||
+            !upload_vector(s, b, D, m->band_b.back()))
+            return false;
+    }
+    const float *fg = rd.next(D);
+    if (!fg) {
+        set_error("pack: missing final gamma");
+        return false;
+    }
+    m->final_gamma = ar.take(D);
+    if (!upload_vector(s, fg, D, m->final_gamma)) return false;
+    for (int k = 0; k < d.bands; k++) {
+        const int in = d.in_dim(k), Hm = d.mask_hidden;
+        const float *w1 = rd.next((uint64_t)Hm * D), *b1 = rd.next(Hm), *w2 = rd.next((uint64_t)2 * in * Hm),
+                    *b2 = rd.next((uint64_t)2 * in);
+        if (!w1 || !b1 || !w2 || !b2) {
+            set_error("pack: truncated mask tensor (band %d)", k);
+            return false;
+        }
+        m->mask_w1.push_back(ar.take((size_t)Hm * D));
+        m->mask_b1.push_back(ar.take(Hm));
+        m->mask_w2.push_back(ar.take((size_t)2 * in * Hm));
+        m->mask_b2.push_back(ar.take(2 * in));
+        if (!upload_weight(s, w1, D, Hm, m->mask_w1.back(), D, 0, 0, stg) || !upload_vector(s, b1, Hm, m->mask_b1.back()) ||
+            !upload_weight(s, w2, Hm, 2 * in, m->mask_w2.back(), Hm, 0, 0, stg) ||
+            !upload_vector(s, b2, 2 * in, m->mask_b2.back()))
+            return false;
+    }
+    if (rd.cur != rd.end) {
+        set_error("pack: %zu trailing bytes", (size_t)(rd.end - rd.cur));
+        return false;
+    }
+    // DSP constants: the reference's float window expression and an exact
+    // double twiddle table.
+    const int N = d.n_fft;
+    std::vector<float> win(N);
+    for (int i = 0; i < N; i++) win[i] = 0.5f - 0.5f * cosf((float)(2.0 * 3.141592653589793238462643383279502884 * i / N));
+    std::vector<double2_t> tw(N / 2);
+    for (int j = 0; j < N / 2; j++) {
+        const double a = -2.0 * 3.141592653589793238462643383279502884 * j / N;
+        tw[j] = {cos(a), sin(a)};
+    }
+    if (!m->window.ensure(N * sizeof(float), "hipMalloc(window)") ||
+        !m->twiddle.ensure(tw.size() * sizeof(double2_t), "hipMalloc(twiddles)"))
+        return false;
+    if (!check(hipMemcpyAsync(m->window.ptr, win.data(), N * sizeof(float), hipMemcpyHostToDevice, s), "hipMemcpy(window)") ||
+        !check(hipMemcpyAsync(m->twiddle.ptr, tw.data(), tw.size() * sizeof(double2_t), hipMemcpyHostToDevice, s),
+               "hipMemcpy(twiddles)"))
+        return false;
+    int f0 = 0;
+    for (int k = 0; k < d.bands; k++) {
+        m->first_freq.push_back(f0);
+        f0 += d.band_widths[k];
+        m->band_in_total += d.in_dim(k);
+        m->proj_total += 2 * d.in_dim(k);
+    }
+    return check(hipStreamSynchronize(s), "hipStreamSynchronize(model upload)");
+}
+
+// ---- pipeline stages on `chunks` windows at once --------------------------
+
+int log2i(int n) {
+    int l = 0;
+    while ((1 << l) < n) l++;
+    return l;
+}
+
+bool stage_stft(vh_model *m, const float *audio, int64_t audio_len, const int64_t *starts_dev, int sig_len, int chunks,
+                int T, float *source) {
+    const Dims &d = m->d;
+    StftArgs a;
+    a.audio = audio; a.audio_len = audio_len; a.starts = starts_dev; a.sig_len = sig_len;
+    a.C = d.channels; a.T = T; a.F = d.freq_bins(); a.n_fft = d.n_fft; a.log2n = log2i(d.n_fft); a.hop = d.hop;
+    a.window = m->window.f(); a.tw = static_cast<const double2_t *>(m->twiddle.ptr); a.source = source;
+    Scope sc(&m->ctx->timer, m->ctx->stream, "stft");
+    hipLaunchKernelGGL(stft_kernel, dim3(T, chunks * d.channels), dim3(256), d.n_fft * sizeof(double2_t), m->ctx->stream, a);
+    return sync_debug(m->ctx->stream, "stft_kernel");
+}
+
+// source[chunks][F][C][T][2] -> rows of out: band-major (time_sequences,
+// row b*M + m) or frame-major (row m*B + b).
+bool stage_band_split(vh_model *m, const float *source, int chunks, int T, float *out, bool frame_major) {
+    const Dims &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int M = chunks * T, B = d.bands, D = d.dim;
+    if (!m->bandin.ensure((size_t)M * m->band_in_total * sizeof(float), "hipMalloc(band input)") ||
+        !m->tables.ensure(sizeof(BandTable) + sizeof(MaskTable), "hipMalloc(tables)"))
+        return false;
+    BandTable tab;
+    memset(&tab, 0, sizeof(tab));
+    int64_t off = 0;
+    std::vector<GemmArgs> gs;
+    for (int b = 0; b < B; b++) {
+        tab.first_freq[b] = m->first_freq[b];
+        tab.width[b] = d.band_widths[b];
+        tab.in_offset[b] = off;
+        tab.gamma[b] = m->band_gamma[b];
+        const int in = d.in_dim(b);
+        float *C = frame_major ? out + (size_t)b * D : out + (size_t)b * M * D;
+        gs.push_back({m->bandin.f() + off, in, m->band_w[b], in, m->band_b[b], C, frame_major ? B * D : D, M, D, in});
+        off += (int64_t)M * in;
+    }
+    if (!check(hipMemcpyAsync(m->tables.ptr, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(band table)"))
+        return false;
+    {
+        Scope sc(&m->ctx->timer, s, "band_gather");
+        hipLaunchKernelGGL(band_gather_norm_kernel, dim3((M + 3) / 4, B), dim3(256), 0, s, source,
+                           (const BandTable *)m->tables.ptr, m->bandin.f(), M, T, d.freq_bins(), d.channels);
+        if (!sync_debug(s, "band_gather_norm_kernel")) return false;
+    }
+    // The table must stay intact until the gather has read it.
+    if (!check(hipStreamSynchronize(s), "hipStreamSynchronize(band table)")) return false;
+    return gemm_batched(s, gs, EPI_STORE, &m->ctx->timer, "gemm_band_split");
+}
+
+// final-normed features (frame-major rows m*B + b) -> mask[chunks][F][C][T][2]
+bool stage_mask(vh_model *m, const float *normed, int chunks, int T, float *mask) {
+    const Dims &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int M = chunks * T, B = d.bands, D = d.dim, Hm = d.mask_hidden;
+    if (!m->mhidden.ensure((size_t)B * M * Hm * sizeof(float), "hipMalloc(mask hidden)") ||
+        !m->proj.ensure((size_t)M * m->proj_total * sizeof(float), "hipMalloc(mask projection)") ||
+        !m->tables.ensure(sizeof(BandTable) + sizeof(MaskTable), "hipMalloc(tables)"))
+        return false;
+    std::vector<GemmArgs> g1, g2;
+    MaskTable tab;
+    memset(&tab, 0, sizeof(tab));
+    int64_t off = 0;
+    for (int b = 0; b < B; b++) {
+        float *hid = m->mhidden.f() + (size_t)b * M * Hm;
+        g1.push_back({normed + (size_t)b * D, B * D, m->mask_w1[b], D, m->mask_b1[b], hid, Hm, M, Hm, D});
+        const int out = 2 * d.in_dim(b);
+        g2.push_back({hid, Hm, m->mask_w2[b], Hm, m->mask_b2[b], m->proj.f() + off, out, M, out, Hm});
+        tab.first_freq[b] = m->first_freq[b];
+        tab.dim[b] = d.in_dim(b);
+        tab.proj_offset[b] = off;
+        off += (int64_t)M * out;
+    }
+    if (!gemm_batched(s, g1, EPI_TANH, &m->ctx->timer, "gemm_mask1")) return false;
+    if (!gemm_batched(s, g2, EPI_STORE, &m->ctx->timer, "gemm_mask2")) return false;
+    MaskTable *dtab = reinterpret_cast<MaskTable *>(static_cast<char *>(m->tables.ptr) + sizeof(BandTable));
+    if (!check(hipMemcpyAsync(dtab, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(mask table)")) return false;
+    int maxdim = 0;
+    for (int b = 0; b < B; b++) maxdim = std::max(maxdim, d.in_dim(b));
+    {
+        Scope sc(&m->ctx->timer, s, "mask_glu");
+        hipLaunchKernelGGL(mask_glu_scatter_kernel, dim3((unsigned)(((int64_t)M * maxdim + 255) / 256), B), dim3(256), 0, s,
+                           m->proj.f(), dtab, mask, M, T, d.freq_bins(), d.channels);
+        if (!sync_debug(s, "mask_glu_scatter_kernel")) return false;
+    }
+    return check(hipStreamSynchronize(s), "hipStreamSynchronize(mask table)");
+}
+
+// source, mask -> out[chunks*C][pitch] (first `length` samples of each)
+bool stage_istft(vh_model *m, const float *source, const float *mask, int chunks, int T, int length, float *out,
+                 int64_t pitch) {
+    const Dims &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int sigs = chunks * d.channels;
+    if (!m->frames.ensure((size_t)sigs * T * d.n_fft * sizeof(float), "hipMalloc(istft frames)")) return false;
+    IstftArgs a;
+    a.source = source; a.mask = mask; a.C = d.channels; a.T = T; a.F = d.freq_bins(); a.n_fft = d.n_fft;
+    a.log2n = log2i(d.n_fft); a.window = m->window.f(); a.tw = static_cast<const double2_t *>(m->twiddle.ptr);
+    a.frames = m->frames.f();
+    Scope sc(&m->ctx->timer, s, "istft");
+    hipLaunchKernelGGL(istft_frames_kernel, dim3(T, sigs), dim3(256), d.n_fft * sizeof(double2_t), s, a);
+    if (!sync_debug(s, "istft_frames_kernel")) return false;
+    OlaArgs o;
+    o.frames = m->frames.f(); o.window = m->window.f(); o.T = T; o.n_fft = d.n_fft; o.hop = d.hop; o.length = length;
+    o.out = out; o.out_pitch = pitch;
+    hipLaunchKernelGGL(ola_kernel, dim3((length + 255) / 256, sigs), dim3(256), 0, s, o);
+    return sync_debug(s, "ola_kernel");
+}
+
+bool stage_stack(vh_model *m, float *x, int chunks, int T) {
+    const Dims &d = m->d;
+    const int64_t tokens = (int64_t)chunks * T * d.bands;
+    vh_context *ctx = m->ctx;
+    for (int l = 0; l < d.depth; l++) {
+        if (!transformer_block(ctx->stream, d, m->layers[2 * l], x, tokens, time_axis_layout(chunks, T, d.bands),
+                               ctx->scratch, ctx->rope, &ctx->timer))
+            return false;
+        if (!transformer_block(ctx->stream, d, m->layers[2 * l + 1], x, tokens, band_axis_layout(chunks, T, d.bands),
+                               ctx->scratch, ctx->rope, &ctx->timer))
+            return false;
+    }
+    return true;
+}
+
+// Windows of `sig_len` samples (chunk k starts at starts[k]) -> separated
+// windows out[chunks*C][pitch].
+bool run_windows(vh_model *m, const float *audio, int64_t audio_len, const int64_t *starts_dev, int sig_len, int chunks,
+                 float *out, int64_t pitch) {
+    const Dims &d = m->d;
+    const int T = d.frames(sig_len);
+    const int64_t tokens = (int64_t)chunks * T * d.bands;
+    const size_t spec = (size_t)chunks * d.freq_bins() * d.channels * T * 2;
+    if (!m->source.ensure(spec * sizeof(float), "hipMalloc(source)") ||
+        !m->mask.ensure(spec * sizeof(float), "hipMalloc(mask)") ||
+        !m->x.ensure((size_t)tokens * d.dim * sizeof(float), "hipMalloc(features)") ||
+        !m->normed.ensure((size_t)tokens * d.dim * sizeof(float), "hipMalloc(normed features)"))
+        return false;
+    if (!stage_stft(m, audio, audio_len, starts_dev, sig_len, chunks, T, m->source.f())) return false;
+    if (!stage_band_split(m, m->source.f(), chunks, T, m->x.f(), true)) return false;
+    if (!stage_stack(m, m->x.f(), chunks, T)) return false;
+    if (!rmsnorm(m->ctx->stream, m->x.f(), d.dim, m->final_gamma, m->normed.f(), d.dim, tokens, d.dim, &m->ctx->timer))
+        return false;
+    if (!stage_mask(m, m->normed.f(), chunks, T, m->mask.f())) return false;
+    return stage_istft(m, m->source.f(), m->mask.f(), chunks, T, sig_len, out, pitch);
+}
+
+}  // namespace
+
+extern "C" vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const void *pack, size_t bytes) {
+    if (!ctx || !dims || !pack) return nullptr;
+    vh_model *m = new vh_model();
+    m->ctx = ctx;
+    m->d = dims_from(*dims);
+    char why[256];
+    if (!m->d.valid(why, sizeof(why))) {
+        set_error("model shape: %s", why);
+        delete m;
+        return nullptr;
+    }
+    if (!upload_pack(m, pack, bytes)) {
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+extern "C" void vh_model_free(vh_model *m) {
+    if (!m) return;
+    (void)hipStreamSynchronize(m->ctx->stream);
+    delete m;
+}
+
+extern "C" int vh_transformer(vh_context *ctx, vh_model *m, int layer, int axis, float *x, int S, int L) {
+    if (!ctx || !m || layer < 0 || layer >= m->d.depth || axis < 0 || axis > 1 || S <= 0 || L <= 0) return 0;
+    return transformer_block(ctx->stream, m->d, m->layers[2 * layer + axis], x, (int64_t)S * L, contiguous_layout(S, L),
+                             ctx->scratch, ctx->rope, &ctx->timer)
+               ? 1
+               : 0;
+}
+
+extern "C" int vh_stft(vh_context *ctx, vh_model *m, const float *audio, int length, float *source) {
+    if (!ctx || !m || length <= 0) return 0;
+    return stage_stft(m, audio, length, nullptr, length, 1, m->d.frames(length), source) ? 1 : 0;
+}
+
+extern "C" int vh_istft(vh_context *ctx, vh_model *m, const float *source, const float *mask, int length, float *audio) {
+    if (!ctx || !m || length <= 0) return 0;
+    return stage_istft(m, source, mask, 1, m->d.frames(length), length, audio, length) ? 1 : 0;
+}
+
+extern "C" int vh_band_split(vh_context *ctx, vh_model *m, const float *source, int frames, float *time_sequences) {
+    if (!ctx || !m || frames <= 0) return 0;
+    return stage_band_split(m, source, 1, frames, time_sequences, false) ? 1 : 0;
+}
+
+extern "C" int vh_mask_estimate(vh_context *ctx, vh_model *m, const float *features, int frames, float *mask) {
+    if (!ctx || !m || frames <= 0) return 0;
+    return stage_mask(m, features, 1, frames, mask) ? 1 : 0;
+}
+
+extern "C" int vh_forward(vh_context *ctx, vh_model *m, const float *audio, int length, float *vocals) {
+    if (!ctx || !m || length <= 0) return 0;
+    return run_windows(m, audio, length, nullptr, length, 1, vocals, length) ? 1 : 0;
+}
+
+extern "C" int vh_separate(vh_context *ctx, vh_model *m, const float *audio, int length, int chunk, int step, int batch,
+                           float *vocals) {
+    if (!ctx || !m || length <= 0 || chunk <= 0 || step <= 0 || step > chunk || batch <= 0) {
+        set_error("vh_separate: bad arguments");
+        return 0;
+    }
+    const Dims &d = m->d;
+    const int count = length <= chunk ? 1 : 1 + (length - chunk + step - 1) / step;
+    hipStream_t s = ctx->stream;
+    std::vector<int64_t> starts(count);
+    for (int k = 0; k < count; k++) starts[k] = (int64_t)k * step;
+    if (!m->starts.ensure(count * sizeof(int64_t), "hipMalloc(chunk starts)") ||
+        !m->chunk_out.ensure((size_t)count * d.channels * chunk * sizeof(float), "hipMalloc(chunk outputs)"))
+        return 0;
+    if (!check(hipMemcpyAsync(m->starts.ptr, starts.data(), count * sizeof(int64_t), hipMemcpyHostToDevice, s),
+               "hipMemcpy(chunk starts)") ||
+        !check(hipStreamSynchronize(s), "hipStreamSynchronize(starts)"))
+        return 0;
+    for (int k0 = 0; k0 < count; k0 += batch) {
+        const int n = std::min(batch, count - k0);
+        if (!run_windows(m, audio, length, static_cast<const int64_t *>(m->starts.ptr) + k0, chunk, n,
+                         m->chunk_out.f() + (size_t)k0 * d.channels * chunk, chunk))
+            return 0;
+    }
+    FadeArgs a;
+    a.chunks = m->chunk_out.f(); a.count = count; a.chunk = chunk; a.step = step; a.C = d.channels; a.length = length;
+    a.out = vocals;
+    Scope sc(&ctx->timer, s, "crossfade");
+    hipLaunchKernelGGL(crossfade_kernel, dim3((unsigned)((length + 255) / 256), d.channels), dim3(256), 0, s, a);
+    return sync_debug(s, "crossfade_kernel") ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- timing
+extern "C" int vh_timing_enable(vh_context *ctx, int enable) {
+    if (!ctx) return 0;
+    ctx->timer.enabled = enable != 0;
+    return 1;
+}
+
+extern "C" int vh_timing_reset(vh_context *ctx) {
+    if (!ctx) return 0;
+    (void)hipStreamSynchronize(ctx->stream);
+    ctx->timer.reset();
+    return 1;
+}
+
+extern "C" int vh_timing_get(vh_context *ctx, const char *name, double *total_ms, int64_t *count) {
+    if (!ctx || !name) return 0;
+    ctx->timer.collect();
+    auto it = ctx->timer.totals.find(name);
+    if (it == ctx->timer.totals.end()) return 0;
+    if (total_ms) *total_ms = it->second.first;
+    if (count) *count = it->second.second;
+    return 1;
+}

@@ -1,0 +1,225 @@
+"""ctypes binding of lib/libvocalarc_hip.so (include/vocalarc_hip.h and
+include/native_gpu.h).
+
+Device buffers are passed as raw pointers; the tests and the benchmark use
+torch tensors on cuda:0 for device memory and streams.  There is no fallback:
+if the library is missing the import of `lib()` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+from .dims import CDims, ModelDims, to_c
+
+PKG = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
+
+# Every entry point declared in include/vocalarc_hip.h and include/native_gpu.h.
+HARNESS_SYMBOLS = [
+    "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
+    "vh_rmsnorm", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_attention",
+    "vh_model_load", "vh_model_free", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
+    "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
+]
+ABI_SYMBOLS = [
+    "native_gpu_create", "native_gpu_destroy", "native_gpu_matmul", "native_gpu_backend", "native_gpu_device",
+    "native_gpu_uses_full_batches", "native_gpu_can_use_full_batches", "native_gpu_transformer",
+    "native_gpu_resident_begin", "native_gpu_resident_transformer", "native_gpu_resident_transpose",
+    "native_gpu_resident_end", "native_gpu_resident_mask",
+]
+
+EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_lib = None
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise NativeError(f"{LIB_PATH} is missing: build it with `make -C {PKG}`")
+    L = ctypes.CDLL(str(LIB_PATH))
+    sig = {
+        "vh_create": (_P, []), "vh_destroy": (None, [_P]), "vh_set_stream": (_I, [_P, _P]),
+        "vh_synchronize": (_I, [_P]), "vh_last_error": (ctypes.c_char_p, []), "vh_device_name": (ctypes.c_char_p, [_P]),
+        "vh_rmsnorm": (_I, [_P, _I64, _I, _P, _P, _P]),
+        "vh_softmax_rows": (_I, [_P, _I64, _I, _P, _P]),
+        "vh_rope_bhld": (_I, [_P, _I64, _I, _I, _P]),
+        "vh_geglu": (_I, [_P, _I64, _I, _P, _P]),
+        "vh_residual_add": (_I, [_P, _I64, _P, _P]),
+        "vh_gemm": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
+        "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I]),
+        "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
+        "vh_model_free": (None, [_P]),
+        "vh_transformer": (_I, [_P, _P, _I, _I, _P, _I, _I]),
+        "vh_stft": (_I, [_P, _P, _P, _I, _P]),
+        "vh_istft": (_I, [_P, _P, _P, _P, _I, _P]),
+        "vh_band_split": (_I, [_P, _P, _P, _I, _P]),
+        "vh_mask_estimate": (_I, [_P, _P, _P, _I, _P]),
+        "vh_forward": (_I, [_P, _P, _P, _I, _P]),
+        "vh_separate": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+        "vh_timing_enable": (_I, [_P, _I]), "vh_timing_reset": (_I, [_P]),
+        "vh_timing_get": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
+        "native_gpu_create": (_P, []), "native_gpu_destroy": (None, [_P]),
+        "native_gpu_matmul": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
+        "native_gpu_backend": (ctypes.c_char_p, [_P]), "native_gpu_device": (ctypes.c_char_p, [_P]),
+        "native_gpu_uses_full_batches": (_I, [_P]), "native_gpu_can_use_full_batches": (_I, [_P, _I]),
+        "native_gpu_transformer": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
+        "native_gpu_resident_begin": (_I, [_P, _I, _I, _P]),
+        "native_gpu_resident_transformer": (_I, [_P, _I, _I, _P]),
+        "native_gpu_resident_transpose": (_I, [_P, _I, _I]),
+        "native_gpu_resident_end": (_I, [_P, _P]),
+        "native_gpu_resident_mask": (_I, [_P, _I, _P, _P, _P, _I]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    e = lib().vh_last_error()
+    return e.decode() if e else ""
+
+
+def _ok(rc: int, what: str) -> None:
+    if not rc:
+        raise NativeError(f"{what} failed: {last_error()}")
+
+
+def ptr(t) -> int:
+    """Device (or host) address of a torch tensor / numpy array."""
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+class Context:
+    """vh_context bound to a HIP stream (default: torch's current stream)."""
+
+    def __init__(self, stream: int | None = None):
+        self.h = lib().vh_create()
+        if not self.h:
+            raise NativeError(f"vh_create failed: {last_error()}")
+        if stream is None:
+            try:
+                import torch
+                stream = torch.cuda.current_stream().cuda_stream
+            except Exception:  # noqa: BLE001 - no torch: the null stream
+                stream = 0
+        _ok(lib().vh_set_stream(self.h, stream), "vh_set_stream")
+
+    def close(self):
+        if self.h:
+            lib().vh_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+    @property
+    def device_name(self) -> str:
+        return lib().vh_device_name(self.h).decode()
+
+    def sync(self):
+        _ok(lib().vh_synchronize(self.h), "vh_synchronize")
+
+    # -- isolated kernels (device pointers) --
+    def rmsnorm(self, x, gamma, y, rows: int, dim: int):
+        _ok(lib().vh_rmsnorm(self.h, rows, dim, ptr(x), ptr(gamma), ptr(y)), "vh_rmsnorm")
+
+    def softmax_rows(self, x, y, rows: int, length: int):
+        _ok(lib().vh_softmax_rows(self.h, rows, length, ptr(x), ptr(y)), "vh_softmax_rows")
+
+    def rope_bhld(self, x, bh: int, length: int, dim_head: int = 64):
+        _ok(lib().vh_rope_bhld(self.h, bh, length, dim_head, ptr(x)), "vh_rope_bhld")
+
+    def geglu(self, x, y, rows: int, width: int):
+        _ok(lib().vh_geglu(self.h, rows, width, ptr(x), ptr(y)), "vh_geglu")
+
+    def residual_add(self, x, r, n: int):
+        _ok(lib().vh_residual_add(self.h, n, ptr(x), ptr(r)), "vh_residual_add")
+
+    def gemm(self, A, W, C, M: int, N: int, K: int, bias=None, epilogue: int = EPI_STORE,
+             lda: int | None = None, ldw: int | None = None, ldc: int | None = None):
+        _ok(lib().vh_gemm(self.h, M, N, K, ptr(A), lda or K, ptr(W), ldw or K,
+                          ptr(bias) if bias is not None else None, ptr(C),
+                          ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm")
+
+    def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True):
+        _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary)), "vh_attention")
+
+    # -- timing --
+    def timing(self, enable: bool = True):
+        _ok(lib().vh_timing_enable(self.h, int(enable)), "vh_timing_enable")
+
+    def timing_reset(self):
+        _ok(lib().vh_timing_reset(self.h), "vh_timing_reset")
+
+    def timing_get(self, name: str) -> tuple[float, int]:
+        ms = ctypes.c_double(0.0)
+        n = _I64(0)
+        if not lib().vh_timing_get(self.h, name.encode(), ctypes.byref(ms), ctypes.byref(n)):
+            return 0.0, 0
+        return ms.value, n.value
+
+
+class Model:
+    """A VSCNAT01 pack uploaded to the device."""
+
+    def __init__(self, ctx: Context, dims: ModelDims, pack) -> None:
+        self.ctx = ctx
+        self.dims = dims
+        self._cd = to_c(dims)
+        self.h = lib().vh_model_load(ctx.h, ctypes.byref(self._cd), ptr(pack), pack.nbytes)
+        if not self.h:
+            raise NativeError(f"vh_model_load failed: {last_error()}")
+
+    def close(self):
+        if self.h:
+            lib().vh_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+    def transformer(self, layer: int, axis: int, x, sequences: int, length: int):
+        _ok(lib().vh_transformer(self.ctx.h, self.h, layer, axis, ptr(x), sequences, length), "vh_transformer")
+
+    def stft(self, audio, length: int, source):
+        _ok(lib().vh_stft(self.ctx.h, self.h, ptr(audio), length, ptr(source)), "vh_stft")
+
+    def istft(self, source, mask, length: int, audio):
+        _ok(lib().vh_istft(self.ctx.h, self.h, ptr(source), ptr(mask), length, ptr(audio)), "vh_istft")
+
+    def band_split(self, source, frames: int, out):
+        _ok(lib().vh_band_split(self.ctx.h, self.h, ptr(source), frames, ptr(out)), "vh_band_split")
+
+    def mask_estimate(self, features, frames: int, mask):
+        _ok(lib().vh_mask_estimate(self.ctx.h, self.h, ptr(features), frames, ptr(mask)), "vh_mask_estimate")
+
+    def forward(self, audio, length: int, vocals):
+        _ok(lib().vh_forward(self.ctx.h, self.h, ptr(audio), length, ptr(vocals)), "vh_forward")
+
+    def separate(self, audio, length: int, chunk: int, step: int, batch: int, vocals):
+        _ok(lib().vh_separate(self.ctx.h, self.h, ptr(audio), length, chunk, step, batch, ptr(vocals)),
+            "vh_separate")

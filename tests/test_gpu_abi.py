@@ -1,0 +1,225 @@
+"""The native_gpu.h drop-in boundary on the GPU.
+
+1. The provider driven through its C-ABI exactly as the reference host drives
+   it (native/vocalarc_separation.c:1356-1406), checked against the oracle.
+2. The reference C11 host itself (compiled from the reference sources into
+   oracle/_ref and linked against lib/libvocalarc_hip.so) checked against the
+   reference CPU executable on the same pack and WAV: the north-star bar,
+   max |delta| <= 1e-4 and SNR >= 80 dB on the vocals and instrumental.
+"""
+
+import ctypes
+import os
+import tempfile
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, gpu_available, snr_db
+
+pytestmark = pytest.mark.gpu
+
+if gpu_available():
+    import oracle as O
+    from vocalarc_hip import audio, native, pack
+    from vocalarc_hip.dims import REFERENCE_DIMS as RD
+
+_F = ctypes.POINTER(ctypes.c_float)
+
+
+class TW(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("gamma", "qkv", "gate_weight", "gate_bias", "out_weight", "ff_gamma",
+                                             "ff1_weight", "ff1_bias", "ff2_weight", "ff2_bias")]
+
+
+class MB(ctypes.Structure):
+    _fields_ = [("first_weight", ctypes.c_void_p), ("first_bias", ctypes.c_void_p),
+                ("second_weight", ctypes.c_void_p), ("second_bias", ctypes.c_void_p),
+                ("input_dim", ctypes.c_int), ("first_frequency", ctypes.c_int)]
+
+
+def _weights(views, layer, axis):
+    p = f"layers.{layer}.{axis}."
+    return TW(*[views[p + n].ctypes.data for n in ("gamma", "qkv", "gate_weight", "gate_bias", "out_weight",
+                                                    "ff_gamma", "ff1_weight", "ff1_bias", "ff2_weight", "ff2_bias")])
+
+
+@pytest.fixture(scope="module")
+def provider():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    L = native.lib()
+    g = L.native_gpu_create()
+    assert g, "native_gpu_create returned NULL on a GPU box"
+    yield L, g
+    L.native_gpu_destroy(g)
+
+
+@pytest.fixture(scope="module")
+def views(ref_pack):
+    return pack.tensor_views(RD, ref_pack)
+
+
+def test_backend_strings(provider):
+    L, g = provider
+    assert L.native_gpu_backend(g) == b"native-hip-fused"
+    dev = L.native_gpu_device(g).decode()
+    assert dev and '"' not in dev and "\\" not in dev
+    assert L.native_gpu_backend(None) == b"native-cpu"
+    assert L.native_gpu_device(None) == b"none"
+    assert L.native_gpu_uses_full_batches(g) == 1
+    assert L.native_gpu_can_use_full_batches(g, 87) == 1
+    assert L.native_gpu_can_use_full_batches(g, 0) == 0
+
+
+def test_resident_path_matches_oracle(provider, views, ref_pack):
+    """begin -> 16 x {time, transpose, band, transpose} -> mask, as the host
+    calls it, vs the oracle's stack + final norm + mask estimator."""
+    L, g = provider
+    om = O.Model(RD, ref_pack)
+    x = audio.sine_mix(0.25, 21)
+    src = O.stft(RD, x)
+    T = src.shape[2]
+    seq = om.band_split(src)  # [B][T][D]
+    # oracle stack on the same input
+    feats = seq.transpose(1, 0, 2).copy()
+    cur = seq.copy()
+    for layer in range(RD.depth):
+        cur = om.transformer(layer, 0, cur, RD.bands, T)
+        feats = cur.transpose(1, 0, 2).copy()
+        feats = om.transformer(layer, 1, feats, T, RD.bands)
+        cur = feats.transpose(1, 0, 2).copy()
+    normed = O.rms_norm(feats.reshape(-1, RD.dim), views["final_gamma"]).reshape(feats.shape)
+    ref_mask = om.mask_estimate(normed)
+
+    assert L.native_gpu_resident_begin(g, RD.bands, T, seq.ctypes.data) == 1
+    for layer in range(RD.depth):
+        tw, fw = _weights(views, layer, 0), _weights(views, layer, 1)
+        assert L.native_gpu_resident_transformer(g, RD.bands, T, ctypes.byref(tw)) == 1
+        assert L.native_gpu_resident_transpose(g, RD.bands, T) == 1
+        assert L.native_gpu_resident_transformer(g, T, RD.bands, ctypes.byref(fw)) == 1
+        if layer + 1 < RD.depth:
+            assert L.native_gpu_resident_transpose(g, T, RD.bands) == 1
+    bands = (MB * RD.bands)()
+    for b, f0 in enumerate(RD.first_frequencies()):
+        bands[b] = MB(views[f"masks.{b}.first_weight"].ctypes.data, views[f"masks.{b}.first_bias"].ctypes.data,
+                      views[f"masks.{b}.second_weight"].ctypes.data, views[f"masks.{b}.second_bias"].ctypes.data,
+                      RD.input_dims()[b], f0)
+    mask = np.zeros_like(ref_mask)
+    assert L.native_gpu_resident_mask(g, T, views["final_gamma"].ctypes.data, mask.ctypes.data, bands, RD.bands) == 1
+    assert_close(ref_mask, mask, rtol=1e-3, atol=1e-5, min_snr=80, what="resident mask")
+    # residency ended with the mask
+    assert L.native_gpu_resident_transpose(g, T, RD.bands) == 0
+
+
+def test_resident_transpose_and_end_roundtrip(provider, rng):
+    """transpose is a logical flip; end returns the tensor in the current
+    logical order, bit for bit."""
+    L, g = provider
+    S, Ln = 90, 17
+    x = rng.standard_normal((S, Ln, RD.dim), dtype=np.float32)
+    out = np.empty_like(x)
+    assert L.native_gpu_resident_begin(g, S, Ln, x.ctypes.data) == 1
+    assert L.native_gpu_resident_transpose(g, S, Ln) == 1
+    o2 = np.empty((Ln, S, RD.dim), np.float32)
+    assert L.native_gpu_resident_end(g, o2.ctypes.data) == 1
+    assert np.array_equal(o2, x.transpose(1, 0, 2))
+    # two transposes give back the original
+    assert L.native_gpu_resident_begin(g, S, Ln, x.ctypes.data) == 1
+    assert L.native_gpu_resident_transpose(g, S, Ln) == 1
+    assert L.native_gpu_resident_transpose(g, Ln, S) == 1
+    assert L.native_gpu_resident_end(g, out.ctypes.data) == 1
+    assert np.array_equal(out, x)
+    # a stale residency is reset by the next begin
+    assert L.native_gpu_resident_begin(g, S, Ln, x.ctypes.data) == 1
+    assert L.native_gpu_resident_begin(g, S, Ln, x.ctypes.data) == 1
+    assert L.native_gpu_resident_end(g, out.ctypes.data) == 1
+    # token-count mismatch is refused
+    assert L.native_gpu_resident_begin(g, S, Ln, x.ctypes.data) == 1
+    assert L.native_gpu_resident_transformer(g, S, Ln + 1, None) == 0
+    assert L.native_gpu_resident_end(g, out.ctypes.data) == 1
+
+
+def test_nonresident_transformer(provider, views, ref_pack, rng):
+    L, g = provider
+    om = O.Model(RD, ref_pack)
+    S, Ln = 16, 40
+    x = rng.standard_normal((S, Ln, RD.dim), dtype=np.float32)
+    ref = om.transformer(3, 0, x, S, Ln)
+    data = x.copy()
+    w = _weights(views, 3, 0)
+    assert L.native_gpu_transformer(g, S, Ln, data.ctypes.data, None, None, None, None, ctypes.byref(w)) == 1
+    assert_close(ref, data, rtol=1e-4, atol=1e-4, min_snr=100, what="native_gpu_transformer")
+
+
+def test_matmul(provider, views, rng, monkeypatch):
+    L, g = provider
+    monkeypatch.setenv("VOCALARC_GPU_MIN_WORK", "0")
+    for b in (0, 60, 89):
+        in_dim = RD.input_dims()[b]
+        x = rng.standard_normal((37, in_dim), dtype=np.float32)
+        w, bias = views[f"bands.{b}.weight"], views[f"bands.{b}.bias"]
+        ref = O.matmul(x, w, RD.dim, bias)
+        out = np.empty((37, RD.dim), np.float32)
+        assert L.native_gpu_matmul(g, 37, in_dim, RD.dim, x.ctypes.data, w.ctypes.data, bias.ctypes.data,
+                                   out.ctypes.data) == 1
+        assert_close(ref, out, rtol=2e-5, atol=2e-6, what=f"matmul band {b}")
+    monkeypatch.setenv("VOCALARC_GPU_MIN_WORK", str(1 << 40))
+    assert L.native_gpu_matmul(g, 37, 8, RD.dim, x.ctypes.data, w.ctypes.data, None, out.ctypes.data) == 0
+
+
+# ---------------------------------------------------------------- host path
+
+def _run_host(exe, pack_path, wav, tmp, tag, env=None, threads=16):
+    v, i = tmp / f"{tag}-v.wav", tmp / f"{tag}-i.wav"
+    resp = O.run_reference(exe, pack_path, wav, v, i, threads=threads, env_extra=env)
+    sep = [r for r in resp if r.get("type") == "separated"]
+    assert sep and sep[0]["ok"], resp
+    return sep[0], audio.read_wav_float(v)[0], audio.read_wav_float(i)[0]
+
+
+@pytest.fixture(scope="module")
+def host_setup(ref_pack):
+    if not gpu_available():
+        pytest.skip("no GPU")
+    if not (O.REF_EXE.exists() and O.REF_GPU_EXE.exists()):
+        pytest.skip("reference executables not built (make -C oracle ref gpu-host)")
+    tmp = Path(tempfile.mkdtemp(prefix="vocalarc-host-"))
+    pack_path = tmp / "model.f32"
+    pack.write_pack(pack_path, ref_pack)
+    wav = tmp / "in.wav"
+    audio.write_wav_float(wav, audio.sine_mix(1.0, 2026))
+    cpu = _run_host(O.REF_EXE, pack_path, wav, tmp, "cpu")
+    return tmp, pack_path, wav, cpu
+
+
+def test_reference_host_with_hip_provider(host_setup):
+    tmp, pack_path, wav, (cpu_resp, cpu_v, cpu_i) = host_setup
+    resp, v, i = _run_host(O.REF_GPU_EXE, pack_path, wav, tmp, "gpu")
+    assert resp["backend"] == "native-hip-fused"
+    assert cpu_resp["backend"] == "native-cpu"
+    for ref, out, name in ((cpu_v, v, "vocals"), (cpu_i, i, "instrumental")):
+        err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+        assert err <= 1e-4, (name, err)
+        assert snr_db(ref, out) >= 80, (name, snr_db(ref, out))
+    print(f"host path 1 s: cpu {cpu_resp['inferenceMs']:.1f} ms, hip {resp['inferenceMs']:.1f} ms, "
+          f"vocals SNR {snr_db(cpu_v, v):.1f} dB")
+
+
+def test_reference_host_nonresident_groups(host_setup):
+    """VOCALARC_GPU_FULL_BATCHES=0: the host keeps its bounded groups and calls
+    native_gpu_transformer per group (native/vocalarc_separation.c:846)."""
+    tmp, pack_path, wav, (_, cpu_v, _) = host_setup
+    resp, v, _ = _run_host(O.REF_GPU_EXE, pack_path, wav, tmp, "gpu-groups", env={"VOCALARC_GPU_FULL_BATCHES": "0"})
+    assert resp["backend"] == "native-hip-fused"
+    assert float(np.max(np.abs(v.astype(np.float64) - cpu_v))) <= 1e-4
+    assert snr_db(cpu_v, v) >= 80
+
+
+def test_reference_host_gpu_off_is_cpu_path(host_setup):
+    """VOCALARC_GPU=off: no provider; the gpu executable is the CPU path."""
+    tmp, pack_path, wav, (_, cpu_v, _) = host_setup
+    resp, v, _ = _run_host(O.REF_GPU_EXE, pack_path, wav, tmp, "gpu-off", env={"VOCALARC_GPU": "off"})
+    assert resp["backend"] == "native-cpu"
+    assert np.array_equal(v, cpu_v)

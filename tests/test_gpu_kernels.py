@@ -1,0 +1,174 @@
+"""HIP kernels vs the oracle, through the vocalarc_hip.h C-ABI.
+
+Tolerances (fp32 path): GEMM / norms / attention compare against the oracle's
+reference-order FMA chains, so differences are summation-order rounding:
+rtol 2e-5 relative to the output scale.  Elementwise kernels (rotary,
+GELU-GLU, residual) are within a few ulps.
+"""
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, empty_dev, from_dev, gpu_available, snr_db, to_dev
+
+pytestmark = pytest.mark.gpu
+
+if gpu_available():
+    import torch
+    import oracle as O
+    from vocalarc_hip import native, pack
+    from vocalarc_hip.dims import CONFIG_DIMS, REFERENCE_DIMS
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    c = native.Context()
+    yield c
+    c.close()
+
+
+def _interleave_glu_rows(w: np.ndarray) -> np.ndarray:
+    """[2F][K] value|gate rows -> the library's 32-row interleave."""
+    two_f = w.shape[0]
+    f = two_f // 2
+    out = np.empty_like(w)
+    for c in range(f):
+        out[(c // 32) * 64 + (c % 32)] = w[c]
+        out[(c // 32) * 64 + 32 + (c % 32)] = w[f + c]
+    return out
+
+
+GEMM_CASES = [
+    # M, N, K, epilogue, bias
+    (300, 200, 96, 0, True),
+    (1000, 1536, 384, 0, False),
+    (257, 1024, 256, 1, True),
+    (77, 384, 1536, 3, True),
+    (50, 16, 1536, 0, True),
+    (40, 256, 516, 0, True),
+    (33, 8, 256, 0, True),
+    (130, 1536, 384, 2, True),
+    (1, 32, 8, 0, True),
+    (4097, 768, 384, 0, True),
+]
+
+
+@pytest.mark.parametrize("M,N,K,epi,has_bias", GEMM_CASES)
+def test_gemm_matches_oracle(ctx, rng, M, N, K, epi, has_bias):
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if has_bias else None
+    ref = O.matmul(x, pack.pack_matrix(w), N, b)
+    if epi == native.EPI_GELU:
+        ref = O.gelu(ref)
+    elif epi == native.EPI_TANH:
+        ref = np.tanh(ref.astype(np.float64)).astype(np.float32)
+    c0 = rng.standard_normal((M, N), dtype=np.float32)
+    if epi == native.EPI_RESIDUAL:
+        ref = c0 + ref
+    dx, dw = to_dev(x), to_dev(w)
+    db = to_dev(b) if b is not None else None
+    dc = to_dev(c0)
+    ctx.gemm(dx, dw, dc, M, N, K, bias=db, epilogue=epi)
+    out = from_dev(dc)
+    scale = float(np.sqrt(K)) * 0.05 * 4 + 1.0
+    assert_close(ref, out, rtol=2e-5, atol=2e-5 * scale, what=f"gemm {M}x{N}x{K} epi{epi}")
+
+
+def test_gemm_geglu_epilogue(ctx, rng):
+    M, F, K = 190, 1536, 384
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((2 * F, K))).astype(np.float32)
+    b = rng.standard_normal(2 * F).astype(np.float32)
+    ref = O.geglu(O.matmul(x, pack.pack_matrix(w), 2 * F, b))
+    wi = _interleave_glu_rows(w)
+    bi = _interleave_glu_rows(b[:, None])[:, 0].copy()
+    dc = empty_dev((M, F))
+    ctx.gemm(to_dev(x), to_dev(wi), dc, M, 2 * F, K, bias=to_dev(bi), epilogue=native.EPI_GEGLU)
+    assert_close(ref, from_dev(dc), rtol=2e-5, atol=5e-5, what="gemm geglu")
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 8), (333, 384), (1000, 256), (64, 516), (49662, 384)])
+def test_rmsnorm(ctx, rng, rows, dim):
+    x = rng.standard_normal((rows, dim), dtype=np.float32)
+    g = (1.0 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    ref = O.rms_norm(x, g)
+    dy = empty_dev((rows, dim))
+    ctx.rmsnorm(to_dev(x), to_dev(g), dy, rows, dim)
+    assert_close(ref, from_dev(dy), rtol=4e-6, atol=1e-6, what=f"rmsnorm {rows}x{dim}")
+
+
+@pytest.mark.parametrize("rows,length", [(7, 801), (100, 62), (3, 1), (5, 2048), (2000, 801)])
+def test_softmax_rows(ctx, rng, rows, length):
+    x = (3.0 * rng.standard_normal((rows, length))).astype(np.float32)
+    ref = O.softmax_rows(x)
+    dy = empty_dev((rows, length))
+    ctx.softmax_rows(to_dev(x), dy, rows, length)
+    out = from_dev(dy)
+    assert_close(ref, out, rtol=1e-5, atol=1e-9, what="softmax")
+    assert np.allclose(out.astype(np.float64).sum(-1), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("b,length", [(62, 801), (801, 62), (3, 5)])
+def test_rope_bhld(ctx, rng, b, length):
+    x = rng.standard_normal((b, 8, length, 64), dtype=np.float32)
+    ref = O.rope_bhld(x)
+    dx = to_dev(x)
+    ctx.rope_bhld(dx, b * 8, length)
+    out = from_dev(dx)
+    assert_close(ref, out, rtol=1e-6, atol=1e-6, what="rope")
+    # rotation preserves the norm of each pair
+    n_in = x[..., 0::2] ** 2 + x[..., 1::2] ** 2
+    n_out = out[..., 0::2].astype(np.float64) ** 2 + out[..., 1::2] ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,width", [(49662, 1536), (7, 4)])
+def test_geglu(ctx, rng, rows, width):
+    x = rng.standard_normal((rows, 2 * width), dtype=np.float32)
+    ref = O.geglu(x)
+    dy = empty_dev((rows, width))
+    ctx.geglu(to_dev(x), dy, rows, width)
+    # 1 + erf(g/sqrt2) cancels for strongly negative gates, so the few-ulp
+    # difference between the device and libm erff is bounded in absolute
+    # terms (outputs are O(1) here), not relative ones.
+    assert_close(ref, from_dev(dy), rtol=2e-6, atol=2e-6, what="geglu")
+
+
+def test_residual_add(ctx, rng):
+    n = 49662 * 384
+    x = rng.standard_normal(n, dtype=np.float32)
+    r = rng.standard_normal(n, dtype=np.float32)
+    dx = to_dev(x)
+    ctx.residual_add(dx, to_dev(r), n)
+    assert np.array_equal(from_dev(dx), x + r)
+
+
+def _rotate_qk(qkv: np.ndarray, length: int, heads: int) -> np.ndarray:
+    cos, sin = O.rope_table(length, 64)
+    out = qkv.copy()
+    tokens = qkv.shape[0]
+    pos = np.arange(tokens) % length
+    inner = heads * 64
+    for which in range(2):
+        blk = out[:, which * inner:(which + 1) * inner].reshape(tokens, heads, 32, 2)
+        a, b = blk[..., 0].copy(), blk[..., 1].copy()
+        c, s = cos[pos][:, None, :], sin[pos][:, None, :]
+        blk[..., 0] = a * c - b * s
+        blk[..., 1] = a * s + b * c
+        out[:, which * inner:(which + 1) * inner] = blk.reshape(tokens, inner)
+    return out
+
+
+@pytest.mark.parametrize("S,L", [(5, 62), (2, 801), (3, 33), (4, 1), (1, 65), (2, 130)])
+def test_attention_core(ctx, rng, S, L):
+    H = 8
+    qkv = rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32)
+    ref = O.attention(REFERENCE_DIMS, _rotate_qk(qkv, L, H), S, L)
+    dout = empty_dev((S * L, H * 64))
+    ctx.attention(to_dev(qkv), dout, S, L, H, rotary=True)
+    out = from_dev(dout)
+    assert_close(ref, out, rtol=2e-5, atol=2e-5, what=f"attention S={S} L={L}")
+    assert snr_db(ref, out) > 100

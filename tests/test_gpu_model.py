@@ -1,0 +1,161 @@
+"""Device pipeline (vocalarc_hip.h model entry points) vs the oracle.
+
+Stage tests compare one stage at a time on identical inputs; the forward and
+chunked tests compare whole waveforms at the north-star bar for the fp32
+path: per-sample max |delta| <= 1e-4 and SNR >= 80 dB.
+"""
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, empty_dev, from_dev, gpu_available, snr_db, to_dev
+
+pytestmark = pytest.mark.gpu
+
+if gpu_available():
+    import oracle as O
+    from vocalarc_hip import audio, native, pack
+    from vocalarc_hip.dims import CONFIG_DIMS, REFERENCE_DIMS
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    c = native.Context()
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def cfg2():
+    """Config shape (dim 384, 62 bands, hop 441, GELU-GLU) at depth 2."""
+    d = CONFIG_DIMS.with_depth(2)
+    return d, pack.synthetic_pack(d, 77)
+
+
+@pytest.fixture(scope="module")
+def cfg2_models(ctx, cfg2):
+    d, blob = cfg2
+    return O.Model(d, blob), native.Model(ctx, d, blob)
+
+
+@pytest.fixture(scope="module")
+def ref_models(ctx, ref_pack):
+    return O.Model(REFERENCE_DIMS, ref_pack), native.Model(ctx, REFERENCE_DIMS, ref_pack)
+
+
+@pytest.mark.parametrize("axis,S,L", [(0, 4, 62), (1, 3, 130), (0, 2, 801)])
+def test_transformer_block_config(cfg2_models, rng, axis, S, L):
+    om, dm = cfg2_models
+    x = rng.standard_normal((S, L, om.d.dim), dtype=np.float32)
+    ref = om.transformer(1, axis, x, S, L)
+    dx = to_dev(x)
+    dm.transformer(1, axis, dx, S, L)
+    out = from_dev(dx)
+    assert_close(ref, out, rtol=1e-4, atol=1e-4, min_snr=100, what="transformer (config)")
+
+
+@pytest.mark.parametrize("axis,S,L", [(0, 90, 23), (1, 23, 90)])
+def test_transformer_block_reference_shape(ref_models, rng, axis, S, L):
+    om, dm = ref_models
+    x = rng.standard_normal((S, L, om.d.dim), dtype=np.float32)
+    ref = om.transformer(5, axis, x, S, L)
+    dx = to_dev(x)
+    dm.transformer(5, axis, dx, S, L)
+    assert_close(ref, from_dev(dx), rtol=1e-4, atol=1e-4, min_snr=100, what="transformer (reference)")
+
+
+@pytest.mark.parametrize("which", ["config", "reference"])
+def test_stft_istft(ctx, cfg2_models, ref_models, which):
+    om, dm = cfg2_models if which == "config" else ref_models
+    d = om.d
+    x = audio.sine_mix(0.5, 3)
+    length = x.shape[1]
+    T = d.frames(length)
+    src = O.stft(d, x)
+    dsrc = empty_dev(src.shape)
+    dm.stft(to_dev(x), length, dsrc)
+    gsrc = from_dev(dsrc)
+    assert_close(src, gsrc, rtol=1e-6, atol=2e-6, min_snr=120, what="stft")
+    rng = np.random.default_rng(5)
+    mask = rng.standard_normal(src.shape).astype(np.float32)
+    ref = O.istft(d, src, mask, length)
+    dout = empty_dev((d.channels, length))
+    dm.istft(to_dev(src), to_dev(mask), length, dout)
+    assert_close(ref, from_dev(dout), rtol=1e-5, atol=1e-6, min_snr=120, what="istft")
+    assert T == src.shape[2]
+
+
+def test_istft_perfect_reconstruction(ctx, cfg2_models):
+    """A unit mask reproduces the input (closed form: Hann OLA normalised by
+    the summed squared window)."""
+    om, dm = cfg2_models
+    d = om.d
+    x = audio.sine_mix(0.4, 9)
+    length = x.shape[1]
+    dsrc = empty_dev((d.freq_bins, d.channels, d.frames(length), 2))
+    dm.stft(to_dev(x), length, dsrc)
+    ones = np.zeros((d.freq_bins, d.channels, d.frames(length), 2), np.float32)
+    ones[..., 0] = 1.0
+    dout = empty_dev((d.channels, length))
+    dm.istft(dsrc, to_dev(ones), length, dout)
+    assert_close(x, from_dev(dout), rtol=0, atol=2e-6, what="istft(stft(x))")
+
+
+@pytest.mark.parametrize("which", ["config", "reference"])
+def test_band_split_and_mask(ctx, cfg2_models, ref_models, which, rng):
+    om, dm = cfg2_models if which == "config" else ref_models
+    d = om.d
+    x = audio.sine_mix(0.3, 4)
+    src = O.stft(d, x)
+    T = src.shape[2]
+    ref = om.band_split(src)
+    dout = empty_dev(ref.shape)
+    dm.band_split(to_dev(src), T, dout)
+    assert_close(ref, from_dev(dout), rtol=1e-4, atol=2e-5, min_snr=110, what="band split")
+    feats = rng.standard_normal((T, d.bands, d.dim), dtype=np.float32)
+    mref = om.mask_estimate(feats)
+    dmask = empty_dev(mref.shape)
+    dm.mask_estimate(to_dev(feats), T, dmask)
+    assert_close(mref, from_dev(dmask), rtol=1e-4, atol=1e-5, min_snr=110, what="mask estimator")
+
+
+def test_forward_config_shape(cfg2_models):
+    om, dm = cfg2_models
+    x = audio.sine_mix(0.5, 11)
+    ref = om.forward(x)
+    dv = empty_dev(x.shape)
+    dm.forward(to_dev(x), x.shape[1], dv)
+    out = from_dev(dv)
+    err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    assert err <= 1e-4, err
+    assert snr_db(ref, out) >= 80
+
+
+def test_forward_reference_shape(ref_models):
+    om, dm = ref_models
+    x = audio.sine_mix(0.2, 12)
+    ref = om.forward(x)
+    dv = empty_dev(x.shape)
+    dm.forward(to_dev(x), x.shape[1], dv)
+    out = from_dev(dv)
+    err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    assert err <= 1e-4, err
+    assert snr_db(ref, out) >= 80
+
+
+def test_chunked_separation(ctx):
+    d = CONFIG_DIMS.with_depth(1)
+    blob = pack.synthetic_pack(d, 91)
+    om, dm = O.Model(d, blob), native.Model(ctx, d, blob)
+    x = audio.sine_mix(1.0, 13)
+    chunk, step = 13230, 8820  # 0.3 s windows every 0.2 s -> 5 chunks
+    ref = om.separate_chunked(x, chunk, step)
+    dv = empty_dev(x.shape)
+    dm.separate(to_dev(x), x.shape[1], chunk, step, 2, dv)
+    out = from_dev(dv)
+    assert O.chunk_count(x.shape[1], chunk, step) == 5
+    err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    assert err <= 1e-4, err
+    assert snr_db(ref, out) >= 80
