@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Benchmark: realtime factor of the full separation path on one MI355X.
+
+Workload (one "step"): separate a 5-minute stereo 44.1 kHz seeded mix (6 sine
+partials per channel + white noise) with a random-init BS-RoFormer of dim 384,
+depth 12, 62 bands, 8 heads x 64, GELU-GLU FFN (mult 4), hop 441, n_fft 2048:
+8 s windows with 2 s overlap (50 windows), 8 windows per device pass, linear
+cross-fade.  The input waveform is resident in HBM when the timed region
+starts; the output waveform is in HBM when it ends.  fp32 throughout.
+
+value = audio seconds separated per wall second (realtime factor).
+roofline: the dominant kernel (the FFN up-projection GEMM with the GELU-GLU
+epilogue), timed with HIP events on the launch stream inside the timed
+region; FLOPs counted algorithmically (2*M*K*N per launch).
+cpu_baseline: the oracle (C restatement of the reference CPU path) on the
+host cores, timed on a bounded sample of the same workload and scaled to the
+whole job.
+
+    python bench.py [--gpus 1] [--steps 3] [--warmup 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "karaoke-platform-sidecar-native_amd"))
+
+SECONDS = 300.0
+CHUNK_S, STEP_S, BATCH = 8.0, 6.0, 8
+RATE = 44_100
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+DOMINANT = "gemm_ff1"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def ff1_flops_per_step(d, chunk: int, step: int, length: int, batch: int) -> float:
+    count = 1 if length <= chunk else 1 + (length - chunk + step - 1) // step
+    T = d.frames(chunk)
+    flops = 0.0
+    for k0 in range(0, count, batch):
+        n = min(batch, count - k0)
+        M = n * T * d.bands
+        flops += 2 * d.depth * (2.0 * M * d.dim * d.ff1_out)  # time + band axis per layer
+    return flops
+
+
+def cpu_baseline(d, blob, x, chunk: int, step: int, threads: int) -> dict:
+    """Oracle on one 8 s window: the front end + one axial layer, the front end
+    alone (difference = one layer), and the mask estimator + iSTFT; scaled to
+    depth 12 and to all windows of the job."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
+    import oracle as O
+
+    O.set_threads(threads)
+    m = O.Model(d, blob)
+    w = np.ascontiguousarray(x[:, :chunk])
+    t0 = time.perf_counter()
+    m.forward_layers(w, 0)
+    t_front = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    feats = m.forward_layers(w, 1)
+    t_front_layer = time.perf_counter() - t0
+    t_layer = max(t_front_layer - t_front, 1e-9)
+    src = O.stft(d, w)
+    t0 = time.perf_counter()
+    normed = O.rms_norm(feats.reshape(-1, d.dim), _final_gamma(d, blob)).reshape(feats.shape)
+    mask = m.mask_estimate(normed)
+    O.istft(d, src, mask, chunk)
+    t_back = time.perf_counter() - t0
+    per_window = t_front + d.depth * t_layer + t_back
+    count = 1 + (x.shape[1] - chunk + step - 1) // step
+    job = per_window * count
+    sample = t_front + t_front_layer + t_back
+    return {
+        "value": round(x.shape[1] / RATE / job, 4),
+        "unit": "audio s / wall s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle (C restatement of the reference CPU path, OpenMP) on one 8 s window: front end "
+                   f"{t_front:.2f} s, one axial layer {t_layer:.2f} s, mask+iSTFT {t_back:.2f} s "
+                   f"({sample:.1f} s of CPU work); scaled to depth {d.depth} x {count} windows = {job:.0f} s"),
+    }
+
+
+def _final_gamma(d, blob):
+    from vocalarc_hip import pack
+    return pack.tensor_views(d, blob)["final_gamma"]
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--seconds", type=float, default=SECONDS)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build runs the separation path on a single GPU "
+              "(multi-GPU sharding by windows is described in DESIGN.md, not implemented)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from vocalarc_hip import audio, native, pack
+    from vocalarc_hip.dims import CONFIG_DIMS
+
+    d = CONFIG_DIMS
+    chunk, step = int(CHUNK_S * RATE), int(STEP_S * RATE)
+    log("generating synthetic pack and input ...")
+    blob = pack.synthetic_pack(d, 2026)
+    x = audio.sine_mix(args.seconds, 300)
+    length = x.shape[1]
+
+    ctx = native.Context()
+    model = native.Model(ctx, d, blob)
+    dx = torch.from_numpy(x).to("cuda:0")
+    dv = torch.empty_like(dx)
+    torch.cuda.synchronize()
+
+    for i in range(args.warmup):
+        t0 = time.perf_counter()
+        model.separate(dx, length, chunk, step, BATCH, dv)
+        ctx.sync()
+        log(f"warmup step {i}: {time.perf_counter() - t0:.3f} s")
+
+    ctx.timing(DOMINANT)
+    ctx.timing_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        model.separate(dx, length, chunk, step, BATCH, dv)
+    ctx.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ctx.timing(None)
+    ms, launches = ctx.timing_get(DOMINANT)
+    log(f"timed {args.steps} steps: {wall:.3f} s")
+
+    out = dv.cpu().numpy()
+    assert np.all(np.isfinite(out)), "non-finite output"
+
+    flops = ff1_flops_per_step(d, chunk, step, length, BATCH) * args.steps
+    achieved = flops / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+    roofline = {
+        "kernel": "gemm_f32_kernel<GELU-GLU> (FFN up-projection, M=397296 K=384 N=3072 per 8-window pass)",
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": MFMA_FP32_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "launches": launches,
+        "avg_launch_ms": round(ms / max(launches, 1), 4),
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle) ...")
+        cpu = cpu_baseline(d, blob, x, chunk, step, os.cpu_count() or 1)
+
+    audio_s = length / RATE * args.steps
+    line = {
+        "metric": "realtime factor (audio s / wall s) on 1xMI355X; kernel HBM GB/s & MFMA % of peak",
+        "value": round(audio_s / wall, 3),
+        "unit": "audio s / wall s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded sine+noise mix, random-init weights N(0,0.02), gammas N(1,0.02))",
+        "config": {
+            "workload": "full BS-RoFormer separation, 5 min stereo 44.1 kHz, 8 s windows / 2 s overlap, "
+                        "8 windows per device pass",
+            "audio_seconds": round(length / RATE, 3),
+            "dim": d.dim, "depth": d.depth, "bands": d.bands, "heads": d.heads, "dim_head": d.dim_head,
+            "ffn": "GELU-GLU x4", "n_fft": d.n_fft, "hop": d.hop, "windows_per_pass": BATCH,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    model.close()
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -104,8 +104,11 @@ int vh_separate(vh_context *ctx, vh_model *model, const float *audio, int length
                 float *vocals);
 
 /* ---- measurement --------------------------------------------------------- */
-/* Per-kernel-class timing with HIP events on the context stream. */
-int vh_timing_enable(vh_context *ctx, int enable);
+/* Per-kernel-class timing with HIP events recorded on the context stream
+   around each launch of the selected classes: a comma-separated list of
+   class names (e.g. "gemm_ff1,attention_long"), "*" for all, NULL or ""
+   to stop timing. */
+int vh_timing_enable(vh_context *ctx, const char *classes);
 int vh_timing_reset(vh_context *ctx);
 /* Total milliseconds and launch count of a kernel class since the last reset
    (after vh_synchronize).  Returns 0 if the class never ran. */

@@ -71,6 +71,13 @@ void DeviceBuffer::release() {
 }
 
 // ----------------------------------------------------------------- timing
+bool KernelTimer::wants(const char *name) const {
+    if (all) return true;
+    for (const auto &n : only)
+        if (n == name) return true;
+    return false;
+}
+
 void KernelTimer::begin(hipStream_t s, const char *, hipEvent_t *a) {
     (void)hipEventCreate(a);
     (void)hipEventRecord(*a, s);

@@ -43,6 +43,9 @@ struct DeviceBuffer {
 // stream around each launch of a named class (e.g. "gemm_ff1").
 struct KernelTimer {
     bool enabled = false;
+    bool all = false;
+    std::vector<std::string> only;  // classes to time when !all
+    bool wants(const char *name) const;
     struct Pending { std::string name; hipEvent_t a, b; };
     std::vector<Pending> pending;
     std::map<std::string, std::pair<double, int64_t>> totals;  // ms, count
@@ -58,10 +61,10 @@ struct Scope {
     const char *name;
     hipEvent_t a = nullptr;
     Scope(KernelTimer *t_, hipStream_t s_, const char *n) : t(t_), s(s_), name(n) {
-        if (t && t->enabled) t->begin(s, name, &a);
+        if (t && t->enabled && t->wants(name)) t->begin(s, name, &a);
     }
     ~Scope() {
-        if (t && t->enabled) t->end(s, name, a);
+        if (a) t->end(s, name, a);
     }
 };
 

@@ -563,9 +563,21 @@ extern "C" int vh_separate(vh_context *ctx, vh_model *m, const float *audio, int
 }
 
 // ---------------------------------------------------------------- timing
-extern "C" int vh_timing_enable(vh_context *ctx, int enable) {
+extern "C" int vh_timing_enable(vh_context *ctx, const char *classes) {
     if (!ctx) return 0;
-    ctx->timer.enabled = enable != 0;
+    KernelTimer &t = ctx->timer;
+    t.only.clear();
+    t.all = classes && strcmp(classes, "*") == 0;
+    t.enabled = classes && classes[0];
+    if (t.enabled && !t.all) {
+        const char *p = classes;
+        while (*p) {
+            const char *e = strchr(p, ',');
+            const size_t n = e ? (size_t)(e - p) : strlen(p);
+            if (n) t.only.emplace_back(p, n);
+            p += n + (e ? 1 : 0);
+        }
+    }
     return 1;
 }
 

@@ -69,7 +69,7 @@ def lib():
         "vh_mask_estimate": (_I, [_P, _P, _P, _I, _P]),
         "vh_forward": (_I, [_P, _P, _P, _I, _P]),
         "vh_separate": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
-        "vh_timing_enable": (_I, [_P, _I]), "vh_timing_reset": (_I, [_P]),
+        "vh_timing_enable": (_I, [_P, ctypes.c_char_p]), "vh_timing_reset": (_I, [_P]),
         "vh_timing_get": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
         "native_gpu_create": (_P, []), "native_gpu_destroy": (None, [_P]),
         "native_gpu_matmul": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
@@ -166,8 +166,9 @@ class Context:
         _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary)), "vh_attention")
 
     # -- timing --
-    def timing(self, enable: bool = True):
-        _ok(lib().vh_timing_enable(self.h, int(enable)), "vh_timing_enable")
+    def timing(self, classes: str | None = "*"):
+        """Time the named kernel classes (comma list, "*" = all, None = off)."""
+        _ok(lib().vh_timing_enable(self.h, classes.encode() if classes else None), "vh_timing_enable")
 
     def timing_reset(self):
         _ok(lib().vh_timing_reset(self.h), "vh_timing_reset")
