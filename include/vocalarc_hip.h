@@ -93,15 +93,17 @@ int vh_band_split(vh_context *ctx, vh_model *model, const float *source, int fra
    final-normed device features[T][B][dim] -> device mask[F][C][T][2]. */
 int vh_mask_estimate(vh_context *ctx, vh_model *model, const float *features, int frames, float *mask);
 /* Whole forward of one window (native/vocalarc_separation.c:1342-1445):
-   device audio[C][length] -> device vocals[C][length]. */
-int vh_forward(vh_context *ctx, vh_model *model, const float *audio, int length, float *vocals);
+   device audio[C][length] -> device vocals[C][length]; when `instrumental`
+   is not NULL it receives audio - vocals (native/vocalarc_separation.c:1589-1591). */
+int vh_forward(vh_context *ctx, vh_model *model, const float *audio, int length, float *vocals,
+               float *instrumental);
 /* Chunked separation of a long device audio[C][length]: windows of `chunk`
    samples every `step` samples (zero-padded at the end), `batch` windows per
    device pass, linear cross-fade over the overlap normalised by the summed
-   fade weights.  No reference counterpart (the reference host runs the whole
+   fade weights; `instrumental` (nullable) as for vh_forward.  No reference counterpart (the reference host runs the whole
    file as one window, native/vocalarc_separation.c:1344). */
 int vh_separate(vh_context *ctx, vh_model *model, const float *audio, int length, int chunk, int step, int batch,
-                float *vocals);
+                float *vocals, float *instrumental);
 
 /* ---- measurement --------------------------------------------------------- */
 /* Per-kernel-class timing with HIP events recorded on the context stream

@@ -169,6 +169,8 @@ struct FadeArgs {
     int count, chunk, step, C;
     int64_t length;
     float *out;
+    const float *mix;    // input audio [C][length] (for the instrumental)
+    float *instrumental; // may be null
 };
 
 VH_DEVICE float fade_weight(int i, int k, int count, int chunk, int step) {
@@ -194,7 +196,17 @@ static __global__ __launch_bounds__(256) void crossfade_kernel(FadeArgs a) {
         acc += w * a.chunks[((size_t)k * a.C + c) * a.chunk + i];
         ws += w;
     }
-    a.out[(size_t)c * a.length + s] = acc / ws;
+    const float v = acc / ws;
+    a.out[(size_t)c * a.length + s] = v;
+    if (a.instrumental) a.instrumental[(size_t)c * a.length + s] = a.mix[(size_t)c * a.length + s] - v;
+}
+
+// instrumental = mix - vocals (native/vocalarc_separation.c:1589-1591)
+static __global__ __launch_bounds__(256) void subtract_kernel(const float *__restrict__ mix,
+                                                              const float *__restrict__ vocals,
+                                                              float *__restrict__ inst, int64_t n) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e < n) inst[e] = mix[e] - vocals[e];
 }
 
 }  // namespace vh

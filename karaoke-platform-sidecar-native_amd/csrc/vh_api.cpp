@@ -525,13 +525,21 @@ extern "C" int vh_mask_estimate(vh_context *ctx, vh_model *m, const float *featu
     return stage_mask(m, features, 1, frames, mask) ? 1 : 0;
 }
 
-extern "C" int vh_forward(vh_context *ctx, vh_model *m, const float *audio, int length, float *vocals) {
+extern "C" int vh_forward(vh_context *ctx, vh_model *m, const float *audio, int length, float *vocals,
+                          float *instrumental) {
     if (!ctx || !m || length <= 0) return 0;
-    return run_windows(m, audio, length, nullptr, length, 1, vocals, length) ? 1 : 0;
+    if (!run_windows(m, audio, length, nullptr, length, 1, vocals, length)) return 0;
+    if (instrumental) {
+        const int64_t n = (int64_t)m->d.channels * length;
+        hipLaunchKernelGGL(subtract_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, audio, vocals,
+                           instrumental, n);
+        if (!sync_debug(ctx->stream, "subtract_kernel")) return 0;
+    }
+    return 1;
 }
 
 extern "C" int vh_separate(vh_context *ctx, vh_model *m, const float *audio, int length, int chunk, int step, int batch,
-                           float *vocals) {
+                           float *vocals, float *instrumental) {
     if (!ctx || !m || length <= 0 || chunk <= 0 || step <= 0 || step > chunk || batch <= 0) {
         set_error("vh_separate: bad arguments");
         return 0;
@@ -557,6 +565,8 @@ extern "C" int vh_separate(vh_context *ctx, vh_model *m, const float *audio, int
     FadeArgs a;
     a.chunks = m->chunk_out.f(); a.count = count; a.chunk = chunk; a.step = step; a.C = d.channels; a.length = length;
     a.out = vocals;
+    a.mix = audio;
+    a.instrumental = instrumental;
     Scope sc(&ctx->timer, s, "crossfade");
     hipLaunchKernelGGL(crossfade_kernel, dim3((unsigned)((length + 255) / 256), d.channels), dim3(256), 0, s, a);
     return sync_debug(s, "crossfade_kernel") ? 1 : 0;

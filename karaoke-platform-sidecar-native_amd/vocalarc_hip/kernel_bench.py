@@ -1,0 +1,144 @@
+"""Per-kernel throughput on one MI355X against the roofline.
+
+Isolated kernels (fp32, inputs N(0,1), gammas N(1,0.02)):
+  RMSNorm [49662, 384]; row softmax [496, 801, 801]; rotary [62,8,801,64] and
+  [801,8,62,64]; GELU-GLU [49662, 3072] -> [49662, 1536]; residual add
+  [49662, 384].
+One axial layer at dim 384 (weights N(0,0.02), activations N(0,1)):
+  time transformer (62 sequences x 801), band transformer (801 x 62).
+Front/back end on 60 s of audio (hop 441, n_fft 2048, 62 bands):
+  STFT, complex mask multiply + iSTFT + overlap-add, band split, mask estimator.
+
+Work per launch is algorithmic (each tensor read and written once; 2*M*K*N
+per GEMM); time is the mean over repetitions measured with HIP events on the
+launch stream.  One JSON line per kernel on stdout.
+
+    PYTHONPATH=karaoke-platform-sidecar-native_amd python -m vocalarc_hip.kernel_bench
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+import numpy as np
+
+HBM_GBS = 8000.0
+FP32_TFLOPS = 157.3
+
+
+def _event_time(fn, reps: int) -> float:
+    import torch
+    fn()  # warm-up (also builds per-length tables)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | None = None, shape: str = "") -> dict:
+    rec = {"kernel": name, "shape": shape, "ms": round(ms, 4)}
+    if gbytes is not None:
+        gbs = gbytes / (ms * 1e-3)
+        rec.update({"algorithmic_GB": round(gbytes, 4), "GB_per_s": round(gbs, 1),
+                    "bound": "hbm", "frac_of_peak": round(gbs / HBM_GBS, 4)})
+    if gflop is not None:
+        tf = gflop / (ms * 1e-3) / 1e3
+        rec.update({"algorithmic_GFLOP": round(gflop, 2), "TFLOP_per_s": round(tf, 2),
+                    "bound": "mfma", "frac_of_peak": round(tf / FP32_TFLOPS, 4)})
+    print(json.dumps(rec), flush=True)
+    return rec
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--only", default="", help="comma list of groups: c1,c2,c3")
+    args = ap.parse_args()
+    groups = set(args.only.split(",")) if args.only else {"c1", "c2", "c3"}
+
+    import torch
+
+    from . import audio, native, pack
+    from .dims import CONFIG_DIMS
+
+    dev = "cuda:0"
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    ctx = native.Context()
+    reps = args.reps
+
+    if "c1" in groups:
+        rows, dim = 49662, 384
+        x = torch.randn(rows, dim, device=dev, generator=g)
+        gamma = 1 + 0.02 * torch.randn(dim, device=dev, generator=g)
+        y = torch.empty_like(x)
+        _emit("rmsnorm", _event_time(lambda: ctx.rmsnorm(x, gamma, y, rows, dim), reps),
+              gbytes=2 * rows * dim * 4 / 1e9, shape="[49662,384]")
+        s = torch.randn(496 * 801, 801, device=dev, generator=g)
+        so = torch.empty_like(s)
+        _emit("softmax_rows", _event_time(lambda: ctx.softmax_rows(s, so, 496 * 801, 801), reps),
+              gbytes=2 * s.numel() * 4 / 1e9, shape="[496,801,801]")
+        del s, so
+        for b, length in ((62, 801), (801, 62)):
+            r = torch.randn(b, 8, length, 64, device=dev, generator=g)
+            _emit("rope", _event_time(lambda: ctx.rope_bhld(r, b * 8, length), reps),
+                  gbytes=2 * r.numel() * 4 / 1e9, shape=f"[{b},8,{length},64]")
+        gi = torch.randn(rows, 3072, device=dev, generator=g)
+        go = torch.empty(rows, 1536, device=dev)
+        _emit("geglu", _event_time(lambda: ctx.geglu(gi, go, rows, 1536), reps),
+              gbytes=(gi.numel() + go.numel()) * 4 / 1e9, shape="[49662,3072]->[49662,1536]")
+        del gi, go
+        r = torch.randn(rows, dim, device=dev, generator=g)
+        _emit("residual_add", _event_time(lambda: ctx.residual_add(x, r, rows * dim), reps),
+              gbytes=3 * rows * dim * 4 / 1e9, shape="[49662,384]")
+        del x, y, r
+
+    if "c2" in groups or "c3" in groups:
+        d = CONFIG_DIMS.with_depth(1)
+        blob = pack.synthetic_pack(d, 2)
+        model = native.Model(ctx, d, blob)
+        T, B, D = 801, 62, 384
+        tokens = T * B
+        lin = 2.0 * tokens * (D * 1536 + D * 8 + 512 * D + D * 3072 + 1536 * D) / 1e9
+        if "c2" in groups:
+            xt = torch.randn(B, T, D, device=dev, generator=g)
+            att_t = 4.0 * B * 8 * T * T * 64 / 1e9
+            _emit("time_transformer", _event_time(lambda: model.transformer(0, 0, xt, B, T), max(3, reps // 4)),
+                  gflop=lin + att_t, shape="62 seq x 801, dim 384")
+            xb = torch.randn(T, B, D, device=dev, generator=g)
+            att_b = 4.0 * T * 8 * B * B * 64 / 1e9
+            _emit("band_transformer", _event_time(lambda: model.transformer(0, 1, xb, T, B), max(3, reps // 4)),
+                  gflop=lin + att_b, shape="801 seq x 62, dim 384")
+            del xt, xb
+        if "c3" in groups:
+            x = torch.from_numpy(audio.sine_mix(60.0, 60)).to(dev)
+            length = x.shape[1]
+            Tf = d.frames(length)
+            src = torch.empty(d.freq_bins, d.channels, Tf, 2, device=dev)
+            _emit("stft", _event_time(lambda: model.stft(x, length, src), reps),
+                  gbytes=(x.numel() + src.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}")
+            mask = torch.randn_like(src)
+            out = torch.empty_like(x)
+            _emit("istft", _event_time(lambda: model.istft(src, mask, length, out), reps),
+                  gbytes=(2 * src.numel() + out.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}")
+            seq = torch.empty(d.bands, Tf, D, device=dev)
+            _emit("band_split", _event_time(lambda: model.band_split(src, Tf, seq), reps),
+                  gflop=2.0 * Tf * sum(d.input_dims()) * D / 1e9, shape=f"T={Tf}, 62 bands")
+            feats = torch.randn(Tf, d.bands, D, device=dev, generator=g)
+            mout = torch.empty_like(src)
+            gf = 2.0 * Tf * (d.bands * D * d.mask_hidden + d.mask_hidden * 2 * sum(d.input_dims())) / 1e9
+            _emit("mask_estimator", _event_time(lambda: model.mask_estimate(feats, Tf, mout), max(3, reps // 4)),
+                  gflop=gf, shape=f"T={Tf}, 62 bands")
+        model.close()
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

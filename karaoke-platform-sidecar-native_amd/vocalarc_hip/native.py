@@ -67,8 +67,8 @@ def lib():
         "vh_istft": (_I, [_P, _P, _P, _P, _I, _P]),
         "vh_band_split": (_I, [_P, _P, _P, _I, _P]),
         "vh_mask_estimate": (_I, [_P, _P, _P, _I, _P]),
-        "vh_forward": (_I, [_P, _P, _P, _I, _P]),
-        "vh_separate": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+        "vh_forward": (_I, [_P, _P, _P, _I, _P, _P]),
+        "vh_separate": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
         "vh_timing_enable": (_I, [_P, ctypes.c_char_p]), "vh_timing_reset": (_I, [_P]),
         "vh_timing_get": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
         "native_gpu_create": (_P, []), "native_gpu_destroy": (None, [_P]),
@@ -218,9 +218,10 @@ class Model:
     def mask_estimate(self, features, frames: int, mask):
         _ok(lib().vh_mask_estimate(self.ctx.h, self.h, ptr(features), frames, ptr(mask)), "vh_mask_estimate")
 
-    def forward(self, audio, length: int, vocals):
-        _ok(lib().vh_forward(self.ctx.h, self.h, ptr(audio), length, ptr(vocals)), "vh_forward")
+    def forward(self, audio, length: int, vocals, instrumental=None):
+        _ok(lib().vh_forward(self.ctx.h, self.h, ptr(audio), length, ptr(vocals),
+                             ptr(instrumental) if instrumental is not None else None), "vh_forward")
 
-    def separate(self, audio, length: int, chunk: int, step: int, batch: int, vocals):
-        _ok(lib().vh_separate(self.ctx.h, self.h, ptr(audio), length, chunk, step, batch, ptr(vocals)),
-            "vh_separate")
+    def separate(self, audio, length: int, chunk: int, step: int, batch: int, vocals, instrumental=None):
+        _ok(lib().vh_separate(self.ctx.h, self.h, ptr(audio), length, chunk, step, batch, ptr(vocals),
+                              ptr(instrumental) if instrumental is not None else None), "vh_separate")

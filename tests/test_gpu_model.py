@@ -125,12 +125,15 @@ def test_forward_config_shape(cfg2_models):
     om, dm = cfg2_models
     x = audio.sine_mix(0.5, 11)
     ref = om.forward(x)
-    dv = empty_dev(x.shape)
-    dm.forward(to_dev(x), x.shape[1], dv)
+    dv, di = empty_dev(x.shape), empty_dev(x.shape)
+    dm.forward(to_dev(x), x.shape[1], dv, di)
     out = from_dev(dv)
     err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    print(f"forward (dim 384, depth 2, 0.5 s): max|d| {err:.3e}, SNR {snr_db(ref, out):.1f} dB")
     assert err <= 1e-4, err
     assert snr_db(ref, out) >= 80
+    # instrumental = mix - vocals, computed on the device from the same vocals
+    assert np.array_equal(from_dev(di), x - out)
 
 
 def test_forward_reference_shape(ref_models):
@@ -141,6 +144,7 @@ def test_forward_reference_shape(ref_models):
     dm.forward(to_dev(x), x.shape[1], dv)
     out = from_dev(dv)
     err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    print(f"forward (reference shape, depth 16, 0.2 s): max|d| {err:.3e}, SNR {snr_db(ref, out):.1f} dB")
     assert err <= 1e-4, err
     assert snr_db(ref, out) >= 80
 
@@ -152,10 +156,12 @@ def test_chunked_separation(ctx):
     x = audio.sine_mix(1.0, 13)
     chunk, step = 13230, 8820  # 0.3 s windows every 0.2 s -> 5 chunks
     ref = om.separate_chunked(x, chunk, step)
-    dv = empty_dev(x.shape)
-    dm.separate(to_dev(x), x.shape[1], chunk, step, 2, dv)
+    dv, di = empty_dev(x.shape), empty_dev(x.shape)
+    dm.separate(to_dev(x), x.shape[1], chunk, step, 2, dv, di)
     out = from_dev(dv)
     assert O.chunk_count(x.shape[1], chunk, step) == 5
+    assert np.array_equal(from_dev(di), x - out)
     err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    print(f"chunked separation (5 windows, batch 2): max|d| {err:.3e}, SNR {snr_db(ref, out):.1f} dB")
     assert err <= 1e-4, err
     assert snr_db(ref, out) >= 80
