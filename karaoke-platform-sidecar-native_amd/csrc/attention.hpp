@@ -43,9 +43,9 @@ struct AttnArgs {
 };
 
 constexpr int ATT_DH = 64;
-constexpr int ATT_KB = 32;             // keys per block
-constexpr int ATT_KPITCH = ATT_DH + 4; // K tile row pitch
-constexpr int ATT_VPITCH = ATT_KB + 4; // V^T tile row pitch
+constexpr int ATT_KB = 32;             // keys per iteration
+constexpr int ATT_KPITCH = ATT_DH + 4; // K tile row pitch (floats)
+constexpr int ATT_VPITCH = ATT_KB + 4; // V^T tile row pitch (floats)
 
 VH_DEVICE int attn_row(const AttnArgs &a, int s, int p) {
     return (s / a.group) * a.group_stride + (s % a.group) * a.seq_stride + p * a.pos_stride;
@@ -64,11 +64,18 @@ VH_DEVICE floatx4 rope4(floatx4 v, const float *cs, const float *sn, int pos, in
     return r;
 }
 
+// Workgroup: WAVES wavefronts x 32 queries of one (sequence, head).  Each
+// iteration stages 32 keys (K rows and V transposed) in LDS, double
+// buffered (35 KB, so several workgroups share a CU).  Staging map: thread e
+// loads key e%16 (+16 for e >= 256) and 16-byte chunk (e/16)%16 of that key's
+// 64 dims, which makes both the K row writes and the V column writes
+// bank-conflict free.
 template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void attention_kernel(AttnArgs a) {
     constexpr int NT = 64 * WAVES;
-    constexpr int KV_F4 = ATT_KB * ATT_DH / 4;             // float4s per K (or V) tile
-    constexpr int PER_T = (KV_F4 + NT - 1) / NT;           // per thread
+    constexpr int KV_F4 = ATT_KB * ATT_DH / 4;   // float4s per K (or V) tile
+    constexpr int PER_T = KV_F4 / NT;            // per thread
+    static_assert(KV_F4 % NT == 0, "tile must divide evenly");
     __shared__ __attribute__((aligned(16))) float Ks[2][ATT_KB][ATT_KPITCH];
     __shared__ __attribute__((aligned(16))) float Vt[2][ATT_DH][ATT_VPITCH];
 
@@ -88,51 +95,50 @@ __global__ __launch_bounds__(64 * WAVES) void attention_kernel(AttnArgs a) {
     const int kcol = a.inner + h * ATT_DH;
     const int vcol = 2 * a.inner + h * ATT_DH;
 
-    // Q for query q0+li, dims 8g + 4lh .. +3, rotated and pre-scaled (the
-    // scale 1/8 is a power of two, so this is exact).
+    // Q for query q0+li, dims 8g + 4lh .. +3, rotated, then scaled by
+    // scale*log2(e) so the scores come out in the base-2 exponent domain.
     floatx4 qr[8];
     {
         const int q = min(q0 + li, a.L - 1);
         const float *qp = a.qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+        const float qs = a.scale * 1.4426950408889634f;
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             const int d0 = 8 * g + 4 * lh;
-            floatx4 v = rope4(ld4(qp + d0), a.rope_cos, a.rope_sin, q, d0);
-            qr[g] = v * a.scale;
+            qr[g] = rope4(ld4(qp + d0), a.rope_cos, a.rope_sin, q, d0) * qs;
         }
     }
 
     floatx4 kreg[PER_T], vreg[PER_T];
+    auto slot = [&](int i, int &kk, int &d0) {
+        const int e = tid + NT * i;
+        kk = (e & 15) + 16 * (e >> 8);  // key within the tile
+        d0 = 4 * ((e >> 4) & 15);       // first dim of the chunk
+    };
     auto load = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
-            const int e = tid + NT * i;
-            if (e < KV_F4) {
-                const int kk = e >> 4, d0 = 4 * (e & 15);
-                const int p = kb * ATT_KB + kk;
-                if (p < a.L) {
-                    const size_t row = (size_t)attn_row(a, s, p) * a.ld;
-                    kreg[i] = rope4(ld4(a.qkv + row + kcol + d0), a.rope_cos, a.rope_sin, p, d0);
-                    vreg[i] = ld4(a.qkv + row + vcol + d0);
-                } else {
-                    kreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-                    vreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-                }
+            int kk, d0;
+            slot(i, kk, d0);
+            const int p = kb * ATT_KB + kk;
+            if (p < a.L) {
+                const size_t row = (size_t)attn_row(a, s, p) * a.ld;
+                kreg[i] = rope4(ld4(a.qkv + row + kcol + d0), a.rope_cos, a.rope_sin, p, d0);
+                vreg[i] = ld4(a.qkv + row + vcol + d0);
+            } else {
+                kreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+                vreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
             }
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
-            const int e = tid + NT * i;
-            if (e < KV_F4) {
-                const int kk = e >> 4, d0 = 4 * (e & 15);
-                st4(&Ks[buf][kk][d0], kreg[i]);
-                Vt[buf][d0 + 0][kk] = vreg[i][0];
-                Vt[buf][d0 + 1][kk] = vreg[i][1];
-                Vt[buf][d0 + 2][kk] = vreg[i][2];
-                Vt[buf][d0 + 3][kk] = vreg[i][3];
-            }
+            int kk, d0;
+            slot(i, kk, d0);
+            st4(&Ks[buf][kk][d0], kreg[i]);
+#pragma unroll
+            for (int c = 0; c < 4; c++) Vt[buf][d0 + c][kk] = vreg[i][c];
         }
     };
 
@@ -156,41 +162,46 @@ __global__ __launch_bounds__(64 * WAVES) void attention_kernel(AttnArgs a) {
             for (int r = 0; r < 16; r++) sc[r] = 0.0f;
 #pragma unroll
             for (int g = 0; g < 8; g++) {
-                floatx4 kf = ld4(&Ks[buf][li][8 * g + 4 * lh]);
+                const floatx4 kf = ld4(&Ks[buf][li][8 * g + 4 * lh]);
 #pragma unroll
                 for (int r = 0; r < 4; r++) sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[r], qr[g][r], sc, 0, 0, 0);
             }
-            // sc[r]: score of key kb*32 + 8*(r/4) + 4*lh + r%4 for query q0+li
+            // sc[r]: score (log2 domain) of key kb*32 + 8*(r/4) + 4*lh + r%4 for
+            // query q0 + li.
             const int valid = a.L - kb * ATT_KB;
+            if (valid < ATT_KB) {
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
+            }
             float mb = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (key >= valid) sc[r] = -INFINITY;
-                mb = fmaxf(mb, sc[r]);
-            }
+            for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
             mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
             const float m_new = fmaxf(m_run, mb);
-            const float alpha = fast_exp_dev(m_run - m_new);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             float ls = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                sc[r] = fast_exp_dev(sc[r] - m_new);
+                sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_new);
                 ls += sc[r];
             }
             l_run = l_run * alpha + ls;
             m_run = m_new;
+            o[0] *= alpha;
+            o[1] *= alpha;
+            // O^T += V^T * P^T: step (qq, r) consumes keys 8qq + 4lh + r, which
+            // is register 4qq + r of the lane's own half.
 #pragma unroll
-            for (int t = 0; t < 2; t++) o[t] *= alpha;
+            for (int qq = 0; qq < 4; qq++) {
+                const floatx4 v0 = ld4(&Vt[buf][li][8 * qq + 4 * lh]);
+                const floatx4 v1 = ld4(&Vt[buf][32 + li][8 * qq + 4 * lh]);
 #pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int qq = 0; qq < 4; qq++) {
-                    floatx4 vf = ld4(&Vt[buf][32 * t + li][8 * qq + 4 * lh]);
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[r], sc[4 * qq + r], o[t], 0, 0, 0);
+                for (int r = 0; r < 4; r++) {
+                    o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[r], sc[4 * qq + r], o[0], 0, 0, 0);
+                    o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[r], sc[4 * qq + r], o[1], 0, 0, 0);
                 }
+            }
         }
         if (kb + 1 < nkb) store(buf ^ 1);
         __syncthreads();

@@ -8,11 +8,13 @@
 //
 // Tiling: 128x128 block tile, 4 wavefronts in a 2x2 grid, each owning a 64x64
 // sub-tile = 2x2 v_mfma_f32_32x32x2f32 accumulators (64 acc registers).  K is
-// staged through LDS in chunks of 32 with one register-staged prefetch
-// (double-buffered LDS, one barrier per chunk).  Operand reads are
-// ds_read_b128: lane (i, h) of a 32x32x2 MFMA feeds element k = 8g + 4h + r
-// at step (g, r), so one 16-byte read per operand serves four MFMAs.  The LDS
-// row pitch is 36 floats, which spreads the 32 rows of a read over all banks.
+// staged through LDS in chunks of 16 with one register-staged prefetch
+// (double-buffered LDS, one barrier per chunk); 40 KB of LDS per workgroup
+// lets four workgroups share a CU, so global-load latency of one is hidden
+// behind the matrix work of the others.  Operand reads are ds_read_b128:
+// lane (i, h) of a 32x32x2 MFMA feeds element k = 8g + 4h + r at step (g, r),
+// so one 16-byte read per operand serves four MFMAs.  The LDS row pitch of 20
+// floats puts the 16 rows of each read phase on disjoint banks.
 #pragma once
 
 #include "common.hpp"
@@ -28,7 +30,7 @@ struct GemmDesc {
     int lda, ldb, ldc;
 };
 
-constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_BK = 32, GEMM_PITCH = GEMM_BK + 4;
+constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_BK = 16, GEMM_PITCH = GEMM_BK + 4;
 constexpr int GEMM_THREADS = 256;
 // Descriptors of a ragged batch travel in the kernel arguments (<= 4 KiB).
 constexpr int GEMM_MAX_BATCH = 64;
@@ -52,25 +54,29 @@ __device__ __forceinline__ void gemm_f32_body(const GemmDesc &d, int tile) {
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 31, lh = lane >> 5;
 
-    // global -> register staging: thread covers rows (tid>>3) + 32q, k-quad tid&7
-    const int ld_row = tid >> 3, ld_c4 = tid & 7;
-    floatx4 ra[4], rb[4];
+    // global -> register staging: a k-chunk row holds GEMM_BK/4 float4s;
+    // thread covers rows ld_row + RSTEP*q and float4 ld_c4 of the chunk.
+    constexpr int C4 = GEMM_BK / 4;                  // float4s per tile row
+    constexpr int RSTEP = GEMM_THREADS / C4;         // rows covered per pass
+    constexpr int NQ = GEMM_BM / RSTEP;              // passes
+    const int ld_row = tid / C4, ld_c4 = tid % C4;
+    floatx4 ra[NQ], rb[NQ];
     auto load = [&](int k0) {
         const int kk = k0 + 4 * ld_c4;
         const bool kin = kk < d.K;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            int gm = min(m0 + ld_row + 32 * q, d.M - 1);
-            int gn = min(n0 + ld_row + 32 * q, d.N - 1);
+        for (int q = 0; q < NQ; q++) {
+            int gm = min(m0 + ld_row + RSTEP * q, d.M - 1);
+            int gn = min(n0 + ld_row + RSTEP * q, d.N - 1);
             ra[q] = kin ? ld4(d.A + (size_t)gm * d.lda + kk) : floatx4{0.f, 0.f, 0.f, 0.f};
             rb[q] = kin ? ld4(d.B + (size_t)gn * d.ldb + kk) : floatx4{0.f, 0.f, 0.f, 0.f};
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            st4(&As[buf][ld_row + 32 * q][4 * ld_c4], ra[q]);
-            st4(&Bs[buf][ld_row + 32 * q][4 * ld_c4], rb[q]);
+        for (int q = 0; q < NQ; q++) {
+            st4(&As[buf][ld_row + RSTEP * q][4 * ld_c4], ra[q]);
+            st4(&Bs[buf][ld_row + RSTEP * q][4 * ld_c4], rb[q]);
         }
     };
 
@@ -153,12 +159,12 @@ __device__ __forceinline__ void gemm_f32_body(const GemmDesc &d, int tile) {
 }
 
 template <int EPI>
-__global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_f32_kernel(GemmDesc d) {
+__global__ __launch_bounds__(GEMM_THREADS, 4) void gemm_f32_kernel(GemmDesc d) {
     gemm_f32_body<EPI>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
 template <int EPI>
-__global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_f32_batched_kernel(GemmBatch b) {
+__global__ __launch_bounds__(GEMM_THREADS, 4) void gemm_f32_batched_kernel(GemmBatch b) {
     gemm_f32_body<EPI>(b.d[blockIdx.z], (int)blockIdx.x);
 }
 

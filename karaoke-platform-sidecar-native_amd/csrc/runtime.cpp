@@ -203,19 +203,18 @@ bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *
 }
 
 bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int len, KernelTimer *t) {
-    if (len <= 0 || len > 64 * 32) {
-        set_error("softmax_rows: unsupported length %d", len);
+    if (len <= 0 || len > 4 * 64 * 16 - 4 || (((uintptr_t)in | (uintptr_t)out) & 15)) {
+        set_error("softmax_rows: unsupported length %d or unaligned buffers", len);
         return false;
     }
     Scope sc(t, s, "softmax");
     const unsigned grid = blocks_for(rows, 4);
-    const int per = (len + 63) / 64;
-    if (per <= 2) hipLaunchKernelGGL(softmax_rows_kernel<2>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else if (per <= 4) hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else if (per <= 8) hipLaunchKernelGGL(softmax_rows_kernel<8>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else if (per <= 13) hipLaunchKernelGGL(softmax_rows_kernel<13>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else if (per <= 16) hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else hipLaunchKernelGGL(softmax_rows_kernel<32>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    const int chunks = (len + 3) / 4 + 1;  // a row covers at most this many float4 chunks
+    if (chunks <= 64) hipLaunchKernelGGL(softmax_rows_kernel<1>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else if (chunks <= 128) hipLaunchKernelGGL(softmax_rows_kernel<2>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else if (chunks <= 256) hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else if (chunks <= 512) hipLaunchKernelGGL(softmax_rows_kernel<8>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    else hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
     return sync_debug(s, "softmax_rows_kernel");
 }
 

@@ -58,9 +58,9 @@ def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | N
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--only", default="", help="comma list of groups: c1,c2,c3")
+    ap.add_argument("--only", default="", help="comma list of groups: c1,c2,c3,gemm,attn")
     args = ap.parse_args()
-    groups = set(args.only.split(",")) if args.only else {"c1", "c2", "c3"}
+    groups = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "gemm", "attn"}
 
     import torch
 
@@ -74,6 +74,13 @@ def main() -> int:
     reps = args.reps
 
     if "c1" in groups:
+        # practical ceiling of a 1:1 read/write stream: a plain device copy
+        # (torch's copy kernel) of the softmax tensor's size
+        cs = torch.randn(496 * 801 * 801, device=dev, generator=g)
+        cd = torch.empty_like(cs)
+        _emit("copy_reference", _event_time(lambda: cd.copy_(cs), reps), gbytes=2 * cs.numel() * 4 / 1e9,
+              shape="1.27 GB -> 1.27 GB")
+        del cs, cd
         rows, dim = 49662, 384
         x = torch.randn(rows, dim, device=dev, generator=g)
         gamma = 1 + 0.02 * torch.randn(dim, device=dev, generator=g)
@@ -98,6 +105,29 @@ def main() -> int:
         _emit("residual_add", _event_time(lambda: ctx.residual_add(x, r, rows * dim), reps),
               gbytes=3 * rows * dim * 4 / 1e9, shape="[49662,384]")
         del x, y, r
+
+    if "gemm" in groups:
+        # the transformer GEMMs of one 8-window pass (M = 8 * 801 * 62 tokens)
+        M = 8 * 801 * 62
+        for name, K, N, epi, ocols in (("gemm_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
+                                       ("gemm_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
+                                       ("gemm_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
+                                       ("gemm_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384)):
+            a = torch.randn(M, K, device=dev, generator=g)
+            w = 0.05 * torch.randn(N, K, device=dev, generator=g)
+            b = torch.randn(N, device=dev, generator=g)
+            c = torch.zeros(M, ocols, device=dev)
+            _emit(name, _event_time(lambda: ctx.gemm(a, w, c, M, N, K, bias=b, epilogue=epi), max(3, reps // 4)),
+                  gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}")
+            del a, w, b, c
+
+    if "attn" in groups:
+        for S, L in ((8 * 62, 801), (8 * 801, 62)):
+            qkv = torch.randn(S * L, 3 * 512, device=dev, generator=g)
+            o = torch.empty(S * L, 512, device=dev)
+            _emit("attention", _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True), max(3, reps // 4)),
+                  gflop=4.0 * S * 8 * L * L * 64 / 1e9, shape=f"S={S} L={L} H=8")
+            del qkv, o
 
     if "c2" in groups or "c3" in groups:
         d = CONFIG_DIMS.with_depth(1)
