@@ -32,6 +32,8 @@ struct GemmDesc {
 
 constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_BK = 16, GEMM_PITCH = GEMM_BK + 4;
 constexpr int GEMM_THREADS = 256;
+constexpr int GEMM_GROUP_M = 16;
+constexpr size_t GEMM_L2_RESIDENT_BYTES = 3u << 20;
 // Descriptors of a ragged batch travel in the kernel arguments (<= 4 KiB).
 constexpr int GEMM_MAX_BATCH = 64;
 struct GemmBatch {
@@ -46,8 +48,20 @@ __device__ __forceinline__ void gemm_f32_body(const GemmDesc &d, int tile) {
     const int tiles_n = (d.N + GEMM_BN - 1) / GEMM_BN;
     const int tiles_m = (d.M + GEMM_BM - 1) / GEMM_BM;
     if (tile >= tiles_m * tiles_n) return;
-    const int m0 = (tile / tiles_n) * GEMM_BM;
-    const int n0 = (tile % tiles_n) * GEMM_BN;
+    // Grouped order: GEMM_GROUP_M row tiles x all column tiles, row fastest.
+    // Consecutive workgroups share one weight tile (read once into L2 for
+    // GEMM_GROUP_M of them) while the group's activation rows stay resident;
+    // with column-fastest order a K=384 fp32 weight matrix wider than ~2000
+    // rows no longer fits an XCD's 4 MB L2 and is re-fetched per row tile.
+    // A weight matrix that fits comfortably in L2 is kept resident by plain
+    // column-fastest order (group of one row tile), which reads each
+    // activation row tile exactly once.
+    const int gsz = (size_t)d.N * d.K * sizeof(float) <= GEMM_L2_RESIDENT_BYTES ? 1 : GEMM_GROUP_M;
+    const int group = tile / (gsz * tiles_n);
+    const int in_group = tile % (gsz * tiles_n);
+    const int group_rows = min(gsz, tiles_m - group * gsz);
+    const int m0 = (group * gsz + in_group % group_rows) * GEMM_BM;
+    const int n0 = (in_group / group_rows) * GEMM_BN;
 
     const int tid = (int)threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
