@@ -93,6 +93,19 @@ def cpu_baseline(d, blob, x, chunk: int, step: int, threads: int) -> dict:
     }
 
 
+def measured_traffic() -> tuple[int | None, str | None]:
+    """HBM bytes per launch of the dominant kernel, from the committed
+    calibrated rocprofv3 counter summary (FETCH_SIZE/WRITE_SIZE scaled by a
+    plain copy); None if that summary is absent."""
+    path = ROOT / "profiles" / "gemm-ff1-geglu_traffic.md"
+    if not path.exists():
+        return None, None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1]), str(path.relative_to(ROOT))
+    return None, None
+
+
 def _final_gamma(d, blob):
     from vocalarc_hip import pack
     return pack.tensor_views(d, blob)["final_gamma"]
@@ -154,6 +167,7 @@ def main() -> int:
 
     flops = ff1_flops_per_step(d, chunk, step, length, BATCH) * args.steps
     achieved = flops / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+    traffic, traffic_src = measured_traffic()
     roofline = {
         "kernel": "gemm_f32_kernel<GELU-GLU> (FFN up-projection, M=397296 K=384 N=3072 per 8-window pass)",
         "bound": "mfma",
@@ -161,7 +175,9 @@ def main() -> int:
         "peak": MFMA_FP32_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_unit": "bytes per full 8-window launch (beyond L2; algorithmic 3.056e9)",
+        "traffic_source": traffic_src,
         "launches": launches,
         "avg_launch_ms": round(ms / max(launches, 1), 4),
     }

@@ -58,9 +58,9 @@ def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | N
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--only", default="", help="comma list of groups: c1,c2,c3,gemm,attn")
+    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,attn")
     args = ap.parse_args()
-    groups = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "gemm", "attn"}
+    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "attn"}
 
     import torch
 
@@ -73,14 +73,17 @@ def main() -> int:
     ctx = native.Context()
     reps = args.reps
 
-    if "c1" in groups:
-        # practical ceiling of a 1:1 read/write stream: a plain device copy
-        # (torch's copy kernel) of the softmax tensor's size
+    if "copy" in groups:
+        # practical ceiling of a 1:1 read/write stream, and the calibration
+        # kernel for the FETCH_SIZE / WRITE_SIZE counters: a plain device copy
+        # (torch's copy kernel) of 1.27 GB
         cs = torch.randn(496 * 801 * 801, device=dev, generator=g)
         cd = torch.empty_like(cs)
         _emit("copy_reference", _event_time(lambda: cd.copy_(cs), reps), gbytes=2 * cs.numel() * 4 / 1e9,
               shape="1.27 GB -> 1.27 GB")
         del cs, cd
+
+    if "c1" in groups:
         rows, dim = 49662, 384
         x = torch.randn(rows, dim, device=dev, generator=g)
         gamma = 1 + 0.02 * torch.randn(dim, device=dev, generator=g)
@@ -106,13 +109,16 @@ def main() -> int:
               gbytes=3 * rows * dim * 4 / 1e9, shape="[49662,384]")
         del x, y, r
 
-    if "gemm" in groups:
+    if "gemm" in groups or "ff1" in groups:
         # the transformer GEMMs of one 8-window pass (M = 8 * 801 * 62 tokens)
         M = 8 * 801 * 62
-        for name, K, N, epi, ocols in (("gemm_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
-                                       ("gemm_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
-                                       ("gemm_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
-                                       ("gemm_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384)):
+        shapes = (("gemm_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
+                  ("gemm_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
+                  ("gemm_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
+                  ("gemm_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384))
+        if "gemm" not in groups:
+            shapes = shapes[2:3]
+        for name, K, N, epi, ocols in shapes:
             a = torch.randn(M, K, device=dev, generator=g)
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
             b = torch.randn(N, device=dev, generator=g)
