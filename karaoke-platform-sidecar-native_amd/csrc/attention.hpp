@@ -71,7 +71,7 @@ VH_DEVICE floatx4 rope4(floatx4 v, const float *cs, const float *sn, int pos, in
 // 64 dims, which makes both the K row writes and the V column writes
 // bank-conflict free.
 template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     constexpr int NT = 64 * WAVES;
     constexpr int KV_F4 = ATT_KB * ATT_DH / 4;   // float4s per K (or V) tile
     constexpr int PER_T = KV_F4 / NT;            // per thread
