@@ -6,7 +6,10 @@ partials per channel + white noise) with a random-init BS-RoFormer of dim 384,
 depth 12, 62 bands, 8 heads x 64, GELU-GLU FFN (mult 4), hop 441, n_fft 2048:
 8 s windows with 2 s overlap (50 windows), 8 windows per device pass, linear
 cross-fade.  The input waveform is resident in HBM when the timed region
-starts; the output waveform is in HBM when it ends.  fp32 throughout.
+starts; the output waveform is in HBM when it ends.  fp32 throughout for
+`value`; the bf16-MFMA variant of the same job (bf16 operands at the matrix
+cores, fp32 accumulation and everything else fp32) is timed after it and
+reported separately under "bf16_variant" with its SNR against the fp32 output.
 
 value = audio seconds separated per wall second (realtime factor).
 roofline: the dominant kernel (the FFN up-projection GEMM with the GELU-GLU
@@ -35,6 +38,7 @@ SECONDS = 300.0
 CHUNK_S, STEP_S, BATCH = 8.0, 6.0, 8
 RATE = 44_100
 MFMA_FP32_PEAK_TFLOPS = 157.3
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBS = 8000.0
 DOMINANT = "gemm_ff1"
 
@@ -106,6 +110,47 @@ def measured_traffic() -> tuple[int | None, str | None]:
     return None, None
 
 
+def bf16_variant(ctx, model, dx, dv, ref_out, length, chunk, step, args, d) -> dict:
+    """The same job with bf16 matrix-core operands; SNR against the fp32 output."""
+    import numpy as np
+    import torch
+
+    from vocalarc_hip import native
+
+    model.set_precision(native.PRECISION_BF16)
+    for i in range(args.warmup):
+        model.separate(dx, length, chunk, step, BATCH, dv)
+        ctx.sync()
+    ctx.timing(DOMINANT)
+    ctx.timing_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        model.separate(dx, length, chunk, step, BATCH, dv)
+    ctx.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ctx.timing(None)
+    ms, launches = ctx.timing_get(DOMINANT)
+    model.set_precision(native.PRECISION_FP32)
+    log(f"bf16 variant: timed {args.steps} steps: {wall:.3f} s")
+    out = dv.cpu().numpy().astype(np.float64)
+    ref = ref_out.astype(np.float64)
+    snr = 10 * np.log10(np.sum(ref * ref) / max(np.sum((out - ref) ** 2), 1e-300))
+    tf = ff1_flops_per_step(d, chunk, step, length, BATCH) * args.steps / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+    return {
+        "value": round(length / RATE * args.steps / wall, 3),
+        "unit": "audio s / wall s",
+        "ms_per_step": round(wall / args.steps * 1e3, 2),
+        "dtype": "bf16 MFMA operands, fp32 accumulation",
+        "snr_db_vs_fp32": round(float(snr), 2),
+        "dominant_kernel": {"kernel": "gemm_bf16_kernel<GELU-GLU>", "achieved": round(tf, 2),
+                            "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                            "avg_launch_ms": round(ms / max(launches, 1), 4)},
+    }
+
+
 def _final_gamma(d, blob):
     from vocalarc_hip import pack
     return pack.tensor_views(d, blob)["final_gamma"]
@@ -118,6 +163,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--seconds", type=float, default=SECONDS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-MFMA variant")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs the separation path on a single GPU "
@@ -182,6 +228,10 @@ def main() -> int:
         "avg_launch_ms": round(ms / max(launches, 1), 4),
     }
 
+    bf16 = None
+    if not args.no_bf16:
+        bf16 = bf16_variant(ctx, model, dx, dv, out, length, chunk, step, args, d)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
@@ -210,6 +260,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "bf16_variant": bf16,
     }
     print(json.dumps(line), flush=True)
     model.close()

@@ -67,6 +67,14 @@ int vh_residual_add(vh_context *ctx, int64_t n, float *x, const float *r);
    2 tanh, 3 residual (C +=), 4 GELU-GLU on interleaved columns. */
 int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const float *W, int ldw,
             const float *bias, float *C, int ldc, int epilogue);
+/* bf16-MFMA variant of vh_gemm: A fp32 rounded to bf16 (round to nearest
+   even) as it is staged, Wh a bf16 weight copy [N][ldw] (ldw a multiple of 8,
+   >= K, zero padded), fp32 accumulation and epilogue.  K and lda multiples of
+   4, A and Wh 16-byte aligned. */
+int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Wh, int ldw,
+                 const float *bias, float *C, int ldc, int epilogue);
+/* fp32 src[rows][cols] -> bf16 dst[rows][ld] (round to nearest even). */
+int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld);
 /* Fused attention core over qkv[S*L][3*H*64] (rotary applied here):
    native/vocalarc_separation.c:692-793.  out[S*L][H*64]. */
 int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, float *out,
@@ -77,6 +85,15 @@ int vh_attention(vh_context *ctx, int sequences, int length, int heads, const fl
    `dims` from host memory.  Returns NULL on a malformed pack. */
 vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const void *pack, size_t bytes);
 void vh_model_free(vh_model *model);
+/* Arithmetic of the model's matrix products (every linear of the transformer
+   stack, band split and mask estimator): VH_PRECISION_FP32 (default; fp32
+   MFMA, the parity path) or VH_PRECISION_BF16 (activations rounded to bf16
+   as they enter the matrix cores, bf16 weight copies made on the first
+   switch, fp32 accumulation, normalisation, softmax and DSP).  The reference
+   CUDA provider's counterpart is its TF32 switch (native/native_gpu_cuda.cu:566-570). */
+#define VH_PRECISION_FP32 0
+#define VH_PRECISION_BF16 1
+int vh_model_set_precision(vh_model *model, int precision);
 /* One axial transformer (native/vocalarc_separation.c:836-873) in place on
    device x[S][L][dim]; axis 0 = time weights, 1 = band weights. */
 int vh_transformer(vh_context *ctx, vh_model *model, int layer, int axis, float *x, int sequences, int length);

@@ -12,6 +12,7 @@
 #include "attention.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
+#include "gemm_bf16.hpp"
 
 namespace vh {
 
@@ -112,9 +113,12 @@ void KernelTimer::reset() {
 // --------------------------------------------------------------- launchers
 static inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
 
+// Output columns a GEMM writes per row (GELU-GLU halves them).
+static int out_cols(int N, int epilogue) { return epilogue == EPI_GEGLU ? N / 2 : N; }
+
 static bool gemm_ok(const GemmArgs &g) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0) return false;
-    if (g.K % 4 || g.lda % 4 || g.ldb % 4) return false;
+    if (g.K % 4 || g.lda % 4 || g.ldb % 4 || g.lda < g.K || g.ldb < g.K) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.B) & 15) return false;
     if (g.M > INT32_MAX / 2) return false;
     return true;
@@ -152,7 +156,7 @@ static int64_t tiles_of(const GemmArgs &g) {
 }
 
 bool gemm(hipStream_t s, const GemmArgs &g, int epilogue, KernelTimer *t, const char *name) {
-    if (!gemm_ok(g)) {
+    if (!gemm_ok(g) || g.ldc < out_cols(g.N, epilogue)) {
         set_error("gemm: unsupported shape M=%lld N=%d K=%d lda=%d ldb=%d", (long long)g.M, g.N, g.K, g.lda, g.ldb);
         return false;
     }
@@ -174,7 +178,7 @@ bool gemm_batched(hipStream_t s, const std::vector<GemmArgs> &gs, int epilogue, 
         int64_t max_tiles = 0;
         for (size_t i = 0; i < count; i++) {
             const GemmArgs &g = gs[first + i];
-            if (!gemm_ok(g) || (epilogue == EPI_GEGLU && g.N % 64)) {
+            if (!gemm_ok(g) || g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) {
                 set_error("gemm_batched: unsupported shape M=%lld N=%d K=%d", (long long)g.M, g.N, g.K);
                 return false;
             }
@@ -184,6 +188,87 @@ bool gemm_batched(hipStream_t s, const std::vector<GemmArgs> &gs, int epilogue, 
         if (!launch_gemm(s, epilogue, nullptr, &b, (unsigned)max_tiles, (unsigned)count)) return false;
     }
     return true;
+}
+
+// ------------------------------------------------------------ bf16 GEMM
+static bool gemm_bf16_ok(const GemmArgsBF16 &g, int epilogue) {
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2) return false;
+    if (g.K % 4 || g.lda % 4 || g.lda < g.K || g.ldb % 8 || g.ldb < bf16_pitch(g.K)) return false;
+    if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
+    if (((uintptr_t)g.A | (uintptr_t)g.B) & 15) return false;
+    return true;
+}
+
+static GemmDescBF16 to_desc_bf16(const GemmArgsBF16 &g) {
+    GemmDescBF16 d;
+    d.A = g.A; d.B = static_cast<const bf16 *>(g.B); d.bias = g.bias; d.C = g.C;
+    d.M = (int)g.M; d.N = g.N; d.K = g.K;
+    d.lda = g.lda; d.ldb = g.ldb; d.ldc = g.ldc;
+    return d;
+}
+
+static int64_t tiles_bf16(const GemmArgsBF16 &g) {
+    return ((g.M + GB_BM - 1) / GB_BM) * ((g.N + GB_BN - 1) / GB_BN);
+}
+
+template <int EPI>
+static void launch_bf16_epi(hipStream_t s, const GemmDescBF16 *single, const GemmBatchBF16 *batch, unsigned tiles,
+                            unsigned n) {
+    if (single) hipLaunchKernelGGL(gemm_bf16_kernel<EPI>, dim3(tiles), dim3(GB_THREADS), 0, s, *single);
+    else hipLaunchKernelGGL(gemm_bf16_batched_kernel<EPI>, dim3(tiles, 1, n), dim3(GB_THREADS), 0, s, *batch);
+}
+
+static bool launch_bf16(hipStream_t s, int epi, const GemmDescBF16 *single, const GemmBatchBF16 *batch,
+                        unsigned tiles, unsigned n) {
+    switch (epi) {
+        case EPI_STORE: launch_bf16_epi<EPI_STORE>(s, single, batch, tiles, n); break;
+        case EPI_GELU: launch_bf16_epi<EPI_GELU>(s, single, batch, tiles, n); break;
+        case EPI_TANH: launch_bf16_epi<EPI_TANH>(s, single, batch, tiles, n); break;
+        case EPI_RESIDUAL: launch_bf16_epi<EPI_RESIDUAL>(s, single, batch, tiles, n); break;
+        case EPI_GEGLU: launch_bf16_epi<EPI_GEGLU>(s, single, batch, tiles, n); break;
+        default: set_error("unknown GEMM epilogue %d", epi); return false;
+    }
+    return sync_debug(s, "gemm_bf16_kernel");
+}
+
+bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *t, const char *name) {
+    if (!gemm_bf16_ok(g, epilogue)) {
+        set_error("gemm_bf16: unsupported shape M=%lld N=%d K=%d lda=%d ldb=%d", (long long)g.M, g.N, g.K, g.lda,
+                  g.ldb);
+        return false;
+    }
+    GemmDescBF16 d = to_desc_bf16(g);
+    Scope sc(t, s, name);
+    return launch_bf16(s, epilogue, &d, nullptr, (unsigned)tiles_bf16(g), 1);
+}
+
+bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &gs, int epilogue, KernelTimer *t,
+                       const char *name) {
+    Scope sc(t, s, name);
+    for (size_t first = 0; first < gs.size(); first += GB_MAX_BATCH) {
+        const size_t count = std::min(gs.size() - first, (size_t)GB_MAX_BATCH);
+        GemmBatchBF16 b;
+        memset(&b, 0, sizeof(b));
+        int64_t max_tiles = 0;
+        for (size_t i = 0; i < count; i++) {
+            const GemmArgsBF16 &g = gs[first + i];
+            if (!gemm_bf16_ok(g, epilogue)) {
+                set_error("gemm_bf16_batched: unsupported shape M=%lld N=%d K=%d", (long long)g.M, g.N, g.K);
+                return false;
+            }
+            b.d[i] = to_desc_bf16(g);
+            max_tiles = std::max(max_tiles, tiles_bf16(g));
+        }
+        if (!launch_bf16(s, epilogue, nullptr, &b, (unsigned)max_tiles, (unsigned)count)) return false;
+    }
+    return true;
+}
+
+bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst, int ld) {
+    const int64_t n = (int64_t)rows * cols;
+    hipLaunchKernelGGL(to_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, src, static_cast<bf16 *>(dst),
+                       (int64_t)rows, cols, ld);
+    return sync_debug(s, "to_bf16_kernel");
 }
 
 bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
@@ -364,26 +449,35 @@ bool BlockScratch::ensure(const Dims &d, int64_t tokens) {
 }
 
 bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, float *x, int64_t tokens,
-                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t) {
+                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t, int precision) {
     if (!scr.ensure(d, tokens)) return false;
     const float *cs = nullptr, *sn = nullptr;
     if (!rope.get(lay.L, d.dim_head, s, &cs, &sn)) return false;
     const int D = d.dim, inner = d.inner(), nq = d.qkvg_dim();
     float *normed = scr.normed.f(), *qkvg = scr.qkvg.f(), *attn = scr.attn.f(), *hid = scr.hidden.f();
     // pre-norm -> fused QKV (+gate logits with their bias)
+    const bool h = precision == PREC_BF16;
+    if (h && !(w.wqkvg_h && w.wout_h && w.w1_h && w.w2_h)) {
+        set_error("transformer: bf16 weights not prepared");
+        return false;
+    }
+    auto linear = [&](const float *A, int lda, const float *W, const void *Wh, const float *bias, float *C, int ldc,
+                      int N, int K, int epi, const char *name) {
+        if (h) return gemm_bf16(s, {A, lda, Wh, bf16_pitch(K), bias, C, ldc, tokens, N, K}, epi, t, name);
+        return gemm(s, {A, lda, W, K, bias, C, ldc, tokens, N, K}, epi, t, name);
+    };
     if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
-    if (!gemm(s, {normed, D, w.wqkvg, D, w.bqkvg, qkvg, nq, tokens, nq, D}, EPI_STORE, t, "gemm_qkv")) return false;
+    if (!linear(normed, D, w.wqkvg, w.wqkvg_h, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
     // rotary + attention + gates
     if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, d.gated ? d.qkv_dim() : -1, t)) return false;
     // out projection added to the residual stream
-    if (!gemm(s, {attn, inner, w.wout, inner, nullptr, x, D, tokens, D, inner}, EPI_RESIDUAL, t, "gemm_out")) return false;
+    if (!linear(attn, inner, w.wout, w.wout_h, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;
     // FFN
     if (!rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
-    if (!gemm(s, {normed, D, w.w1, D, w.b1, hid, d.ff_dim, tokens, d.ff1_out(), D}, d.ffn_glu ? EPI_GEGLU : EPI_GELU, t,
-              "gemm_ff1"))
+    if (!linear(normed, D, w.w1, w.w1_h, w.b1, hid, d.ff_dim, d.ff1_out(), D, d.ffn_glu ? EPI_GEGLU : EPI_GELU,
+                "gemm_ff1"))
         return false;
-    if (!gemm(s, {hid, d.ff_dim, w.w2, d.ff_dim, w.b2, x, D, tokens, D, d.ff_dim}, EPI_RESIDUAL, t, "gemm_ff2"))
-        return false;
+    if (!linear(hid, d.ff_dim, w.w2, w.w2_h, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, "gemm_ff2")) return false;
     return true;
 }
 

@@ -90,6 +90,23 @@ bool gemm(hipStream_t s, const GemmArgs &g, int epilogue, KernelTimer *t = nullp
 bool gemm_batched(hipStream_t s, const std::vector<GemmArgs> &g, int epilogue, KernelTimer *t = nullptr,
                   const char *name = "gemm_batched");
 
+// bf16-MFMA variant: A fp32 (rounded to bf16 on the way into LDS), B a bf16
+// weight copy with row pitch ldb >= K rounded up to 8 and zero padding.
+struct GemmArgsBF16 {
+    const float *A; int lda;
+    const void *B; int ldb;  // bf16 [N][ldb]
+    const float *bias;
+    float *C; int ldc;
+    int64_t M; int N, K;
+};
+bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *t = nullptr,
+               const char *name = "gemm_bf16");
+bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &g, int epilogue, KernelTimer *t = nullptr,
+                       const char *name = "gemm_bf16_batched");
+// fp32 [rows][cols] -> bf16 [rows][ld] (ld >= cols, padding zeroed by the caller)
+bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst, int ld);
+inline int bf16_pitch(int k) { return (k + 7) & ~7; }
+
 bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
              KernelTimer *t = nullptr);
 bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int len, KernelTimer *t = nullptr);
@@ -132,7 +149,13 @@ struct LayerWeights {
     float *wout = nullptr;                     // [D][inner]
     float *w1 = nullptr, *b1 = nullptr;        // [ff1_out][D] (value/gate interleaved for GLU)
     float *w2 = nullptr, *b2 = nullptr;        // [D][ff_dim]
+    // bf16 copies for the reduced-precision variant (null: fp32 only)
+    void *wqkvg_h = nullptr, *wout_h = nullptr, *w1_h = nullptr, *w2_h = nullptr;
 };
+
+// Arithmetic of the matrix products: fp32 MFMA (parity path) or bf16 MFMA
+// with fp32 accumulation (separately reported variant).
+enum Precision : int { PREC_FP32 = 0, PREC_BF16 = 1 };
 
 // Rotary cos/sin tables per sequence length, built on the host with the
 // reference's float expressions (native/vocalarc_separation.c:726-731,1312).
@@ -153,7 +176,8 @@ struct BlockScratch {
 // (native/vocalarc_separation.c:836-873).  Rows of x are tokens; `lay` maps
 // (sequence, position) to rows.
 bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, float *x, int64_t tokens,
-                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t = nullptr);
+                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t = nullptr,
+                       int precision = PREC_FP32);
 
 // Host packed weight (reference layout) -> device [out][in] rows, through a
 // staging buffer.  mode as unpack_weight.

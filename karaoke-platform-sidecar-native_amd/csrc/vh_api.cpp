@@ -44,6 +44,10 @@ struct vh_model {
     float *final_gamma = nullptr;
     std::vector<float *> mask_w1, mask_b1, mask_w2, mask_b2;
     std::vector<int> first_freq;
+    // bf16 copies of every matrix (built on the first switch to bf16)
+    int precision = PREC_FP32;
+    DeviceBuffer weights_h;
+    std::vector<void *> band_w_h, mask_w1_h, mask_w2_h;
     // DSP constants
     DeviceBuffer window, twiddle;
     // pipeline scratch (grown on demand)
@@ -127,6 +131,17 @@ extern "C" int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A,
                        const float *bias, float *C, int ldc, int epilogue) {
     if (!ctx) return 0;
     return gemm(ctx->stream, {A, lda, W, ldw, bias, C, ldc, M, N, K}, epilogue, &ctx->timer, "gemm") ? 1 : 0;
+}
+
+extern "C" int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Wh, int ldw,
+                            const float *bias, float *C, int ldc, int epilogue) {
+    if (!ctx) return 0;
+    return gemm_bf16(ctx->stream, {A, lda, Wh, ldw, bias, C, ldc, M, N, K}, epilogue, &ctx->timer, "gemm_bf16") ? 1 : 0;
+}
+
+extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld) {
+    if (!ctx || rows <= 0 || cols <= 0 || ld < cols || rows * (int64_t)cols > INT32_MAX) return 0;
+    return to_bf16_rows(ctx->stream, src, (int)rows, cols, dst, ld) ? 1 : 0;
 }
 
 extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, float *out,
@@ -319,6 +334,56 @@ bool upload_pack(vh_model *m, const void *pack, size_t bytes) {
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(model upload)");
 }
 
+// bf16 copies of all matrices, rows padded to a multiple of 8 with zeros.
+bool prepare_bf16(vh_model *m) {
+    if (m->weights_h.ptr) return true;
+    const Dims &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int D = d.dim, Hm = d.mask_hidden;
+    auto bytes = [](int64_t rows, int cols) { return ((size_t)rows * bf16_pitch(cols) * 2 + 255) & ~(size_t)255; };
+    size_t total = 0;
+    const size_t per_layer = bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) + bytes(D, d.ff_dim);
+    total += per_layer * m->layers.size();
+    for (int b = 0; b < d.bands; b++)
+        total += bytes(D, d.in_dim(b)) + bytes(Hm, D) + bytes(2 * d.in_dim(b), Hm);
+    if (!m->weights_h.ensure(total, "hipMalloc(bf16 weights)")) return false;
+    if (!check(hipMemsetAsync(m->weights_h.ptr, 0, total, s), "hipMemset(bf16 weights)")) return false;
+    char *cur = static_cast<char *>(m->weights_h.ptr);
+    auto conv = [&](const float *src, int rows, int cols, void **dst) {
+        *dst = cur;
+        cur += bytes(rows, cols);
+        return to_bf16_rows(s, src, rows, cols, *dst, bf16_pitch(cols));
+    };
+    for (LayerWeights &w : m->layers) {
+        if (!conv(w.wqkvg, d.qkvg_dim(), D, &w.wqkvg_h) || !conv(w.wout, D, d.inner(), &w.wout_h) ||
+            !conv(w.w1, d.ff1_out(), D, &w.w1_h) || !conv(w.w2, D, d.ff_dim, &w.w2_h))
+            return false;
+    }
+    m->band_w_h.assign(d.bands, nullptr);
+    m->mask_w1_h.assign(d.bands, nullptr);
+    m->mask_w2_h.assign(d.bands, nullptr);
+    for (int b = 0; b < d.bands; b++) {
+        const int in = d.in_dim(b);
+        if (!conv(m->band_w[b], D, in, &m->band_w_h[b]) || !conv(m->mask_w1[b], Hm, D, &m->mask_w1_h[b]) ||
+            !conv(m->mask_w2[b], 2 * in, Hm, &m->mask_w2_h[b]))
+            return false;
+    }
+    return check(hipStreamSynchronize(s), "hipStreamSynchronize(bf16 weights)");
+}
+
+// Batched token-wise linears of one pipeline stage in the model's precision.
+bool stage_gemms(vh_model *m, const std::vector<GemmArgs> &gs, const std::vector<void *> &wh, int epi,
+                 const char *name) {
+    if (m->precision != PREC_BF16) return gemm_batched(m->ctx->stream, gs, epi, &m->ctx->timer, name);
+    std::vector<GemmArgsBF16> hs;
+    hs.reserve(gs.size());
+    for (size_t i = 0; i < gs.size(); i++) {
+        const GemmArgs &g = gs[i];
+        hs.push_back({g.A, g.lda, wh[i], bf16_pitch(g.K), g.bias, g.C, g.ldc, g.M, g.N, g.K});
+    }
+    return gemm_bf16_batched(m->ctx->stream, hs, epi, &m->ctx->timer, name);
+}
+
 // ---- pipeline stages on `chunks` windows at once --------------------------
 
 int log2i(int n) {
@@ -372,7 +437,7 @@ bool stage_band_split(vh_model *m, const float *source, int chunks, int T, float
     }
     // The table must stay intact until the gather has read it.
     if (!check(hipStreamSynchronize(s), "hipStreamSynchronize(band table)")) return false;
-    return gemm_batched(s, gs, EPI_STORE, &m->ctx->timer, "gemm_band_split");
+    return stage_gemms(m, gs, m->band_w_h, EPI_STORE, "gemm_band_split");
 }
 
 // final-normed features (frame-major rows m*B + b) -> mask[chunks][F][C][T][2]
@@ -398,8 +463,8 @@ bool stage_mask(vh_model *m, const float *normed, int chunks, int T, float *mask
         tab.proj_offset[b] = off;
         off += (int64_t)M * out;
     }
-    if (!gemm_batched(s, g1, EPI_TANH, &m->ctx->timer, "gemm_mask1")) return false;
-    if (!gemm_batched(s, g2, EPI_STORE, &m->ctx->timer, "gemm_mask2")) return false;
+    if (!stage_gemms(m, g1, m->mask_w1_h, EPI_TANH, "gemm_mask1")) return false;
+    if (!stage_gemms(m, g2, m->mask_w2_h, EPI_STORE, "gemm_mask2")) return false;
     MaskTable *dtab = reinterpret_cast<MaskTable *>(static_cast<char *>(m->tables.ptr) + sizeof(BandTable));
     if (!check(hipMemcpyAsync(dtab, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(mask table)")) return false;
     int maxdim = 0;
@@ -440,10 +505,10 @@ bool stage_stack(vh_model *m, float *x, int chunks, int T) {
     vh_context *ctx = m->ctx;
     for (int l = 0; l < d.depth; l++) {
         if (!transformer_block(ctx->stream, d, m->layers[2 * l], x, tokens, time_axis_layout(chunks, T, d.bands),
-                               ctx->scratch, ctx->rope, &ctx->timer))
+                               ctx->scratch, ctx->rope, &ctx->timer, m->precision))
             return false;
         if (!transformer_block(ctx->stream, d, m->layers[2 * l + 1], x, tokens, band_axis_layout(chunks, T, d.bands),
-                               ctx->scratch, ctx->rope, &ctx->timer))
+                               ctx->scratch, ctx->rope, &ctx->timer, m->precision))
             return false;
     }
     return true;
@@ -491,6 +556,16 @@ extern "C" vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const v
     return m;
 }
 
+extern "C" int vh_model_set_precision(vh_model *m, int precision) {
+    if (!m || (precision != VH_PRECISION_FP32 && precision != VH_PRECISION_BF16)) {
+        set_error("vh_model_set_precision: unknown precision %d", precision);
+        return 0;
+    }
+    if (precision == VH_PRECISION_BF16 && !prepare_bf16(m)) return 0;
+    m->precision = precision == VH_PRECISION_BF16 ? PREC_BF16 : PREC_FP32;
+    return 1;
+}
+
 extern "C" void vh_model_free(vh_model *m) {
     if (!m) return;
     (void)hipStreamSynchronize(m->ctx->stream);
@@ -500,7 +575,7 @@ extern "C" void vh_model_free(vh_model *m) {
 extern "C" int vh_transformer(vh_context *ctx, vh_model *m, int layer, int axis, float *x, int S, int L) {
     if (!ctx || !m || layer < 0 || layer >= m->d.depth || axis < 0 || axis > 1 || S <= 0 || L <= 0) return 0;
     return transformer_block(ctx->stream, m->d, m->layers[2 * layer + axis], x, (int64_t)S * L, contiguous_layout(S, L),
-                             ctx->scratch, ctx->rope, &ctx->timer)
+                             ctx->scratch, ctx->rope, &ctx->timer, m->precision)
                ? 1
                : 0;
 }

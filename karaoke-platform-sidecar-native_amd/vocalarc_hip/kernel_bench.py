@@ -26,6 +26,7 @@ import numpy as np
 
 HBM_GBS = 8000.0
 FP32_TFLOPS = 157.3
+BF16_TFLOPS = 2500.0
 
 
 def _event_time(fn, reps: int) -> float:
@@ -41,7 +42,8 @@ def _event_time(fn, reps: int) -> float:
     return a.elapsed_time(b) / reps
 
 
-def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | None = None, shape: str = "") -> dict:
+def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | None = None, shape: str = "",
+          peak_tflops: float = FP32_TFLOPS) -> dict:
     rec = {"kernel": name, "shape": shape, "ms": round(ms, 4)}
     if gbytes is not None:
         gbs = gbytes / (ms * 1e-3)
@@ -50,7 +52,7 @@ def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | N
     if gflop is not None:
         tf = gflop / (ms * 1e-3) / 1e3
         rec.update({"algorithmic_GFLOP": round(gflop, 2), "TFLOP_per_s": round(tf, 2),
-                    "bound": "mfma", "frac_of_peak": round(tf / FP32_TFLOPS, 4)})
+                    "bound": "mfma", "frac_of_peak": round(tf / peak_tflops, 4)})
     print(json.dumps(rec), flush=True)
     return rec
 
@@ -58,9 +60,9 @@ def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | N
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,attn")
+    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,attn,bf16")
     args = ap.parse_args()
-    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "attn"}
+    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "attn", "bf16"}
 
     import torch
 
@@ -126,6 +128,25 @@ def main() -> int:
             _emit(name, _event_time(lambda: ctx.gemm(a, w, c, M, N, K, bias=b, epilogue=epi), max(3, reps // 4)),
                   gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}")
             del a, w, b, c
+
+    if "bf16" in groups:
+        # the same four GEMMs on bf16 matrix-core operands (fp32 activations
+        # rounded on the way into LDS, bf16 weight copies)
+        M = 8 * 801 * 62
+        for name, K, N, epi, ocols in (("gemm_bf16_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
+                                       ("gemm_bf16_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
+                                       ("gemm_bf16_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
+                                       ("gemm_bf16_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384)):
+            a = torch.randn(M, K, device=dev, generator=g)
+            w = 0.05 * torch.randn(N, K, device=dev, generator=g)
+            wh = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
+            ctx.to_bf16(w, wh, N, K, K)
+            b = torch.randn(N, device=dev, generator=g)
+            c = torch.zeros(M, ocols, device=dev)
+            _emit(name, _event_time(lambda: ctx.gemm_bf16(a, wh, c, M, N, K, K, bias=b, epilogue=epi),
+                                    max(3, reps // 4)),
+                  gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=BF16_TFLOPS)
+            del a, w, wh, b, c
 
     if "attn" in groups:
         for S, L in ((8 * 62, 801), (8 * 801, 62)):

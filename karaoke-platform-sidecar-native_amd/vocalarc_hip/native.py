@@ -19,8 +19,8 @@ LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
 # Every entry point declared in include/vocalarc_hip.h and include/native_gpu.h.
 HARNESS_SYMBOLS = [
     "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
-    "vh_rmsnorm", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_attention",
-    "vh_model_load", "vh_model_free", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
+    "vh_rmsnorm", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
+    "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
     "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
 ]
 ABI_SYMBOLS = [
@@ -31,6 +31,7 @@ ABI_SYMBOLS = [
 ]
 
 EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
+PRECISION_FP32, PRECISION_BF16 = 0, 1
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -59,9 +60,11 @@ def lib():
         "vh_geglu": (_I, [_P, _I64, _I, _P, _P]),
         "vh_residual_add": (_I, [_P, _I64, _P, _P]),
         "vh_gemm": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
+        "vh_gemm_bf16": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
+        "vh_to_bf16": (_I, [_P, _I64, _I, _P, _P, _I]),
         "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I]),
         "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
-        "vh_model_free": (None, [_P]),
+        "vh_model_free": (None, [_P]), "vh_model_set_precision": (_I, [_P, _I]),
         "vh_transformer": (_I, [_P, _P, _I, _I, _P, _I, _I]),
         "vh_stft": (_I, [_P, _P, _P, _I, _P]),
         "vh_istft": (_I, [_P, _P, _P, _P, _I, _P]),
@@ -162,6 +165,16 @@ class Context:
                           ptr(bias) if bias is not None else None, ptr(C),
                           ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm")
 
+    def gemm_bf16(self, A, Wh, C, M: int, N: int, K: int, ldw: int, bias=None, epilogue: int = EPI_STORE,
+                  lda: int | None = None, ldc: int | None = None):
+        """Wh: bf16 weight copy [N][ldw] (see to_bf16)."""
+        _ok(lib().vh_gemm_bf16(self.h, M, N, K, ptr(A), lda or K, ptr(Wh), ldw,
+                               ptr(bias) if bias is not None else None, ptr(C),
+                               ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm_bf16")
+
+    def to_bf16(self, src, dst, rows: int, cols: int, ld: int):
+        _ok(lib().vh_to_bf16(self.h, rows, cols, ptr(src), ptr(dst), ld), "vh_to_bf16")
+
     def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True):
         _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary)), "vh_attention")
 
@@ -202,6 +215,9 @@ class Model:
             self.close()
         except Exception:  # noqa: BLE001
             pass
+
+    def set_precision(self, precision: int):
+        _ok(lib().vh_model_set_precision(self.h, precision), "vh_model_set_precision")
 
     def transformer(self, layer: int, axis: int, x, sequences: int, length: int):
         _ok(lib().vh_transformer(self.ctx.h, self.h, layer, axis, ptr(x), sequences, length), "vh_transformer")

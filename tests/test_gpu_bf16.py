@@ -1,0 +1,196 @@
+"""bf16-MFMA variant: conversion, the bf16 GEMM, and the whole model.
+
+The variant rounds activations and weights to bf16 at the matrix-core inputs
+and keeps everything else fp32.  Its kernels are pinned exactly where
+rounding allows it:
+  * fp32 -> bf16 conversion: bit-identical to torch's round-to-nearest-even;
+  * bf16 GEMM: against a float64 product of the same bf16-rounded operands.
+    Every bf16 x bf16 product is exact in fp32, so the only difference is
+    the fp32 summation order: rtol 1e-5 of the output scale.
+The model-level bar is SNR >= 40 dB against the fp32 oracle (the variant is
+reported separately from the fp32 parity path, whose bar is 80 dB).
+"""
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, empty_dev, from_dev, gpu_available, snr_db, to_dev
+
+pytestmark = pytest.mark.gpu
+
+if gpu_available():
+    import torch
+    import oracle as O
+    from vocalarc_hip import audio, native, pack
+    from vocalarc_hip.dims import CONFIG_DIMS, REFERENCE_DIMS
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    c = native.Context()
+    yield c
+    c.close()
+
+
+def _round_bf16(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(x)).to(torch.bfloat16).to(torch.float32).numpy()
+
+
+def _dev_bf16(ctx, w: np.ndarray):
+    """Device bf16 copy [N][ld] with ld = K rounded up to 8 and zero padding."""
+    n, k = w.shape
+    ld = (k + 7) // 8 * 8
+    dst = torch.zeros(n, ld, dtype=torch.bfloat16, device="cuda:0")
+    ctx.to_bf16(to_dev(w), dst, n, k, ld)
+    return dst, ld
+
+
+def test_to_bf16_bit_exact(ctx, rng):
+    x = rng.standard_normal((37, 50), dtype=np.float32) * np.float32(1e3)
+    # exact ties (low 16 bits 0x8000) in both rounding directions, and infinities
+    ties = (np.arange(64, dtype=np.uint32) << 16 | 0x3F800000 | 0x8000).view(np.float32)
+    x[0, :50] = ties[:50]
+    x[1, :4] = [np.inf, -np.inf, 3.0e38, -1.0e-30]
+    pitch = 56
+    dst = torch.full((37, pitch), 7.0, dtype=torch.bfloat16, device="cuda:0")
+    ctx.to_bf16(to_dev(x), dst, 37, 50, pitch)
+    torch.cuda.synchronize()
+    got = dst.cpu()
+    want = torch.from_numpy(x).to(torch.bfloat16)
+    assert torch.equal(got[:, :50].view(torch.int16), want.view(torch.int16))
+    assert torch.all(got[:, 50:] == 7.0), "padding columns must be left untouched"
+
+
+BF16_GEMM_CASES = [
+    # M, N, K, epilogue, bias
+    (300, 200, 96, 0, True),
+    (1000, 1536, 384, 0, False),
+    (257, 1024, 256, 1, True),
+    (77, 384, 1536, 3, True),
+    (50, 16, 1536, 0, True),
+    (40, 256, 516, 0, True),   # K % 8 == 4: zero-padded weight rows
+    (33, 8, 256, 0, True),
+    (130, 1536, 384, 2, True),
+    (1, 32, 8, 0, True),
+    (600, 520, 20, 0, True),   # K below one 32-wide k-step
+    (4097, 768, 384, 0, True),
+]
+
+
+def _ref_linear(x, w, b):
+    y = _round_bf16(x).astype(np.float64) @ _round_bf16(w).astype(np.float64).T
+    if b is not None:
+        y += b.astype(np.float64)
+    return y
+
+
+@pytest.mark.parametrize("M,N,K,epi,has_bias", BF16_GEMM_CASES)
+def test_gemm_bf16_exact_products(ctx, rng, M, N, K, epi, has_bias):
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if has_bias else None
+    ref = _ref_linear(x, w, b)
+    if epi == native.EPI_GELU:
+        ref = O.gelu(ref.astype(np.float32)).astype(np.float64)
+    elif epi == native.EPI_TANH:
+        ref = np.tanh(ref)
+    c0 = rng.standard_normal((M, N), dtype=np.float32)
+    if epi == native.EPI_RESIDUAL:
+        ref = c0 + ref
+    wh, ld = _dev_bf16(ctx, w)
+    dc = to_dev(c0)
+    ctx.gemm_bf16(to_dev(x), wh, dc, M, N, K, ld, bias=to_dev(b) if b is not None else None, epilogue=epi)
+    out = from_dev(dc)
+    scale = float(np.sqrt(K)) * 0.05 * 4 + 1.0
+    assert_close(ref.astype(np.float32), out, rtol=1e-5, atol=1e-5 * scale, what=f"gemm_bf16 {M}x{N}x{K} epi{epi}")
+
+
+def test_gemm_bf16_geglu_epilogue(ctx, rng):
+    M, F, K = 333, 192, 384
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((2 * F, K))).astype(np.float32)
+    b = rng.standard_normal(2 * F).astype(np.float32)
+    y = _ref_linear(x, w, b).astype(np.float32)
+    ref = O.geglu(y)
+    # the library's 32-row interleave of value/gate rows
+    perm = np.empty(2 * F, dtype=np.int64)
+    for c in range(F):
+        perm[(c // 32) * 64 + (c % 32)] = c
+        perm[(c // 32) * 64 + 32 + (c % 32)] = F + c
+    wh, ld = _dev_bf16(ctx, np.ascontiguousarray(w[perm]))
+    dc = empty_dev((M, F))
+    ctx.gemm_bf16(to_dev(x), wh, dc, M, 2 * F, K, ld, bias=to_dev(np.ascontiguousarray(b[perm])),
+                  epilogue=native.EPI_GEGLU)
+    assert_close(ref, from_dev(dc), rtol=1e-5, atol=2e-5, what="gemm_bf16 GELU-GLU")
+
+
+def test_gemm_bf16_rejects_bad_pitch(ctx):
+    x = torch.zeros(8, 20, device="cuda:0")
+    wh = torch.zeros(8, 20, dtype=torch.bfloat16, device="cuda:0")
+    c = torch.zeros(8, 8, device="cuda:0")
+    with pytest.raises(native.NativeError, match="unsupported shape"):
+        ctx.gemm_bf16(x, wh, c, 8, 8, 20, 20)  # ldw must be a multiple of 8 and >= 24
+
+
+def test_bf16_forward_config_depth12(ctx):
+    d = CONFIG_DIMS
+    blob = pack.synthetic_pack(d, 5)
+    om, dm = O.Model(d, blob), native.Model(ctx, d, blob)
+    x = audio.sine_mix(0.5, 21)
+    ref = om.forward(x)
+    dv = empty_dev(x.shape)
+    dm.set_precision(native.PRECISION_BF16)
+    dm.forward(to_dev(x), x.shape[1], dv)
+    out = from_dev(dv)
+    snr = snr_db(ref, out)
+    print(f"bf16 forward (dim 384, depth 12, 0.5 s): SNR {snr:.1f} dB vs the fp32 oracle, "
+          f"max|d| {float(np.max(np.abs(out - ref))):.3e}")
+    assert snr >= 40
+    # switching back restores the fp32 parity path
+    dm.set_precision(native.PRECISION_FP32)
+    dm.forward(to_dev(x), x.shape[1], dv)
+    out32 = from_dev(dv)
+    assert float(np.max(np.abs(out32.astype(np.float64) - ref))) <= 1e-4
+    assert snr_db(ref, out32) >= 80
+    dm.close()
+
+
+def test_bf16_forward_reference_shape(ctx, ref_pack):
+    om, dm = O.Model(REFERENCE_DIMS, ref_pack), native.Model(ctx, REFERENCE_DIMS, ref_pack)
+    x = audio.sine_mix(0.3, 22)
+    ref = om.forward(x)
+    dv = empty_dev(x.shape)
+    dm.set_precision(native.PRECISION_BF16)
+    dm.forward(to_dev(x), x.shape[1], dv)
+    snr = snr_db(ref, from_dev(dv))
+    print(f"bf16 forward (reference shape, depth 16, 0.3 s): SNR {snr:.1f} dB vs the fp32 oracle")
+    assert snr >= 40
+    dm.close()
+
+
+def test_bf16_chunked_separation(ctx):
+    d = CONFIG_DIMS.with_depth(2)
+    blob = pack.synthetic_pack(d, 92)
+    om, dm = O.Model(d, blob), native.Model(ctx, d, blob)
+    x = audio.sine_mix(1.0, 23)
+    chunk, step = 13230, 8820
+    ref = om.separate_chunked(x, chunk, step)
+    dm.set_precision(native.PRECISION_BF16)
+    dv, di = empty_dev(x.shape), empty_dev(x.shape)
+    dm.separate(to_dev(x), x.shape[1], chunk, step, 3, dv, di)
+    out = from_dev(dv)
+    assert np.array_equal(from_dev(di), x - out)
+    snr = snr_db(ref, out)
+    print(f"bf16 chunked separation (5 windows): SNR {snr:.1f} dB vs the fp32 oracle")
+    assert snr >= 40
+    dm.close()
+
+
+def test_set_precision_rejects_unknown(ctx):
+    d = CONFIG_DIMS.with_depth(1)
+    dm = native.Model(ctx, d, pack.synthetic_pack(d, 3))
+    with pytest.raises(native.NativeError, match="unknown precision"):
+        dm.set_precision(7)
+    dm.close()
