@@ -41,6 +41,9 @@ MFMA_FP32_PEAK_TFLOPS = 157.3
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBS = 8000.0
 DOMINANT = "gemm_ff1"
+KERNEL_CLASSES = ("stft", "band_gather", "gemm_band_split", "rmsnorm", "gemm_qkv", "attention_long",
+                  "attention_short", "gemm_out", "gemm_ff1", "gemm_ff2", "gemm_mask1", "gemm_mask2", "mask_glu",
+                  "istft", "crossfade")
 
 
 def log(msg: str) -> None:
@@ -121,6 +124,8 @@ def bf16_variant(ctx, model, dx, dv, ref_out, length, chunk, step, args, d) -> d
     for i in range(args.warmup):
         model.separate(dx, length, chunk, step, BATCH, dv)
         ctx.sync()
+    if args.breakdown:
+        log("bf16 step by kernel class: " + breakdown(ctx, lambda: model.separate(dx, length, chunk, step, BATCH, dv)))
     ctx.timing(DOMINANT)
     ctx.timing_reset()
     torch.cuda.synchronize()
@@ -151,6 +156,18 @@ def bf16_variant(ctx, model, dx, dv, ref_out, length, chunk, step, args, d) -> d
     }
 
 
+def breakdown(ctx, run) -> str:
+    """Per-kernel-class device time of one step (HIP events around each launch)."""
+    ctx.timing("*")
+    ctx.timing_reset()
+    run()
+    ctx.sync()
+    ctx.timing(None)
+    rows = [(name, *ctx.timing_get(name)) for name in KERNEL_CLASSES]
+    total = sum(ms for _, ms, _ in rows) or 1.0
+    return "; ".join(f"{name} {ms:.1f} ms ({100 * ms / total:.1f}%)" for name, ms, n in rows if n)
+
+
 def _final_gamma(d, blob):
     from vocalarc_hip import pack
     return pack.tensor_views(d, blob)["final_gamma"]
@@ -164,6 +181,7 @@ def main() -> int:
     ap.add_argument("--seconds", type=float, default=SECONDS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-MFMA variant")
+    ap.add_argument("--breakdown", action="store_true", help="per-kernel-class time of one untimed step (stderr)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs the separation path on a single GPU "
@@ -194,6 +212,8 @@ def main() -> int:
         model.separate(dx, length, chunk, step, BATCH, dv)
         ctx.sync()
         log(f"warmup step {i}: {time.perf_counter() - t0:.3f} s")
+    if args.breakdown:
+        log("fp32 step by kernel class: " + breakdown(ctx, lambda: model.separate(dx, length, chunk, step, BATCH, dv)))
 
     ctx.timing(DOMINANT)
     ctx.timing_reset()

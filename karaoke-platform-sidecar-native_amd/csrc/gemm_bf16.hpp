@@ -1,15 +1,22 @@
 // bf16-MFMA variant of the token-wise linear: C[M][N] (op)= A[M][K] * B[N][K]^T
-// with A read as fp32 and rounded to bf16 while it is staged into LDS, B a
-// bf16 copy of the weight matrix, fp32 accumulation and the same fused fp32
+// with bf16 matrix-core operands, fp32 accumulation and the same fused fp32
 // epilogues as the fp32 GEMM.  This is the separately reported reduced
 // precision path; the fp32 GEMM (gemm.hpp) is the parity path.
 //
+// A is either fp32 (rounded to bf16, nearest-even, as it is staged into LDS)
+// or already bf16 (written that way by its producer: the normalisation, the
+// attention store or a preceding GEMM's epilogue).  The output is fp32 or
+// bf16 (the residual epilogue is always fp32).
+//
 // Tiling: 256x128 block tile, 4 wavefronts in a 2x2 grid, each owning a
 // 128x64 sub-tile = 4x2 v_mfma_f32_32x32x16_bf16 accumulators.  K is staged in
-// chunks of 32 (two MFMA steps); per step a wave reads 4 A and 2 B operands of
-// 8 bf16 (ds_read_b128) for 8 MFMAs.  LDS rows are padded to 40 bf16 (80 B)
-// so the 16 rows of each read phase fall on disjoint banks.
+// chunks of BK (BK/16 MFMA steps); per step a wave reads 4 A and 2 B operands
+// of 8 bf16 (ds_read_b128) for 8 MFMAs.  LDS rows are padded by 8 bf16 so
+// the 16 rows of each read phase fall on disjoint banks.  Staging is
+// register-prefetched one chunk ahead with double-buffered LDS.
 #pragma once
+
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -20,15 +27,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 struct GemmDescBF16 {
-    const float *A;     // fp32 activations
-    const bf16 *B;      // bf16 weights [N][K]
+    const void *A;      // fp32 or bf16 activations [M][lda]
+    const bf16 *B;      // bf16 weights [N][ldb]
     const float *bias;  // fp32, may be null
-    float *C;
+    void *C;            // fp32 or bf16 [M][ldc]
     int M, N, K;
     int lda, ldb, ldc;
 };
 
-constexpr int GB_BM = 256, GB_BN = 128, GB_BK = 32, GB_PITCH = GB_BK + 8;
+constexpr int GB_BM = 256, GB_BN = 128;
 constexpr int GB_THREADS = 256;
 constexpr int GB_MAX_BATCH = 64;
 struct GemmBatchBF16 {
@@ -44,10 +51,26 @@ VH_DEVICE bf16x4 to_bf16x4(floatx4 v) {
     return r;
 }
 
-template <int EPI>
+template <typename T>
+VH_DEVICE void store_out(T *p, float v) {
+    if constexpr (std::is_same<T, float>::value) *p = v;
+    else *p = (bf16)v;
+}
+
+template <int EPI, typename TA, typename TC, int BK>
 __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) {
-    __shared__ __attribute__((aligned(16))) bf16 As[2][GB_BM][GB_PITCH];
-    __shared__ __attribute__((aligned(16))) bf16 Bs[2][GB_BN][GB_PITCH];
+    constexpr int PITCH = BK + 8;
+    constexpr bool A32 = std::is_same<TA, float>::value;
+    constexpr int A_VEC = A32 ? 4 : 8;                      // elements per 16-byte load
+    constexpr int A_CPR = BK / A_VEC;                       // chunks per row
+    constexpr int A_RPP = GB_THREADS / A_CPR;               // rows per pass
+    constexpr int A_PASSES = GB_BM / A_RPP;
+    constexpr int B_CPR = BK / 8;
+    constexpr int B_RPP = GB_THREADS / B_CPR;
+    constexpr int B_PASSES = GB_BN / B_RPP;
+    static_assert(GB_BM % A_RPP == 0 && GB_BN % B_RPP == 0, "staging must tile the block");
+    __shared__ __attribute__((aligned(16))) bf16 As[2][GB_BM][PITCH];
+    __shared__ __attribute__((aligned(16))) bf16 Bs[2][GB_BN][PITCH];
 
     const int tiles_n = (d.N + GB_BN - 1) / GB_BN;
     const int tiles_m = (d.M + GB_BM - 1) / GB_BM;
@@ -65,23 +88,33 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 31, lh = lane >> 5;
 
-    // A: 256 rows x 8 float4 per chunk -> 8 float4 per thread (row tid/8 + 32q, quad tid%8)
-    // B: 128 rows x 4 x 16 B (8 bf16) per chunk -> 2 per thread (row tid/4 + 64q, part tid%4)
-    const int a_row = tid >> 3, a_c4 = tid & 7;
-    const int b_row = tid >> 2, b_c8 = tid & 3;
-    floatx4 ra[8];
-    bf16x8 rb[2];
+    const int a_row = tid / A_CPR, a_c = tid % A_CPR;
+    const int b_row = tid / B_CPR, b_c = tid % B_CPR;
+    const TA *Ag = static_cast<const TA *>(d.A);
+    floatx4 ra32[A32 ? A_PASSES : 1];
+    bf16x8 ra16[A32 ? 1 : A_PASSES];
+    bf16x8 rb[B_PASSES];
     auto load = [&](int k0) {
-        const int ka = k0 + 4 * a_c4;
+        const int ka = k0 + A_VEC * a_c;
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const int gm = min(m0 + a_row + 32 * q, d.M - 1);
-            ra[q] = ka < d.K ? ld4(d.A + (size_t)gm * d.lda + ka) : floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < A_PASSES; q++) {
+            const int gm = min(m0 + a_row + A_RPP * q, d.M - 1);
+            if constexpr (A32) {
+                ra32[q] = ka < d.K ? ld4(reinterpret_cast<const float *>(Ag) + (size_t)gm * d.lda + ka)
+                                   : floatx4{0.f, 0.f, 0.f, 0.f};
+            } else {
+                if (ka < d.K) {
+                    ra16[q] = *reinterpret_cast<const bf16x8 *>(Ag + (size_t)gm * d.lda + ka);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) ra16[q][e] = (bf16)0.0f;
+                }
+            }
         }
-        const int kb = k0 + 8 * b_c8;
+        const int kb = k0 + 8 * b_c;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int gn = min(n0 + b_row + 64 * q, d.N - 1);
+        for (int q = 0; q < B_PASSES; q++) {
+            const int gn = min(n0 + b_row + B_RPP * q, d.N - 1);
             if (kb < d.K) {
                 rb[q] = *reinterpret_cast<const bf16x8 *>(d.B + (size_t)gn * d.ldb + kb);
             } else {
@@ -92,10 +125,14 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < 8; q++)
-            *reinterpret_cast<bf16x4 *>(&As[buf][a_row + 32 * q][4 * a_c4]) = to_bf16x4(ra[q]);
+        for (int q = 0; q < A_PASSES; q++) {
+            if constexpr (A32)
+                *reinterpret_cast<bf16x4 *>(&As[buf][a_row + A_RPP * q][4 * a_c]) = to_bf16x4(ra32[q]);
+            else
+                *reinterpret_cast<bf16x8 *>(&As[buf][a_row + A_RPP * q][8 * a_c]) = ra16[q];
+        }
 #pragma unroll
-        for (int q = 0; q < 2; q++) *reinterpret_cast<bf16x8 *>(&Bs[buf][b_row + 64 * q][8 * b_c8]) = rb[q];
+        for (int q = 0; q < B_PASSES; q++) *reinterpret_cast<bf16x8 *>(&Bs[buf][b_row + B_RPP * q][8 * b_c]) = rb[q];
     };
 
     floatx16 acc[4][2];
@@ -106,15 +143,15 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    const int nk = (d.K + GB_BK - 1) / GB_BK;
+    const int nk = (d.K + BK - 1) / BK;
     load(0);
     store(0);
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) load((kt + 1) * GB_BK);
+        if (kt + 1 < nk) load((kt + 1) * BK);
 #pragma unroll
-        for (int st = 0; st < GB_BK / 16; st++) {
+        for (int st = 0; st < BK / 16; st++) {
             bf16x8 a[4], b[2];
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -134,6 +171,7 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
 
     // Accumulator layout as for the fp32 32x32 MFMA: lane (li, lh), register r
     // holds row 8*(r/4) + 4*lh + r%4, column li.
+    TC *C = static_cast<TC *>(d.C);
     if constexpr (EPI == EPI_GEGLU) {
         const int nv = n0 + wn * 64 + li;
         const int ng = nv + 32;
@@ -146,10 +184,12 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (row < d.M) d.C[(size_t)row * d.ldc + oc] = (acc[i][0][r] + bv) * gelu_dev(acc[i][1][r] + bg);
+                    if (row < d.M)
+                        store_out(C + (size_t)row * d.ldc + oc, (acc[i][0][r] + bv) * gelu_dev(acc[i][1][r] + bg));
                 }
         }
     } else {
+        static_assert(EPI != EPI_RESIDUAL || std::is_same<TC, float>::value, "residual output is fp32");
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int col = n0 + wn * 64 + j * 32 + li;
@@ -162,24 +202,24 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
                     const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                     if (row >= d.M) continue;
                     const float v = acc[i][j][r] + bc;
-                    float *p = d.C + (size_t)row * d.ldc + col;
-                    if constexpr (EPI == EPI_STORE) *p = v;
-                    else if constexpr (EPI == EPI_GELU) *p = gelu_dev(v);
-                    else if constexpr (EPI == EPI_TANH) *p = tanhf(v);
+                    TC *p = C + (size_t)row * d.ldc + col;
+                    if constexpr (EPI == EPI_STORE) store_out(p, v);
+                    else if constexpr (EPI == EPI_GELU) store_out(p, gelu_dev(v));
+                    else if constexpr (EPI == EPI_TANH) store_out(p, tanhf(v));
                     else if constexpr (EPI == EPI_RESIDUAL) *p = *p + v;
                 }
         }
     }
 }
 
-template <int EPI>
+template <int EPI, typename TA, typename TC, int BK>
 __global__ __launch_bounds__(GB_THREADS, 2) void gemm_bf16_kernel(GemmDescBF16 d) {
-    gemm_bf16_body<EPI>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+    gemm_bf16_body<EPI, TA, TC, BK>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
-template <int EPI>
+template <int EPI, typename TA, typename TC, int BK>
 __global__ __launch_bounds__(GB_THREADS, 2) void gemm_bf16_batched_kernel(GemmBatchBF16 b) {
-    gemm_bf16_body<EPI>(b.d[blockIdx.z], (int)blockIdx.x);
+    gemm_bf16_body<EPI, TA, TC, BK>(b.d[blockIdx.z], (int)blockIdx.x);
 }
 
 // fp32 [rows][cols] -> bf16 [rows][ld] (weights at upload; padding untouched)

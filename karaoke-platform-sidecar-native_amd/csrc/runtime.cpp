@@ -201,7 +201,7 @@ static bool gemm_bf16_ok(const GemmArgsBF16 &g, int epilogue) {
 
 static GemmDescBF16 to_desc_bf16(const GemmArgsBF16 &g) {
     GemmDescBF16 d;
-    d.A = g.A; d.B = static_cast<const bf16 *>(g.B); d.bias = g.bias; d.C = g.C;
+    d.A = g.A; d.B = static_cast<const bf16 *>(g.B); d.bias = g.bias; d.C = g.C;  // fp32 A and C
     d.M = (int)g.M; d.N = g.N; d.K = g.K;
     d.lda = g.lda; d.ldb = g.ldb; d.ldc = g.ldc;
     return d;
@@ -214,8 +214,8 @@ static int64_t tiles_bf16(const GemmArgsBF16 &g) {
 template <int EPI>
 static void launch_bf16_epi(hipStream_t s, const GemmDescBF16 *single, const GemmBatchBF16 *batch, unsigned tiles,
                             unsigned n) {
-    if (single) hipLaunchKernelGGL(gemm_bf16_kernel<EPI>, dim3(tiles), dim3(GB_THREADS), 0, s, *single);
-    else hipLaunchKernelGGL(gemm_bf16_batched_kernel<EPI>, dim3(tiles, 1, n), dim3(GB_THREADS), 0, s, *batch);
+    if (single) hipLaunchKernelGGL((gemm_bf16_kernel<EPI, float, float, 32>), dim3(tiles), dim3(GB_THREADS), 0, s, *single);
+    else hipLaunchKernelGGL((gemm_bf16_batched_kernel<EPI, float, float, 32>), dim3(tiles, 1, n), dim3(GB_THREADS), 0, s, *batch);
 }
 
 static bool launch_bf16(hipStream_t s, int epi, const GemmDescBF16 *single, const GemmBatchBF16 *batch,

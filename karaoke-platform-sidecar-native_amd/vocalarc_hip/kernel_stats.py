@@ -1,0 +1,82 @@
+"""Summarise a `rocprofv3 --kernel-trace --stats` run of bench.py as markdown.
+
+Reads `*_kernel_stats.csv` from the run directory and the bench.py JSON line
+the same command printed, and writes a short table (kernel, calls, total and
+average duration, share) plus the live HIP-event figure of the dominant
+kernel for comparison:
+
+    python -m vocalarc_hip.kernel_stats RUN_DIR BENCH_JSON OUT.md "<command>"
+"""
+
+from __future__ import annotations
+
+import csv
+import json
+import sys
+from pathlib import Path
+
+# kernel-name fragments -> what the launch computes in the separation pass
+ROLES = [
+    ("gemm_f32_kernel<4", "FFN up-projection + GELU-GLU (fp32)"),
+    ("gemm_f32_kernel<3", "out projection / FFN down-projection + residual (fp32)"),
+    ("gemm_f32_kernel<0", "fused QKV + gate projection (fp32)"),
+    ("gemm_f32_batched_kernel<2", "mask estimator layer 1 + tanh, batched over bands (fp32)"),
+    ("gemm_f32_batched_kernel<0", "band split / mask estimator layer 2, batched over bands (fp32)"),
+    ("gemm_bf16_kernel<4", "FFN up-projection + GELU-GLU (bf16 variant)"),
+    ("gemm_bf16_kernel<3", "out / FFN down-projection + residual (bf16 variant)"),
+    ("gemm_bf16_kernel<0", "fused QKV + gate projection (bf16 variant)"),
+    ("gemm_bf16_batched_kernel<2", "mask layer 1 (bf16 variant)"),
+    ("gemm_bf16_batched_kernel<0", "band split / mask layer 2 (bf16 variant)"),
+    ("attention_kernel<4>", "time-axis attention, L = 801"),
+    ("attention_kernel<2>", "band-axis attention, L = 62"),
+    ("rmsnorm_kernel", "pre-norms and final norm"),
+    ("stft_kernel", "STFT"),
+    ("istft_frames_kernel", "mask multiply + inverse FFT"),
+    ("ola_kernel", "overlap-add"),
+    ("band_gather_norm_kernel", "band gather + RMSNorm"),
+    ("mask_glu_scatter_kernel", "mask GLU + bin scatter"),
+    ("crossfade_kernel", "window cross-fade"),
+]
+
+
+def role(name: str) -> str:
+    for frag, what in ROLES:
+        if frag in name.replace(", ", ",").replace("vh::", ""):
+            return what
+    return ""
+
+
+def main() -> int:
+    run_dir, bench_json, out, command = sys.argv[1:5]
+    path = next(Path(run_dir).rglob("*kernel_stats.csv"))
+    rows = list(csv.DictReader(open(path)))
+    bench = None
+    for line in Path(bench_json).read_text().splitlines():
+        if line.startswith("{"):
+            bench = json.loads(line)
+    lines = [
+        "# Kernel time of the 5-minute separation (fp32 timed region, then the bf16 variant)",
+        "", "Command (repository root, MI355X box):", "", "```", command.strip(), "```", "",
+        f"Source: `{path.name}` written by rocprofv3 (durations in ms). The run covers the warm-up, the timed steps and "
+        "the bf16 variant's warm-up and timed steps of bench.py.", "",
+        "| kernel | role | calls | total ms | avg ms | % |", "|---|---|---:|---:|---:|---:|",
+    ]
+    for r in rows:
+        name = r["Name"]
+        short = name if len(name) < 90 else name[:87] + "..."
+        lines.append(f"| `{short}` | {role(name)} | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
+                     f"{float(r['AverageNs']) / 1e6:.4f} | {float(r['Percentage']):.2f} |")
+    if bench:
+        rf = bench["roofline"]
+        dom = next((r for r in rows if "gemm_f32_kernel<4" in r["Name"]), None)
+        lines += ["", f"Dominant kernel: live HIP-event average in bench.py {rf['avg_launch_ms']} ms over "
+                      f"{rf['launches']} launches of the timed region; rocprofv3 average over all its launches "
+                      f"{float(dom['AverageNs']) / 1e6:.4f} ms ({dom['Calls']} launches)." if dom else "",
+                  "", "bench.py line of the same command:", "", "```", json.dumps(bench), "```"]
+    Path(out).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
