@@ -53,6 +53,8 @@ const char *vh_device_name(vh_context *ctx);
 /* RMSNorm rows: y = x * sqrt(dim)/sqrt(sum x^2 + 1e-12) * gamma
    (native/vocalarc_separation.c:419-424, native/native_simd.c:98-121). */
 int vh_rmsnorm(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, float *y);
+/* Same, y written as bf16 (round to nearest even): the bf16 variant's GEMM operand. */
+int vh_rmsnorm_bf16(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, void *y);
 /* Row softmax over [rows][len] (native/native_gpu_cuda.cu:357-381). */
 int vh_softmax_rows(vh_context *ctx, int64_t rows, int len, const float *in, float *out);
 /* Rotary embedding in place on [bh][len][dim_head] with base 10000
@@ -67,18 +69,23 @@ int vh_residual_add(vh_context *ctx, int64_t n, float *x, const float *r);
    2 tanh, 3 residual (C +=), 4 GELU-GLU on interleaved columns. */
 int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const float *W, int ldw,
             const float *bias, float *C, int ldc, int epilogue);
-/* bf16-MFMA variant of vh_gemm: A fp32 rounded to bf16 (round to nearest
-   even) as it is staged, Wh a bf16 weight copy [N][ldw] (ldw a multiple of 8,
-   >= K, zero padded), fp32 accumulation and epilogue.  K and lda multiples of
-   4, A and Wh 16-byte aligned. */
-int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Wh, int ldw,
-                 const float *bias, float *C, int ldc, int epilogue);
+/* bf16-MFMA variant of vh_gemm: Wh a bf16 weight copy [N][ldw] (ldw a
+   multiple of 8, >= K, zero padded), fp32 accumulation and epilogue.
+   A is fp32, rounded to bf16 (nearest even) as it is staged, or bf16 with
+   VH_BF16_A (then K and lda multiples of 8); C is fp32, or bf16 with
+   VH_BF16_C (not with the residual epilogue).  K and lda multiples of 4,
+   A and Wh 16-byte aligned. */
+#define VH_BF16_A 1
+#define VH_BF16_C 2
+int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int lda, const void *Wh, int ldw,
+                 const float *bias, void *C, int ldc, int epilogue, int flags);
 /* fp32 src[rows][cols] -> bf16 dst[rows][ld] (round to nearest even). */
 int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld);
 /* Fused attention core over qkv[S*L][3*H*64] (rotary applied here):
-   native/vocalarc_separation.c:692-793.  out[S*L][H*64]. */
-int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, float *out,
-                 int apply_rotary);
+   native/vocalarc_separation.c:692-793.  out[S*L][H*64], fp32 or (out_bf16)
+   bf16 rounded to nearest even. */
+int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, void *out,
+                 int apply_rotary, int out_bf16);
 
 /* ---- model -------------------------------------------------------------- */
 /* Upload a VSCNAT01 pack (native/vocalarc_separation.c:528-589) laid out for

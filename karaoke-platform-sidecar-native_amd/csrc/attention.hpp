@@ -31,7 +31,7 @@ namespace vh {
 struct AttnArgs {
     const float *qkv;  // fused projection rows
     int ld;            // row pitch of qkv (floats)
-    float *out;        // [rows][ld_out], head h at column h*64
+    void *out;         // [rows][ld_out] fp32 or bf16, head h at column h*64
     int ld_out;
     const float *rope_cos;  // [L][32], may be null (no rotary)
     const float *rope_sin;
@@ -70,7 +70,7 @@ VH_DEVICE floatx4 rope4(floatx4 v, const float *cs, const float *sn, int pos, in
 // loads key e%16 (+16 for e >= 256) and 16-byte chunk (e/16)%16 of that key's
 // 64 dims, which makes both the K row writes and the V column writes
 // bank-conflict free.
-template <int WAVES>
+template <int WAVES, typename TO>
 __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     constexpr int NT = 64 * WAVES;
     constexpr int KV_F4 = ATT_KB * ATT_DH / 4;   // float4s per K (or V) tile
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     const int row = attn_row(a, s, q);
     float gate = 1.0f;
     if (a.gate_col >= 0) gate = sigmoid_dev(a.qkv[(size_t)row * a.ld + a.gate_col + h]);
-    float *op = a.out + (size_t)row * a.ld_out + h * ATT_DH;
+    TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll

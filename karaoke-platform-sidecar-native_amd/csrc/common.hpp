@@ -32,6 +32,23 @@ VH_DEVICE float gelu_dev(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067
 VH_DEVICE floatx4 ld4(const float *p) { return *reinterpret_cast<const floatx4 *>(p); }
 VH_DEVICE void st4(float *p, floatx4 v) { *reinterpret_cast<floatx4 *>(p) = v; }
 
+// bf16 storage (round to nearest even on conversion: v_cvt_pk_bf16_f32)
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+VH_DEVICE bf16x4 to_bf16x4(floatx4 v) {
+    bf16x4 r;
+    r[0] = (bf16)v[0];
+    r[1] = (bf16)v[1];
+    r[2] = (bf16)v[2];
+    r[3] = (bf16)v[3];
+    return r;
+}
+
+// Four consecutive outputs, fp32 or bf16.
+VH_DEVICE void st4(bf16 *p, floatx4 v) { *reinterpret_cast<bf16x4 *>(p) = to_bf16x4(v); }
+
 // Non-temporal streaming variants for data touched exactly once.
 VH_DEVICE floatx4 ld4_stream(const float *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(p));

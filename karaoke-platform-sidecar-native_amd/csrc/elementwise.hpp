@@ -10,15 +10,16 @@ namespace vh {
 // y = x * (sqrt(d) / sqrt(sum(x^2) + 1e-12)) * gamma
 // (native/vocalarc_separation.c:419-424, native/native_simd.c:98-121).
 // One wavefront per row, the row held in registers between the two passes.
-template <int MAXV>
+// TY: fp32, or bf16 when the output feeds a bf16-operand GEMM.
+template <int MAXV, typename TY>
 static __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, int ldx,
                                                       const float *__restrict__ gamma,
-                                                      float *__restrict__ y, int ldy, int rows, int dim) {
+                                                      TY *__restrict__ y, int ldy, int rows, int dim) {
     const int row = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
     const int lane = (int)threadIdx.x & 63;
     if (row >= rows) return;
     const float *xr = x + (size_t)row * ldx;
-    float *yr = y + (size_t)row * ldy;
+    TY *yr = y + (size_t)row * ldy;
     const int nv = dim >> 2;
     floatx4 v[MAXV];
     float ss = 0.0f;

@@ -8,12 +8,13 @@
 // attention store or a preceding GEMM's epilogue).  The output is fp32 or
 // bf16 (the residual epilogue is always fp32).
 //
-// Tiling: 256x128 block tile, 4 wavefronts in a 2x2 grid, each owning a
-// 128x64 sub-tile = 4x2 v_mfma_f32_32x32x16_bf16 accumulators.  K is staged in
-// chunks of BK (BK/16 MFMA steps); per step a wave reads 4 A and 2 B operands
-// of 8 bf16 (ds_read_b128) for 8 MFMAs.  LDS rows are padded by 8 bf16 so
-// the 16 rows of each read phase fall on disjoint banks.  Staging is
-// register-prefetched one chunk ahead with double-buffered LDS.
+// Tiling (template parameters): WM x WN wavefronts, each owning FM x FN
+// 32x32 accumulators of v_mfma_f32_32x32x16_bf16, i.e. a block tile of
+// (32*WM*FM) x (32*WN*FN).  K is staged in chunks of BK (BK/16 MFMA steps);
+// per step a wave reads FM A and FN B operands of 8 bf16 (ds_read_b128) for
+// FM*FN MFMAs.  LDS rows are padded by 8 bf16 so the 16 rows of each read
+// phase fall on disjoint banks.  Staging is register-prefetched one chunk
+// ahead with double-buffered LDS.
 #pragma once
 
 #include <type_traits>
@@ -21,10 +22,6 @@
 #include "common.hpp"
 
 namespace vh {
-
-typedef __bf16 bf16;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 struct GemmDescBF16 {
     const void *A;      // fp32 or bf16 activations [M][lda]
@@ -35,21 +32,10 @@ struct GemmDescBF16 {
     int lda, ldb, ldc;
 };
 
-constexpr int GB_BM = 256, GB_BN = 128;
-constexpr int GB_THREADS = 256;
 constexpr int GB_MAX_BATCH = 64;
 struct GemmBatchBF16 {
     GemmDescBF16 d[GB_MAX_BATCH];
 };
-
-VH_DEVICE bf16x4 to_bf16x4(floatx4 v) {
-    bf16x4 r;
-    r[0] = (bf16)v[0];
-    r[1] = (bf16)v[1];
-    r[2] = (bf16)v[2];
-    r[3] = (bf16)v[3];
-    return r;
-}
 
 template <typename T>
 VH_DEVICE void store_out(T *p, float v) {
@@ -57,8 +43,16 @@ VH_DEVICE void store_out(T *p, float v) {
     else *p = (bf16)v;
 }
 
-template <int EPI, typename TA, typename TC, int BK>
+template <int WM, int WN, int FM, int FN>
+struct BF16Tile {
+    static constexpr int BM = 32 * WM * FM, BN = 32 * WN * FN, THREADS = 64 * WM * WN;
+};
+
+template <int EPI, typename TA, typename TC, int BK, int WM, int WN, int FM, int FN>
 __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) {
+    constexpr int GB_BM = BF16Tile<WM, WN, FM, FN>::BM, GB_BN = BF16Tile<WM, WN, FM, FN>::BN;
+    constexpr int GB_THREADS = BF16Tile<WM, WN, FM, FN>::THREADS;
+    static_assert(FN % 2 == 0 || EPI != EPI_GEGLU, "GELU-GLU needs value/gate column pairs per wave");
     constexpr int PITCH = BK + 8;
     constexpr bool A32 = std::is_same<TA, float>::value;
     constexpr int A_VEC = A32 ? 4 : 8;                      // elements per 16-byte load
@@ -85,7 +79,7 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
 
     const int tid = (int)threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int li = lane & 31, lh = lane >> 5;
 
     const int a_row = tid / A_CPR, a_c = tid % A_CPR;
@@ -135,11 +129,11 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
         for (int q = 0; q < B_PASSES; q++) *reinterpret_cast<bf16x8 *>(&Bs[buf][b_row + B_RPP * q][8 * b_c]) = rb[q];
     };
 
-    floatx16 acc[4][2];
+    floatx16 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
@@ -152,17 +146,17 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
         if (kt + 1 < nk) load((kt + 1) * BK);
 #pragma unroll
         for (int st = 0; st < BK / 16; st++) {
-            bf16x8 a[4], b[2];
+            bf16x8 a[FM], b[FN];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                a[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][wm * 128 + 32 * i + li][16 * st + 8 * lh]);
+            for (int i = 0; i < FM; i++)
+                a[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][wm * 32 * FM + 32 * i + li][16 * st + 8 * lh]);
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-                b[j] = *reinterpret_cast<const bf16x8 *>(&Bs[buf][wn * 64 + 32 * j + li][16 * st + 8 * lh]);
+            for (int j = 0; j < FN; j++)
+                b[j] = *reinterpret_cast<const bf16x8 *>(&Bs[buf][wn * 32 * FN + 32 * j + li][16 * st + 8 * lh]);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < FN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) store(buf ^ 1);
@@ -173,33 +167,37 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
     // holds row 8*(r/4) + 4*lh + r%4, column li.
     TC *C = static_cast<TC *>(d.C);
     if constexpr (EPI == EPI_GEGLU) {
-        const int nv = n0 + wn * 64 + li;
-        const int ng = nv + 32;
-        const int oc = (n0 + wn * 64) / 2 + li;
-        if (ng < d.N) {
+        // accumulator pair (2p, 2p+1) = value and gate columns of one 64-wide group
+#pragma unroll
+        for (int p = 0; p < FN / 2; p++) {
+            const int nv = n0 + wn * 32 * FN + 64 * p + li;
+            const int ng = nv + 32;
+            const int oc = (n0 + wn * 32 * FN + 64 * p) / 2 + li;
+            if (ng >= d.N) continue;
             const float bv = d.bias ? d.bias[nv] : 0.0f;
             const float bg = d.bias ? d.bias[ng] : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const int row = m0 + wm * 32 * FM + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                     if (row < d.M)
-                        store_out(C + (size_t)row * d.ldc + oc, (acc[i][0][r] + bv) * gelu_dev(acc[i][1][r] + bg));
+                        store_out(C + (size_t)row * d.ldc + oc,
+                                  (acc[i][2 * p][r] + bv) * gelu_dev(acc[i][2 * p + 1][r] + bg));
                 }
         }
     } else {
         static_assert(EPI != EPI_RESIDUAL || std::is_same<TC, float>::value, "residual output is fp32");
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int col = n0 + wn * 64 + j * 32 + li;
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + wn * 32 * FN + j * 32 + li;
             if (col >= d.N) continue;
             const float bc = d.bias ? d.bias[col] : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const int row = m0 + wm * 32 * FM + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                     if (row >= d.M) continue;
                     const float v = acc[i][j][r] + bc;
                     TC *p = C + (size_t)row * d.ldc + col;
@@ -212,14 +210,16 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
     }
 }
 
-template <int EPI, typename TA, typename TC, int BK>
-__global__ __launch_bounds__(GB_THREADS, 2) void gemm_bf16_kernel(GemmDescBF16 d) {
-    gemm_bf16_body<EPI, TA, TC, BK>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+// Second launch-bound argument: minimum waves per SIMD the register budget
+// must allow.
+template <int EPI, typename TA, typename TC, int BK, int WM, int WN, int FM, int FN, int OCC>
+__global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_kernel(GemmDescBF16 d) {
+    gemm_bf16_body<EPI, TA, TC, BK, WM, WN, FM, FN>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
-template <int EPI, typename TA, typename TC, int BK>
-__global__ __launch_bounds__(GB_THREADS, 2) void gemm_bf16_batched_kernel(GemmBatchBF16 b) {
-    gemm_bf16_body<EPI, TA, TC, BK>(b.d[blockIdx.z], (int)blockIdx.x);
+template <int EPI, typename TA, typename TC, int BK, int WM, int WN, int FM, int FN, int OCC>
+__global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_batched_kernel(GemmBatchBF16 b) {
+    gemm_bf16_body<EPI, TA, TC, BK, WM, WN, FM, FN>(b.d[blockIdx.z], (int)blockIdx.x);
 }
 
 // fp32 [rows][cols] -> bf16 [rows][ld] (weights at upload; padding untouched)

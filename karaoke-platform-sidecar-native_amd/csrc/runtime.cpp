@@ -194,38 +194,63 @@ bool gemm_batched(hipStream_t s, const std::vector<GemmArgs> &gs, int epilogue, 
 static bool gemm_bf16_ok(const GemmArgsBF16 &g, int epilogue) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2) return false;
     if (g.K % 4 || g.lda % 4 || g.lda < g.K || g.ldb % 8 || g.ldb < bf16_pitch(g.K)) return false;
+    if (g.a_bf16 && (g.K % 8 || g.lda % 8)) return false;
     if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
+    if (g.c_bf16 && epilogue == EPI_RESIDUAL) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.B) & 15) return false;
     return true;
 }
 
 static GemmDescBF16 to_desc_bf16(const GemmArgsBF16 &g) {
     GemmDescBF16 d;
-    d.A = g.A; d.B = static_cast<const bf16 *>(g.B); d.bias = g.bias; d.C = g.C;  // fp32 A and C
+    d.A = g.A; d.B = static_cast<const bf16 *>(g.B); d.bias = g.bias; d.C = g.C;
     d.M = (int)g.M; d.N = g.N; d.K = g.K;
     d.lda = g.lda; d.ldb = g.ldb; d.ldc = g.ldc;
     return d;
 }
 
+// bf16 GEMM tiling: 8 waves in a 4 x 2 grid, 2 x 2 accumulators (64 x 64) per
+// wave, a 256 x 128 block, K chunks of 32, 4 waves per SIMD (122 VGPRs).
+constexpr int BF_WM = 4, BF_WN = 2, BF_FM = 2, BF_FN = 2, BF_BK = 32, BF_OCC = 4;
+using BFTile = BF16Tile<BF_WM, BF_WN, BF_FM, BF_FN>;
+
 static int64_t tiles_bf16(const GemmArgsBF16 &g) {
-    return ((g.M + GB_BM - 1) / GB_BM) * ((g.N + GB_BN - 1) / GB_BN);
+    return ((g.M + BFTile::BM - 1) / BFTile::BM) * ((g.N + BFTile::BN - 1) / BFTile::BN);
+}
+
+template <int EPI, typename TA, typename TC>
+static void launch_bf16_typed(hipStream_t s, const GemmDescBF16 *single, const GemmBatchBF16 *batch, unsigned tiles,
+                              unsigned n) {
+    if (single)
+        hipLaunchKernelGGL((gemm_bf16_kernel<EPI, TA, TC, BF_BK, BF_WM, BF_WN, BF_FM, BF_FN, BF_OCC>), dim3(tiles),
+                           dim3(BFTile::THREADS), 0, s, *single);
+    else
+        hipLaunchKernelGGL((gemm_bf16_batched_kernel<EPI, TA, TC, BF_BK, BF_WM, BF_WN, BF_FM, BF_FN, BF_OCC>),
+                           dim3(tiles, 1, n), dim3(BFTile::THREADS), 0, s, *batch);
 }
 
 template <int EPI>
-static void launch_bf16_epi(hipStream_t s, const GemmDescBF16 *single, const GemmBatchBF16 *batch, unsigned tiles,
-                            unsigned n) {
-    if (single) hipLaunchKernelGGL((gemm_bf16_kernel<EPI, float, float, 32>), dim3(tiles), dim3(GB_THREADS), 0, s, *single);
-    else hipLaunchKernelGGL((gemm_bf16_batched_kernel<EPI, float, float, 32>), dim3(tiles, 1, n), dim3(GB_THREADS), 0, s, *batch);
+static void launch_bf16_epi(hipStream_t s, bool a16, bool c16, const GemmDescBF16 *single, const GemmBatchBF16 *batch,
+                            unsigned tiles, unsigned n) {
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (a16) launch_bf16_typed<EPI, bf16, float>(s, single, batch, tiles, n);
+        else launch_bf16_typed<EPI, float, float>(s, single, batch, tiles, n);
+    } else {
+        if (a16 && c16) launch_bf16_typed<EPI, bf16, bf16>(s, single, batch, tiles, n);
+        else if (a16) launch_bf16_typed<EPI, bf16, float>(s, single, batch, tiles, n);
+        else if (c16) launch_bf16_typed<EPI, float, bf16>(s, single, batch, tiles, n);
+        else launch_bf16_typed<EPI, float, float>(s, single, batch, tiles, n);
+    }
 }
 
-static bool launch_bf16(hipStream_t s, int epi, const GemmDescBF16 *single, const GemmBatchBF16 *batch,
-                        unsigned tiles, unsigned n) {
+static bool launch_bf16(hipStream_t s, int epi, bool a16, bool c16, const GemmDescBF16 *single,
+                        const GemmBatchBF16 *batch, unsigned tiles, unsigned n) {
     switch (epi) {
-        case EPI_STORE: launch_bf16_epi<EPI_STORE>(s, single, batch, tiles, n); break;
-        case EPI_GELU: launch_bf16_epi<EPI_GELU>(s, single, batch, tiles, n); break;
-        case EPI_TANH: launch_bf16_epi<EPI_TANH>(s, single, batch, tiles, n); break;
-        case EPI_RESIDUAL: launch_bf16_epi<EPI_RESIDUAL>(s, single, batch, tiles, n); break;
-        case EPI_GEGLU: launch_bf16_epi<EPI_GEGLU>(s, single, batch, tiles, n); break;
+        case EPI_STORE: launch_bf16_epi<EPI_STORE>(s, a16, c16, single, batch, tiles, n); break;
+        case EPI_GELU: launch_bf16_epi<EPI_GELU>(s, a16, c16, single, batch, tiles, n); break;
+        case EPI_TANH: launch_bf16_epi<EPI_TANH>(s, a16, c16, single, batch, tiles, n); break;
+        case EPI_RESIDUAL: launch_bf16_epi<EPI_RESIDUAL>(s, a16, c16, single, batch, tiles, n); break;
+        case EPI_GEGLU: launch_bf16_epi<EPI_GEGLU>(s, a16, c16, single, batch, tiles, n); break;
         default: set_error("unknown GEMM epilogue %d", epi); return false;
     }
     return sync_debug(s, "gemm_bf16_kernel");
@@ -239,7 +264,7 @@ bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *
     }
     GemmDescBF16 d = to_desc_bf16(g);
     Scope sc(t, s, name);
-    return launch_bf16(s, epilogue, &d, nullptr, (unsigned)tiles_bf16(g), 1);
+    return launch_bf16(s, epilogue, g.a_bf16, g.c_bf16, &d, nullptr, (unsigned)tiles_bf16(g), 1);
 }
 
 bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &gs, int epilogue, KernelTimer *t,
@@ -252,14 +277,17 @@ bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &gs, int e
         int64_t max_tiles = 0;
         for (size_t i = 0; i < count; i++) {
             const GemmArgsBF16 &g = gs[first + i];
-            if (!gemm_bf16_ok(g, epilogue)) {
-                set_error("gemm_bf16_batched: unsupported shape M=%lld N=%d K=%d", (long long)g.M, g.N, g.K);
+            if (!gemm_bf16_ok(g, epilogue) || g.a_bf16 != gs[first].a_bf16 || g.c_bf16 != gs[first].c_bf16) {
+                set_error("gemm_bf16_batched: unsupported shape M=%lld N=%d K=%d (or mixed operand types)",
+                          (long long)g.M, g.N, g.K);
                 return false;
             }
             b.d[i] = to_desc_bf16(g);
             max_tiles = std::max(max_tiles, tiles_bf16(g));
         }
-        if (!launch_bf16(s, epilogue, nullptr, &b, (unsigned)max_tiles, (unsigned)count)) return false;
+        if (!launch_bf16(s, epilogue, gs[first].a_bf16, gs[first].c_bf16, nullptr, &b, (unsigned)max_tiles,
+                         (unsigned)count))
+            return false;
     }
     return true;
 }
@@ -271,20 +299,31 @@ bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst
     return sync_debug(s, "to_bf16_kernel");
 }
 
-bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
-             KernelTimer *t) {
-    if (dim % 4 || dim > 2048 || rows <= 0) {
+template <typename TY>
+static bool rmsnorm_any(hipStream_t s, const float *x, int ldx, const float *gamma, TY *y, int ldy, int64_t rows,
+                        int dim, KernelTimer *t) {
+    if (dim % 4 || dim > 2048 || rows <= 0 || rows > INT32_MAX / 2) {
         set_error("rmsnorm: unsupported dim %d", dim);
         return false;
     }
     Scope sc(t, s, "rmsnorm");
     const unsigned grid = blocks_for(rows, 4);
     const int nv = dim / 4;
-    if (nv <= 64) hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
-    else if (nv <= 128) hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
-    else if (nv <= 256) hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
-    else hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    if (nv <= 64) hipLaunchKernelGGL((rmsnorm_kernel<1, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    else if (nv <= 128) hipLaunchKernelGGL((rmsnorm_kernel<2, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    else if (nv <= 256) hipLaunchKernelGGL((rmsnorm_kernel<4, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    else hipLaunchKernelGGL((rmsnorm_kernel<8, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
     return sync_debug(s, "rmsnorm_kernel");
+}
+
+bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
+             KernelTimer *t) {
+    return rmsnorm_any<float>(s, x, ldx, gamma, y, ldy, rows, dim, t);
+}
+
+bool rmsnorm_bf16(hipStream_t s, const float *x, int ldx, const float *gamma, void *y, int ldy, int64_t rows, int dim,
+                  KernelTimer *t) {
+    return rmsnorm_any<bf16>(s, x, ldx, gamma, static_cast<bf16 *>(y), ldy, rows, dim, t);
 }
 
 bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int len, KernelTimer *t) {
@@ -351,8 +390,8 @@ bool transpose_rows(hipStream_t s, const float *src, float *dst, int outer, int 
     return sync_debug(s, "transpose_rows_kernel");
 }
 
-bool attention(hipStream_t s, const float *qkv, int ld, float *out, int ld_out, const float *rope_cos,
-               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t) {
+bool attention(hipStream_t s, const float *qkv, int ld, void *out, int ld_out, const float *rope_cos,
+               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t, bool out_bf16) {
     if (lay.S <= 0 || lay.L <= 0 || ld % 4 || ld_out % 4) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
@@ -366,10 +405,12 @@ bool attention(hipStream_t s, const float *qkv, int ld, float *out, int ld_out, 
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
     if (lay.L <= 64) {
         const int64_t grid = (int64_t)lay.S * heads * ((lay.L + 63) / 64);
-        hipLaunchKernelGGL(attention_kernel<2>, dim3((unsigned)grid), dim3(128), 0, s, a);
+        if (out_bf16) hipLaunchKernelGGL((attention_kernel<2, bf16>), dim3((unsigned)grid), dim3(128), 0, s, a);
+        else hipLaunchKernelGGL((attention_kernel<2, float>), dim3((unsigned)grid), dim3(128), 0, s, a);
     } else {
         const int64_t grid = (int64_t)lay.S * heads * ((lay.L + 127) / 128);
-        hipLaunchKernelGGL(attention_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, a);
+        if (out_bf16) hipLaunchKernelGGL((attention_kernel<4, bf16>), dim3((unsigned)grid), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attention_kernel<4, float>), dim3((unsigned)grid), dim3(256), 0, s, a);
     }
     return sync_debug(s, "attention_kernel");
 }
@@ -455,29 +496,43 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     if (!rope.get(lay.L, d.dim_head, s, &cs, &sn)) return false;
     const int D = d.dim, inner = d.inner(), nq = d.qkvg_dim();
     float *normed = scr.normed.f(), *qkvg = scr.qkvg.f(), *attn = scr.attn.f(), *hid = scr.hidden.f();
-    // pre-norm -> fused QKV (+gate logits with their bias)
-    const bool h = precision == PREC_BF16;
-    if (h && !(w.wqkvg_h && w.wout_h && w.w1_h && w.w2_h)) {
-        set_error("transformer: bf16 weights not prepared");
-        return false;
+    const int gate = d.gated ? d.qkv_dim() : -1;
+    const int ff1_epi = d.ffn_glu ? EPI_GEGLU : EPI_GELU;
+    if (precision == PREC_BF16) {
+        // bf16 variant: the normalised activations, the attention output and the
+        // FFN hidden layer are stored as bf16 -- exactly the operands the GEMMs
+        // would round them to -- and the residual stream stays fp32.
+        if (!(w.wqkvg_h && w.wout_h && w.w1_h && w.w2_h)) {
+            set_error("transformer: bf16 weights not prepared");
+            return false;
+        }
+        auto lin = [&](const void *A, int lda, const void *Wh, const float *bias, void *C, int ldc, int N, int K,
+                       int epi, bool c16, const char *name) {
+            GemmArgsBF16 g{A, lda, Wh, bf16_pitch(K), bias, C, ldc, tokens, N, K};
+            g.a_bf16 = true;
+            g.c_bf16 = c16;
+            return gemm_bf16(s, g, epi, t, name);
+        };
+        if (!rmsnorm_bf16(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
+        if (!lin(normed, D, w.wqkvg_h, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, false, "gemm_qkv")) return false;
+        if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, gate, t, true)) return false;
+        if (!lin(attn, inner, w.wout_h, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;
+        if (!rmsnorm_bf16(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
+        if (!lin(normed, D, w.w1_h, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, true, "gemm_ff1")) return false;
+        return lin(hid, d.ff_dim, w.w2_h, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, false, "gemm_ff2");
     }
-    auto linear = [&](const float *A, int lda, const float *W, const void *Wh, const float *bias, float *C, int ldc,
-                      int N, int K, int epi, const char *name) {
-        if (h) return gemm_bf16(s, {A, lda, Wh, bf16_pitch(K), bias, C, ldc, tokens, N, K}, epi, t, name);
-        return gemm(s, {A, lda, W, K, bias, C, ldc, tokens, N, K}, epi, t, name);
-    };
+    // pre-norm -> fused QKV (+gate logits with their bias)
     if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
-    if (!linear(normed, D, w.wqkvg, w.wqkvg_h, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
+    if (!gemm(s, {normed, D, w.wqkvg, D, w.bqkvg, qkvg, nq, tokens, nq, D}, EPI_STORE, t, "gemm_qkv")) return false;
     // rotary + attention + gates
-    if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, d.gated ? d.qkv_dim() : -1, t)) return false;
+    if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, gate, t)) return false;
     // out projection added to the residual stream
-    if (!linear(attn, inner, w.wout, w.wout_h, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;
+    if (!gemm(s, {attn, inner, w.wout, inner, nullptr, x, D, tokens, D, inner}, EPI_RESIDUAL, t, "gemm_out")) return false;
     // FFN
     if (!rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
-    if (!linear(normed, D, w.w1, w.w1_h, w.b1, hid, d.ff_dim, d.ff1_out(), D, d.ffn_glu ? EPI_GEGLU : EPI_GELU,
-                "gemm_ff1"))
+    if (!gemm(s, {normed, D, w.w1, D, w.b1, hid, d.ff_dim, tokens, d.ff1_out(), D}, ff1_epi, t, "gemm_ff1")) return false;
+    if (!gemm(s, {hid, d.ff_dim, w.w2, d.ff_dim, w.b2, x, D, tokens, D, d.ff_dim}, EPI_RESIDUAL, t, "gemm_ff2"))
         return false;
-    if (!linear(hid, d.ff_dim, w.w2, w.w2_h, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, "gemm_ff2")) return false;
     return true;
 }
 

@@ -93,11 +93,12 @@ bool gemm_batched(hipStream_t s, const std::vector<GemmArgs> &g, int epilogue, K
 // bf16-MFMA variant: A fp32 (rounded to bf16 on the way into LDS), B a bf16
 // weight copy with row pitch ldb >= K rounded up to 8 and zero padding.
 struct GemmArgsBF16 {
-    const float *A; int lda;
+    const void *A; int lda;  // fp32, or bf16 when a_bf16 (then K and lda multiples of 8)
     const void *B; int ldb;  // bf16 [N][ldb]
     const float *bias;
-    float *C; int ldc;
+    void *C; int ldc;        // fp32, or bf16 when c_bf16 (not with the residual epilogue)
     int64_t M; int N, K;
+    bool a_bf16 = false, c_bf16 = false;
 };
 bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *t = nullptr,
                const char *name = "gemm_bf16");
@@ -109,6 +110,9 @@ inline int bf16_pitch(int k) { return (k + 7) & ~7; }
 
 bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
              KernelTimer *t = nullptr);
+// Same, bf16 output (y is bf16 [rows][ldy]).
+bool rmsnorm_bf16(hipStream_t s, const float *x, int ldx, const float *gamma, void *y, int ldy, int64_t rows, int dim,
+                  KernelTimer *t = nullptr);
 bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int len, KernelTimer *t = nullptr);
 bool rope_bhld(hipStream_t s, float *x, const float *cs, const float *sn, int64_t bh, int len,
                KernelTimer *t = nullptr);
@@ -123,8 +127,10 @@ struct AttnLayout {
     int S, L;
     int group, group_stride, seq_stride, pos_stride;
 };
-bool attention(hipStream_t s, const float *qkv, int ld, float *out, int ld_out, const float *rope_cos,
-               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t = nullptr);
+// out: fp32, or bf16 when out_bf16.
+bool attention(hipStream_t s, const float *qkv, int ld, void *out, int ld_out, const float *rope_cos,
+               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t = nullptr,
+               bool out_bf16 = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {

@@ -102,6 +102,11 @@ extern "C" int vh_rmsnorm(vh_context *ctx, int64_t rows, int dim, const float *x
     return rmsnorm(ctx->stream, x, dim, gamma, y, dim, rows, dim, &ctx->timer) ? 1 : 0;
 }
 
+extern "C" int vh_rmsnorm_bf16(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, void *y) {
+    if (!ctx) return 0;
+    return rmsnorm_bf16(ctx->stream, x, dim, gamma, y, dim, rows, dim, &ctx->timer) ? 1 : 0;
+}
+
 extern "C" int vh_softmax_rows(vh_context *ctx, int64_t rows, int len, const float *in, float *out) {
     if (!ctx) return 0;
     return softmax_rows(ctx->stream, in, out, rows, len, &ctx->timer) ? 1 : 0;
@@ -133,10 +138,13 @@ extern "C" int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A,
     return gemm(ctx->stream, {A, lda, W, ldw, bias, C, ldc, M, N, K}, epilogue, &ctx->timer, "gemm") ? 1 : 0;
 }
 
-extern "C" int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Wh, int ldw,
-                            const float *bias, float *C, int ldc, int epilogue) {
-    if (!ctx) return 0;
-    return gemm_bf16(ctx->stream, {A, lda, Wh, ldw, bias, C, ldc, M, N, K}, epilogue, &ctx->timer, "gemm_bf16") ? 1 : 0;
+extern "C" int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int lda, const void *Wh, int ldw,
+                            const float *bias, void *C, int ldc, int epilogue, int flags) {
+    if (!ctx || (flags & ~(VH_BF16_A | VH_BF16_C))) return 0;
+    GemmArgsBF16 g{A, lda, Wh, ldw, bias, C, ldc, M, N, K};
+    g.a_bf16 = (flags & VH_BF16_A) != 0;
+    g.c_bf16 = (flags & VH_BF16_C) != 0;
+    return gemm_bf16(ctx->stream, g, epilogue, &ctx->timer, "gemm_bf16") ? 1 : 0;
 }
 
 extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld) {
@@ -144,14 +152,14 @@ extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *
     return to_bf16_rows(ctx->stream, src, (int)rows, cols, dst, ld) ? 1 : 0;
 }
 
-extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, float *out,
-                            int apply_rotary) {
+extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, void *out,
+                            int apply_rotary, int out_bf16) {
     if (!ctx) return 0;
     const float *cs = nullptr, *sn = nullptr;
     if (apply_rotary && !ctx->rope.get(length, 64, ctx->stream, &cs, &sn)) return 0;
     const int inner = heads * 64;
     return attention(ctx->stream, qkv, 3 * inner, out, inner, cs, sn, contiguous_layout(sequences, length), heads, -1,
-                     &ctx->timer)
+                     &ctx->timer, out_bf16 != 0)
                ? 1
                : 0;
 }
@@ -371,7 +379,8 @@ bool prepare_bf16(vh_model *m) {
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(bf16 weights)");
 }
 
-// Batched token-wise linears of one pipeline stage in the model's precision.
+// Batched token-wise linears of one pipeline stage in the model's precision
+// (fp32 activations; the bf16 variant rounds them as they are staged).
 bool stage_gemms(vh_model *m, const std::vector<GemmArgs> &gs, const std::vector<void *> &wh, int epi,
                  const char *name) {
     if (m->precision != PREC_BF16) return gemm_batched(m->ctx->stream, gs, epi, &m->ctx->timer, name);
@@ -440,31 +449,58 @@ bool stage_band_split(vh_model *m, const float *source, int chunks, int T, float
     return stage_gemms(m, gs, m->band_w_h, EPI_STORE, "gemm_band_split");
 }
 
-// final-normed features (frame-major rows m*B + b) -> mask[chunks][F][C][T][2]
-bool stage_mask(vh_model *m, const float *normed, int chunks, int T, float *mask) {
+// final-normed features (frame-major rows m*B + b; fp32, or bf16 when
+// normed_bf16) -> mask[chunks][F][C][T][2]
+bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, int T, float *mask) {
     const Dims &d = m->d;
     hipStream_t s = m->ctx->stream;
     const int M = chunks * T, B = d.bands, D = d.dim, Hm = d.mask_hidden;
-    if (!m->mhidden.ensure((size_t)B * M * Hm * sizeof(float), "hipMalloc(mask hidden)") ||
+    const bool h = m->precision == PREC_BF16;
+    if (normed_bf16 && !h) {
+        set_error("mask estimator: bf16 features need the bf16 variant");
+        return false;
+    }
+    const size_t hid_elem = h ? 2 : 4, feat_elem = normed_bf16 ? 2 : 4;  // the bf16 hidden layer feeds layer 2 as is
+    if (!m->mhidden.ensure((size_t)B * M * Hm * hid_elem, "hipMalloc(mask hidden)") ||
         !m->proj.ensure((size_t)M * m->proj_total * sizeof(float), "hipMalloc(mask projection)") ||
         !m->tables.ensure(sizeof(BandTable) + sizeof(MaskTable), "hipMalloc(tables)"))
         return false;
     std::vector<GemmArgs> g1, g2;
+    std::vector<GemmArgsBF16> h1, h2;
     MaskTable tab;
     memset(&tab, 0, sizeof(tab));
     int64_t off = 0;
     for (int b = 0; b < B; b++) {
-        float *hid = m->mhidden.f() + (size_t)b * M * Hm;
-        g1.push_back({normed + (size_t)b * D, B * D, m->mask_w1[b], D, m->mask_b1[b], hid, Hm, M, Hm, D});
+        char *hid = static_cast<char *>(m->mhidden.ptr) + (size_t)b * M * Hm * hid_elem;
+        const char *feat = static_cast<const char *>(normed) + (size_t)b * D * feat_elem;
         const int out = 2 * d.in_dim(b);
-        g2.push_back({hid, Hm, m->mask_w2[b], Hm, m->mask_b2[b], m->proj.f() + off, out, M, out, Hm});
+        float *proj = m->proj.f() + off;
+        if (h) {
+            GemmArgsBF16 a{feat, B * D, m->mask_w1_h[b], bf16_pitch(D), m->mask_b1[b], hid, Hm, M, Hm, D};
+            a.a_bf16 = normed_bf16;
+            a.c_bf16 = true;
+            GemmArgsBF16 c{hid, Hm, m->mask_w2_h[b], bf16_pitch(Hm), m->mask_b2[b], proj, out, M, out, Hm};
+            c.a_bf16 = true;
+            h1.push_back(a);
+            h2.push_back(c);
+        } else {
+            g1.push_back({reinterpret_cast<const float *>(feat), B * D, m->mask_w1[b], D, m->mask_b1[b],
+                          reinterpret_cast<float *>(hid), Hm, M, Hm, D});
+            g2.push_back({reinterpret_cast<const float *>(hid), Hm, m->mask_w2[b], Hm, m->mask_b2[b], proj, out, M, out,
+                          Hm});
+        }
         tab.first_freq[b] = m->first_freq[b];
         tab.dim[b] = d.in_dim(b);
         tab.proj_offset[b] = off;
         off += (int64_t)M * out;
     }
-    if (!stage_gemms(m, g1, m->mask_w1_h, EPI_TANH, "gemm_mask1")) return false;
-    if (!stage_gemms(m, g2, m->mask_w2_h, EPI_STORE, "gemm_mask2")) return false;
+    KernelTimer *t = &m->ctx->timer;
+    if (h) {
+        if (!gemm_bf16_batched(s, h1, EPI_TANH, t, "gemm_mask1") || !gemm_bf16_batched(s, h2, EPI_STORE, t, "gemm_mask2"))
+            return false;
+    } else if (!gemm_batched(s, g1, EPI_TANH, t, "gemm_mask1") || !gemm_batched(s, g2, EPI_STORE, t, "gemm_mask2")) {
+        return false;
+    }
     MaskTable *dtab = reinterpret_cast<MaskTable *>(static_cast<char *>(m->tables.ptr) + sizeof(BandTable));
     if (!check(hipMemcpyAsync(dtab, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(mask table)")) return false;
     int maxdim = 0;
@@ -530,9 +566,13 @@ bool run_windows(vh_model *m, const float *audio, int64_t audio_len, const int64
     if (!stage_stft(m, audio, audio_len, starts_dev, sig_len, chunks, T, m->source.f())) return false;
     if (!stage_band_split(m, m->source.f(), chunks, T, m->x.f(), true)) return false;
     if (!stage_stack(m, m->x.f(), chunks, T)) return false;
-    if (!rmsnorm(m->ctx->stream, m->x.f(), d.dim, m->final_gamma, m->normed.f(), d.dim, tokens, d.dim, &m->ctx->timer))
+    const bool h = m->precision == PREC_BF16;
+    if (h ? !rmsnorm_bf16(m->ctx->stream, m->x.f(), d.dim, m->final_gamma, m->normed.ptr, d.dim, tokens, d.dim,
+                          &m->ctx->timer)
+          : !rmsnorm(m->ctx->stream, m->x.f(), d.dim, m->final_gamma, m->normed.f(), d.dim, tokens, d.dim,
+                     &m->ctx->timer))
         return false;
-    if (!stage_mask(m, m->normed.f(), chunks, T, m->mask.f())) return false;
+    if (!stage_mask(m, m->normed.ptr, h, chunks, T, m->mask.f())) return false;
     return stage_istft(m, m->source.f(), m->mask.f(), chunks, T, sig_len, out, pitch);
 }
 
@@ -597,7 +637,7 @@ extern "C" int vh_band_split(vh_context *ctx, vh_model *m, const float *source, 
 
 extern "C" int vh_mask_estimate(vh_context *ctx, vh_model *m, const float *features, int frames, float *mask) {
     if (!ctx || !m || frames <= 0) return 0;
-    return stage_mask(m, features, 1, frames, mask) ? 1 : 0;
+    return stage_mask(m, features, false, 1, frames, mask) ? 1 : 0;
 }
 
 extern "C" int vh_forward(vh_context *ctx, vh_model *m, const float *audio, int length, float *vocals,

@@ -130,20 +130,21 @@ def main() -> int:
             del a, w, b, c
 
     if "bf16" in groups:
-        # the same four GEMMs on bf16 matrix-core operands (fp32 activations
-        # rounded on the way into LDS, bf16 weight copies)
+        # the same four GEMMs on bf16 matrix-core operands, with the operand
+        # types of the bf16 pipeline: bf16 activations in, bf16 FFN hidden out
         M = 8 * 801 * 62
-        for name, K, N, epi, ocols in (("gemm_bf16_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
-                                       ("gemm_bf16_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
-                                       ("gemm_bf16_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
-                                       ("gemm_bf16_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384)):
-            a = torch.randn(M, K, device=dev, generator=g)
+        for name, K, N, epi, ocols, c16 in (("gemm_bf16_qkv_gates", 384, 1568, native.EPI_STORE, 1568, False),
+                                            ("gemm_bf16_out_residual", 512, 384, native.EPI_RESIDUAL, 384, False),
+                                            ("gemm_bf16_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536, True),
+                                            ("gemm_bf16_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384, False)):
+            a = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
             wh = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
             ctx.to_bf16(w, wh, N, K, K)
             b = torch.randn(N, device=dev, generator=g)
-            c = torch.zeros(M, ocols, device=dev)
-            _emit(name, _event_time(lambda: ctx.gemm_bf16(a, wh, c, M, N, K, K, bias=b, epilogue=epi),
+            c = torch.zeros(M, ocols, device=dev, dtype=torch.bfloat16 if c16 else torch.float32)
+            flags = native.BF16_A | (native.BF16_C if c16 else 0)
+            _emit(name, _event_time(lambda: ctx.gemm_bf16(a, wh, c, M, N, K, K, bias=b, epilogue=epi, flags=flags),
                                     max(3, reps // 4)),
                   gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=BF16_TFLOPS)
             del a, w, wh, b, c

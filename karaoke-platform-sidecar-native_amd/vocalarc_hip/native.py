@@ -19,7 +19,7 @@ LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
 # Every entry point declared in include/vocalarc_hip.h and include/native_gpu.h.
 HARNESS_SYMBOLS = [
     "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
-    "vh_rmsnorm", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
+    "vh_rmsnorm", "vh_rmsnorm_bf16", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
     "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
     "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
 ]
@@ -32,6 +32,7 @@ ABI_SYMBOLS = [
 
 EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16 = 0, 1
+BF16_A, BF16_C = 1, 2  # vh_gemm_bf16 operand flags
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -54,15 +55,15 @@ def lib():
     sig = {
         "vh_create": (_P, []), "vh_destroy": (None, [_P]), "vh_set_stream": (_I, [_P, _P]),
         "vh_synchronize": (_I, [_P]), "vh_last_error": (ctypes.c_char_p, []), "vh_device_name": (ctypes.c_char_p, [_P]),
-        "vh_rmsnorm": (_I, [_P, _I64, _I, _P, _P, _P]),
+        "vh_rmsnorm": (_I, [_P, _I64, _I, _P, _P, _P]), "vh_rmsnorm_bf16": (_I, [_P, _I64, _I, _P, _P, _P]),
         "vh_softmax_rows": (_I, [_P, _I64, _I, _P, _P]),
         "vh_rope_bhld": (_I, [_P, _I64, _I, _I, _P]),
         "vh_geglu": (_I, [_P, _I64, _I, _P, _P]),
         "vh_residual_add": (_I, [_P, _I64, _P, _P]),
         "vh_gemm": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
-        "vh_gemm_bf16": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
+        "vh_gemm_bf16": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I, _I]),
         "vh_to_bf16": (_I, [_P, _I64, _I, _P, _P, _I]),
-        "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I]),
+        "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
         "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
         "vh_model_free": (None, [_P]), "vh_model_set_precision": (_I, [_P, _I]),
         "vh_transformer": (_I, [_P, _P, _I, _I, _P, _I, _I]),
@@ -147,6 +148,9 @@ class Context:
     def rmsnorm(self, x, gamma, y, rows: int, dim: int):
         _ok(lib().vh_rmsnorm(self.h, rows, dim, ptr(x), ptr(gamma), ptr(y)), "vh_rmsnorm")
 
+    def rmsnorm_bf16(self, x, gamma, y, rows: int, dim: int):
+        _ok(lib().vh_rmsnorm_bf16(self.h, rows, dim, ptr(x), ptr(gamma), ptr(y)), "vh_rmsnorm_bf16")
+
     def softmax_rows(self, x, y, rows: int, length: int):
         _ok(lib().vh_softmax_rows(self.h, rows, length, ptr(x), ptr(y)), "vh_softmax_rows")
 
@@ -166,17 +170,18 @@ class Context:
                           ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm")
 
     def gemm_bf16(self, A, Wh, C, M: int, N: int, K: int, ldw: int, bias=None, epilogue: int = EPI_STORE,
-                  lda: int | None = None, ldc: int | None = None):
-        """Wh: bf16 weight copy [N][ldw] (see to_bf16)."""
+                  lda: int | None = None, ldc: int | None = None, flags: int = 0):
+        """Wh: bf16 weight copy [N][ldw] (see to_bf16); flags: BF16_A / BF16_C operand types."""
         _ok(lib().vh_gemm_bf16(self.h, M, N, K, ptr(A), lda or K, ptr(Wh), ldw,
                                ptr(bias) if bias is not None else None, ptr(C),
-                               ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm_bf16")
+                               ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue, flags), "vh_gemm_bf16")
 
     def to_bf16(self, src, dst, rows: int, cols: int, ld: int):
         _ok(lib().vh_to_bf16(self.h, rows, cols, ptr(src), ptr(dst), ld), "vh_to_bf16")
 
-    def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True):
-        _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary)), "vh_attention")
+    def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True, out_bf16: bool = False):
+        _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), int(out_bf16)),
+            "vh_attention")
 
     # -- timing --
     def timing(self, classes: str | None = "*"):

@@ -126,6 +126,70 @@ def test_gemm_bf16_geglu_epilogue(ctx, rng):
     assert_close(ref, from_dev(dc), rtol=1e-5, atol=2e-5, what="gemm_bf16 GELU-GLU")
 
 
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_gemm_bf16_operand_types_exact(ctx, rng, epi):
+    """bf16 A in memory == fp32 A rounded at staging (bit for bit), and a bf16
+    output == the fp32 output rounded to nearest even (bit for bit)."""
+    M, N, K = 700, 384, 512
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    b = to_dev(rng.standard_normal(N).astype(np.float32))
+    wh, ld = _dev_bf16(ctx, w)
+    cols = N // 2 if epi == native.EPI_GEGLU else N
+    c0 = rng.standard_normal((M, cols), dtype=np.float32)
+    dx = to_dev(x)
+    xh = torch.empty(M, K, dtype=torch.bfloat16, device="cuda:0")
+    ctx.to_bf16(dx, xh, M, K, K)
+    c32 = to_dev(c0)
+    ctx.gemm_bf16(dx, wh, c32, M, N, K, ld, bias=b, epilogue=epi)
+    c32a = to_dev(c0)
+    ctx.gemm_bf16(xh, wh, c32a, M, N, K, ld, bias=b, epilogue=epi, flags=native.BF16_A)
+    torch.cuda.synchronize()
+    assert torch.equal(c32.view(torch.int32), c32a.view(torch.int32)), "bf16 A must equal fp32 A rounded at staging"
+    if epi == native.EPI_RESIDUAL:
+        with pytest.raises(native.NativeError, match="unsupported shape"):
+            ctx.gemm_bf16(xh, wh, torch.empty(M, cols, dtype=torch.bfloat16, device="cuda:0"), M, N, K, ld,
+                          bias=b, epilogue=epi, flags=native.BF16_A | native.BF16_C)
+        return
+    for flags, a in ((native.BF16_C, dx), (native.BF16_A | native.BF16_C, xh)):
+        c16 = torch.empty(M, cols, dtype=torch.bfloat16, device="cuda:0")
+        ctx.gemm_bf16(a, wh, c16, M, N, K, ld, bias=b, epilogue=epi, flags=flags)
+        torch.cuda.synchronize()
+        assert torch.equal(c16.view(torch.int16), c32.to(torch.bfloat16).view(torch.int16)), f"flags {flags}"
+
+
+def test_gemm_bf16_operand_alignment_checks(ctx):
+    wh = torch.zeros(64, 24, dtype=torch.bfloat16, device="cuda:0")
+    xh = torch.zeros(8, 20, dtype=torch.bfloat16, device="cuda:0")
+    c = torch.zeros(8, 64, device="cuda:0")
+    with pytest.raises(native.NativeError, match="unsupported shape"):
+        ctx.gemm_bf16(xh, wh, c, 8, 64, 20, 24, flags=native.BF16_A)  # bf16 A needs K % 8 == 0
+
+
+def test_rmsnorm_bf16_is_rounded_fp32(ctx, rng):
+    rows, dim = 1234, 384
+    x = to_dev(rng.standard_normal((rows, dim), dtype=np.float32))
+    g = to_dev((1 + 0.02 * rng.standard_normal(dim)).astype(np.float32))
+    y = torch.empty(rows, dim, device="cuda:0")
+    yh = torch.empty(rows, dim, dtype=torch.bfloat16, device="cuda:0")
+    ctx.rmsnorm(x, g, y, rows, dim)
+    ctx.rmsnorm_bf16(x, g, yh, rows, dim)
+    torch.cuda.synchronize()
+    assert torch.equal(yh.view(torch.int16), y.to(torch.bfloat16).view(torch.int16))
+
+
+@pytest.mark.parametrize("S,L", [(3, 130), (40, 62)])
+def test_attention_bf16_out_is_rounded_fp32(ctx, rng, S, L):
+    H = 8
+    qkv = to_dev(rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32))
+    o = torch.empty(S * L, H * 64, device="cuda:0")
+    oh = torch.empty(S * L, H * 64, dtype=torch.bfloat16, device="cuda:0")
+    ctx.attention(qkv, o, S, L, H, True)
+    ctx.attention(qkv, oh, S, L, H, True, out_bf16=True)
+    torch.cuda.synchronize()
+    assert torch.equal(oh.view(torch.int16), o.to(torch.bfloat16).view(torch.int16))
+
+
 def test_gemm_bf16_rejects_bad_pitch(ctx):
     x = torch.zeros(8, 20, device="cuda:0")
     wh = torch.zeros(8, 20, dtype=torch.bfloat16, device="cuda:0")
