@@ -82,10 +82,14 @@ int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int ld
 /* fp32 src[rows][cols] -> bf16 dst[rows][ld] (round to nearest even). */
 int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld);
 /* Fused attention core over qkv[S*L][3*H*64] (rotary applied here):
-   native/vocalarc_separation.c:692-793.  out[S*L][H*64], fp32 or (out_bf16)
-   bf16 rounded to nearest even. */
-int vh_attention(vh_context *ctx, int sequences, int length, int heads, const float *qkv, void *out,
-                 int apply_rotary, int out_bf16);
+   native/vocalarc_separation.c:692-793.  out[S*L][H*64].  flags:
+   VH_ATT_OUT_BF16 writes out as bf16 (round to nearest even); VH_ATT_BF16
+   takes qkv as bf16 and runs the bf16-MFMA kernel (q, k, v and the
+   probabilities as bf16 operands, fp32 softmax statistics). */
+#define VH_ATT_OUT_BF16 1
+#define VH_ATT_BF16 2
+int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
+                 int apply_rotary, int flags);
 
 /* ---- model -------------------------------------------------------------- */
 /* Upload a VSCNAT01 pack (native/vocalarc_separation.c:528-589) laid out for

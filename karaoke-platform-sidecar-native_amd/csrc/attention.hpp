@@ -29,7 +29,7 @@
 namespace vh {
 
 struct AttnArgs {
-    const float *qkv;  // fused projection rows
+    const void *qkv;   // fused projection rows (fp32, or bf16 for the bf16 kernel)
     int ld;            // row pitch of qkv (floats)
     void *out;         // [rows][ld_out] fp32 or bf16, head h at column h*64
     int ld_out;
@@ -79,6 +79,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float Ks[2][ATT_KB][ATT_KPITCH];
     __shared__ __attribute__((aligned(16))) float Vt[2][ATT_DH][ATT_VPITCH];
 
+    const float *qkv = static_cast<const float *>(a.qkv);
     const int qgroups = (a.L + 32 * WAVES - 1) / (32 * WAVES);
     const int task = (int)blockIdx.x;
     const int qg = task % qgroups;
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     floatx4 qr[8];
     {
         const int q = min(q0 + li, a.L - 1);
-        const float *qp = a.qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+        const float *qp = qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
         const float qs = a.scale * 1.4426950408889634f;
 #pragma unroll
         for (int g = 0; g < 8; g++) {
@@ -123,8 +124,8 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
             const int p = kb * ATT_KB + kk;
             if (p < a.L) {
                 const size_t row = (size_t)attn_row(a, s, p) * a.ld;
-                kreg[i] = rope4(ld4(a.qkv + row + kcol + d0), a.rope_cos, a.rope_sin, p, d0);
-                vreg[i] = ld4(a.qkv + row + vcol + d0);
+                kreg[i] = rope4(ld4(qkv + row + kcol + d0), a.rope_cos, a.rope_sin, p, d0);
+                vreg[i] = ld4(qkv + row + vcol + d0);
             } else {
                 kreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
                 vreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     const float inv = 1.0f / l_tot;
     const int row = attn_row(a, s, q);
     float gate = 1.0f;
-    if (a.gate_col >= 0) gate = sigmoid_dev(a.qkv[(size_t)row * a.ld + a.gate_col + h]);
+    if (a.gate_col >= 0) gate = sigmoid_dev(qkv[(size_t)row * a.ld + a.gate_col + h]);
     TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
 #pragma unroll
     for (int t = 0; t < 2; t++)

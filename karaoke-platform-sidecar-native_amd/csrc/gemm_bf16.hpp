@@ -210,8 +210,8 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
     }
 }
 
-// Second launch-bound argument: minimum waves per SIMD the register budget
-// must allow.
+// Second launch-bound argument: workgroups per CU the register budget must
+// allow (OCC * waves per workgroup / 4 waves per SIMD).
 template <int EPI, typename TA, typename TC, int BK, int WM, int WN, int FM, int FN, int OCC>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_kernel(GemmDescBF16 d) {
     gemm_bf16_body<EPI, TA, TC, BK, WM, WN, FM, FN>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));

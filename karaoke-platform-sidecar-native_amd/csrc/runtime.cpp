@@ -10,6 +10,7 @@
 #include <mutex>
 
 #include "attention.hpp"
+#include "attention_bf16.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
 #include "gemm_bf16.hpp"
@@ -210,8 +211,9 @@ static GemmDescBF16 to_desc_bf16(const GemmArgsBF16 &g) {
 }
 
 // bf16 GEMM tiling: 8 waves in a 4 x 2 grid, 2 x 2 accumulators (64 x 64) per
-// wave, a 256 x 128 block, K chunks of 32, 4 waves per SIMD (122 VGPRs).
-constexpr int BF_WM = 4, BF_WN = 2, BF_FM = 2, BF_FN = 2, BF_BK = 32, BF_OCC = 4;
+// wave, a 256 x 128 block, K chunks of 32; two workgroups per CU (60 KB of LDS
+// each) = 4 waves per SIMD (122 VGPRs).
+constexpr int BF_WM = 4, BF_WN = 2, BF_FM = 2, BF_FN = 2, BF_BK = 32, BF_OCC = 2;
 using BFTile = BF16Tile<BF_WM, BF_WN, BF_FM, BF_FN>;
 
 static int64_t tiles_bf16(const GemmArgsBF16 &g) {
@@ -390,9 +392,22 @@ bool transpose_rows(hipStream_t s, const float *src, float *dst, int outer, int 
     return sync_debug(s, "transpose_rows_kernel");
 }
 
-bool attention(hipStream_t s, const float *qkv, int ld, void *out, int ld_out, const float *rope_cos,
-               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t, bool out_bf16) {
-    if (lay.S <= 0 || lay.L <= 0 || ld % 4 || ld_out % 4) {
+template <int WAVES>
+static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bool out_bf16, bool qkv_bf16) {
+    const dim3 block(64 * WAVES);
+    if (qkv_bf16) {
+        if (out_bf16) hipLaunchKernelGGL((attention_bf16_kernel<WAVES, bf16>), dim3(grid), block, 0, s, a);
+        else hipLaunchKernelGGL((attention_bf16_kernel<WAVES, float>), dim3(grid), block, 0, s, a);
+    } else {
+        if (out_bf16) hipLaunchKernelGGL((attention_kernel<WAVES, bf16>), dim3(grid), block, 0, s, a);
+        else hipLaunchKernelGGL((attention_kernel<WAVES, float>), dim3(grid), block, 0, s, a);
+    }
+}
+
+bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope_cos,
+               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t, bool out_bf16,
+               bool qkv_bf16) {
+    if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
     }
@@ -403,15 +418,8 @@ bool attention(hipStream_t s, const float *qkv, int ld, void *out, int ld_out, c
     a.group = lay.group; a.group_stride = lay.group_stride; a.seq_stride = lay.seq_stride; a.pos_stride = lay.pos_stride;
     a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
-    if (lay.L <= 64) {
-        const int64_t grid = (int64_t)lay.S * heads * ((lay.L + 63) / 64);
-        if (out_bf16) hipLaunchKernelGGL((attention_kernel<2, bf16>), dim3((unsigned)grid), dim3(128), 0, s, a);
-        else hipLaunchKernelGGL((attention_kernel<2, float>), dim3((unsigned)grid), dim3(128), 0, s, a);
-    } else {
-        const int64_t grid = (int64_t)lay.S * heads * ((lay.L + 127) / 128);
-        if (out_bf16) hipLaunchKernelGGL((attention_kernel<4, bf16>), dim3((unsigned)grid), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((attention_kernel<4, float>), dim3((unsigned)grid), dim3(256), 0, s, a);
-    }
+    if (lay.L <= 64) launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16);
+    else launch_attention<4>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 127) / 128)), out_bf16, qkv_bf16);
     return sync_debug(s, "attention_kernel");
 }
 
@@ -499,9 +507,9 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     const int gate = d.gated ? d.qkv_dim() : -1;
     const int ff1_epi = d.ffn_glu ? EPI_GEGLU : EPI_GELU;
     if (precision == PREC_BF16) {
-        // bf16 variant: the normalised activations, the attention output and the
-        // FFN hidden layer are stored as bf16 -- exactly the operands the GEMMs
-        // would round them to -- and the residual stream stays fp32.
+        // bf16 variant: the normalised activations, the fused projection, the
+        // attention output and the FFN hidden layer are stored as bf16 -- the
+        // operands the matrix cores take -- and the residual stream stays fp32.
         if (!(w.wqkvg_h && w.wout_h && w.w1_h && w.w2_h)) {
             set_error("transformer: bf16 weights not prepared");
             return false;
@@ -514,8 +522,8 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
             return gemm_bf16(s, g, epi, t, name);
         };
         if (!rmsnorm_bf16(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
-        if (!lin(normed, D, w.wqkvg_h, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, false, "gemm_qkv")) return false;
-        if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, gate, t, true)) return false;
+        if (!lin(normed, D, w.wqkvg_h, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, true, "gemm_qkv")) return false;
+        if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, gate, t, true, true)) return false;
         if (!lin(attn, inner, w.wout_h, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;
         if (!rmsnorm_bf16(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
         if (!lin(normed, D, w.w1_h, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, true, "gemm_ff1")) return false;

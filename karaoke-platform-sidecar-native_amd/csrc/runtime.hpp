@@ -127,10 +127,11 @@ struct AttnLayout {
     int S, L;
     int group, group_stride, seq_stride, pos_stride;
 };
-// out: fp32, or bf16 when out_bf16.
-bool attention(hipStream_t s, const float *qkv, int ld, void *out, int ld_out, const float *rope_cos,
+// qkv fp32 (fp32 MFMA) or, with qkv_bf16, bf16 (bf16 MFMA); out fp32, or bf16
+// when out_bf16.
+bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope_cos,
                const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t = nullptr,
-               bool out_bf16 = false);
+               bool out_bf16 = false, bool qkv_bf16 = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {

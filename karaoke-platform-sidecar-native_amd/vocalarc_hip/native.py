@@ -33,6 +33,7 @@ ABI_SYMBOLS = [
 EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16 = 0, 1
 BF16_A, BF16_C = 1, 2  # vh_gemm_bf16 operand flags
+ATT_OUT_BF16, ATT_BF16 = 1, 2  # vh_attention flags
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -179,8 +180,11 @@ class Context:
     def to_bf16(self, src, dst, rows: int, cols: int, ld: int):
         _ok(lib().vh_to_bf16(self.h, rows, cols, ptr(src), ptr(dst), ld), "vh_to_bf16")
 
-    def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True, out_bf16: bool = False):
-        _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), int(out_bf16)),
+    def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True, out_bf16: bool = False,
+                  bf16: bool = False):
+        """bf16: qkv is bf16 and the bf16-MFMA kernel runs; out_bf16: out is bf16."""
+        flags = (ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0)
+        _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), flags),
             "vh_attention")
 
     # -- timing --

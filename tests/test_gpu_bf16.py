@@ -190,6 +190,81 @@ def test_attention_bf16_out_is_rounded_fp32(ctx, rng, S, L):
     assert torch.equal(oh.view(torch.int16), o.to(torch.bfloat16).view(torch.int16))
 
 
+def _emulate_bf16_attention(qkv, S, L, H):
+    """float64 statement of the bf16 attention kernel's algorithm: q and k
+    rotated in fp32 and rounded to bf16 (q scaled by 0.125*log2 e first), keys
+    in blocks of 32 with the online softmax in the exp2 domain, probabilities
+    rounded to bf16 for the P*V product, fp32-exact sums in float64."""
+    cs, sn = O.rope_table(L, 64)
+    qs = np.float32(0.125 * 1.4426950408889634)
+
+    def rot(x):
+        x0, x1 = x[:, 0::2], x[:, 1::2]
+        r = np.empty_like(x)
+        r[:, 0::2] = x0 * cs - x1 * sn
+        r[:, 1::2] = x0 * sn + x1 * cs
+        return r
+
+    inner = H * 64
+    out = np.empty((S * L, inner), np.float64)
+    for s in range(S):
+        rows = slice(s * L, (s + 1) * L)
+        for h in range(H):
+            c = slice(h * 64, (h + 1) * 64)
+            q = qkv[rows, c]
+            k = qkv[rows, inner + h * 64:inner + (h + 1) * 64]
+            v = qkv[rows, 2 * inner + h * 64:2 * inner + (h + 1) * 64].astype(np.float64)
+            qr = _round_bf16(rot(q) * qs).astype(np.float64)
+            kr = _round_bf16(rot(k)).astype(np.float64)
+            m = np.full(L, -np.inf)
+            l = np.zeros(L)
+            o = np.zeros((L, 64))
+            for k0 in range(0, L, 32):
+                sc = qr @ kr[k0:k0 + 32].T
+                m_new = np.maximum(m, sc.max(axis=1))
+                alpha = np.exp2(m - m_new)
+                p = np.exp2(sc - m_new[:, None])
+                l = l * alpha + p.sum(axis=1)
+                o = o * alpha[:, None] + _round_bf16(p.astype(np.float32)).astype(np.float64) @ v[k0:k0 + 32]
+                m = m_new
+            out[rows, c] = o / l[:, None]
+    return out
+
+
+@pytest.mark.parametrize("S,L", [(3, 130), (40, 62), (2, 801)])
+def test_attention_bf16_kernel(ctx, rng, S, L):
+    H = 8
+    qkv = _round_bf16(rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32))
+    ref = _emulate_bf16_attention(qkv, S, L, H)
+    dq = torch.from_numpy(qkv).to("cuda:0").to(torch.bfloat16)
+    o = torch.empty(S * L, H * 64, device="cuda:0")
+    ctx.attention(dq, o, S, L, H, True, bf16=True)
+    out = from_dev(o)
+    # Differences from the emulation: fp32 summation order of the scores, the
+    # device exp2, and FMA contraction in the rotation -- each can move a value
+    # that sits on a bf16 rounding tie to the neighbouring bf16 value (a
+    # relative step of 2^-8 in one q, k or p).  So: almost every element
+    # within a tight bound, and the rare flips bounded.
+    err = np.abs(out.astype(np.float64) - ref)
+    tight = err <= 2e-4 + 2e-3 * np.abs(ref)
+    emu_snr = snr_db(ref, out)
+    print(f"bf16 attention S={S} L={L}: SNR {emu_snr:.1f} dB vs the emulated bf16 algorithm, "
+          f"{int((~tight).sum())} of {err.size} beyond the tight bound, max |d| {err.max():.2e}")
+    # (the same output is only ~51 dB from exact fp32 attention, so 75 dB
+    # against the emulation discriminates the algorithm)
+    assert tight.mean() >= 0.999
+    assert err.max() <= 4e-3
+    assert emu_snr >= 75
+    # the exact fp32 attention on the same (bf16-valued) inputs differs by the bf16 roundings
+    from test_gpu_kernels import _rotate_qk
+    ref32 = O.attention(REFERENCE_DIMS, _rotate_qk(qkv, L, H), S, L)
+    print(f"bf16 attention S={S} L={L}: SNR {snr_db(ref32, out):.1f} dB vs fp32 attention on the same inputs")
+    oh = torch.empty(S * L, H * 64, dtype=torch.bfloat16, device="cuda:0")
+    ctx.attention(dq, oh, S, L, H, True, out_bf16=True, bf16=True)
+    torch.cuda.synchronize()
+    assert torch.equal(oh.view(torch.int16), o.to(torch.bfloat16).view(torch.int16))
+
+
 def test_gemm_bf16_rejects_bad_pitch(ctx):
     x = torch.zeros(8, 20, device="cuda:0")
     wh = torch.zeros(8, 20, dtype=torch.bfloat16, device="cuda:0")
