@@ -33,8 +33,7 @@ struct AttnArgs {
     int ld;            // row pitch of qkv (floats)
     void *out;         // [rows][ld_out] fp32 or bf16, head h at column h*64
     int ld_out;
-    const float *rope_cos;  // [L][32], may be null (no rotary)
-    const float *rope_sin;
+    const float *rope;  // [L][32][2] (cos, sin) pairs, may be null (no rotary)
     int S, L, H;
     int group, group_stride, seq_stride, pos_stride;
     int inner;      // H * 64
@@ -51,11 +50,12 @@ VH_DEVICE int attn_row(const AttnArgs &a, int s, int p) {
     return (s / a.group) * a.group_stride + (s % a.group) * a.seq_stride + p * a.pos_stride;
 }
 
-// Rotate the two interleaved pairs of a float4 that starts at dimension d0.
-VH_DEVICE floatx4 rope4(floatx4 v, const float *cs, const float *sn, int pos, int d0) {
-    if (cs == nullptr) return v;
-    const int pi = pos * (ATT_DH / 2) + (d0 >> 1);
-    float c0 = cs[pi], s0 = sn[pi], c1 = cs[pi + 1], s1 = sn[pi + 1];
+// Rotate the two interleaved pairs of a float4 that starts at dimension d0
+// (one 16-byte table load: cos and sin of both pairs).
+VH_DEVICE floatx4 rope4(floatx4 v, const float *tab, int pos, int d0) {
+    if (tab == nullptr) return v;
+    const floatx4 t = ld4(tab + pos * ATT_DH + d0);
+    const float c0 = t[0], s0 = t[1], c1 = t[2], s1 = t[3];
     floatx4 r;
     r[0] = v[0] * c0 - v[1] * s0;
     r[1] = v[0] * s0 + v[1] * c0;
@@ -70,6 +70,35 @@ VH_DEVICE floatx4 rope4(floatx4 v, const float *cs, const float *sn, int pos, in
 // loads key e%16 (+16 for e >= 256) and 16-byte chunk (e/16)%16 of that key's
 // 64 dims, which makes both the K row writes and the V column writes
 // bank-conflict free.
+// One 32-key block of the online softmax for the lane's query: sc holds its
+// scores (log2 domain) on entry and the unnormalised probabilities on exit.
+// The running maximum is raised only when a block exceeds it by more than
+// 2^8 (a factor the fp32 sums absorb exactly), so the rescale of the
+// accumulators -- 34 multiplies -- runs on a few blocks per row instead of
+// every one; o / l is unchanged.  The branch is taken by the whole wave.
+VH_DEVICE void online_softmax_block(floatx16 &sc, float &m_run, float &l_run, floatx16 (&o)[2]) {
+    float mb = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
+    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+    const bool grow = mb > m_run + 8.0f;
+    if (__ballot(grow)) {
+        const float m_new = grow ? mb : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+        o[0] *= alpha;
+        o[1] *= alpha;
+        m_run = m_new;
+    }
+    float ls = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_run);
+        ls += sc[r];
+    }
+    l_run += ls;
+}
+
 template <int WAVES, typename TO>
 __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     constexpr int NT = 64 * WAVES;
@@ -99,14 +128,16 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     // Q for query q0+li, dims 8g + 4lh .. +3, rotated, then scaled by
     // scale*log2(e) so the scores come out in the base-2 exponent domain.
     floatx4 qr[8];
+    float gate_logit = 0.0f;  // loaded with Q so the store does not wait on it
     {
         const int q = min(q0 + li, a.L - 1);
         const float *qp = qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+        if (a.gate_col >= 0) gate_logit = qkv[(size_t)attn_row(a, s, q) * a.ld + a.gate_col + h];
         const float qs = a.scale * 1.4426950408889634f;
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             const int d0 = 8 * g + 4 * lh;
-            qr[g] = rope4(ld4(qp + d0), a.rope_cos, a.rope_sin, q, d0) * qs;
+            qr[g] = rope4(ld4(qp + d0), a.rope, q, d0) * qs;
         }
     }
 
@@ -124,7 +155,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
             const int p = kb * ATT_KB + kk;
             if (p < a.L) {
                 const size_t row = (size_t)attn_row(a, s, p) * a.ld;
-                kreg[i] = rope4(ld4(qkv + row + kcol + d0), a.rope_cos, a.rope_sin, p, d0);
+                kreg[i] = rope4(ld4(qkv + row + kcol + d0), a.rope, p, d0);
                 vreg[i] = ld4(qkv + row + vcol + d0);
             } else {
                 kreg[i] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -175,22 +206,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
                 for (int r = 0; r < 16; r++)
                     if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
             }
-            float mb = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-            const float m_new = fmaxf(m_run, mb);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            float ls = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_new);
-                ls += sc[r];
-            }
-            l_run = l_run * alpha + ls;
-            m_run = m_new;
-            o[0] *= alpha;
-            o[1] *= alpha;
+            online_softmax_block(sc, m_run, l_run, o);
             // O^T += V^T * P^T: step (qq, r) consumes keys 8qq + 4lh + r, which
             // is register 4qq + r of the lane's own half.
 #pragma unroll
@@ -216,8 +232,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
     if (q >= a.L) return;
     const float inv = 1.0f / l_tot;
     const int row = attn_row(a, s, q);
-    float gate = 1.0f;
-    if (a.gate_col >= 0) gate = sigmoid_dev(qkv[(size_t)row * a.ld + a.gate_col + h]);
+    const float gate = a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f;
     TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
 #pragma unroll
     for (int t = 0; t < 2; t++)

@@ -31,9 +31,9 @@ VH_DEVICE floatx4 hi4(bf16x8 v) { return floatx4{(float)v[4], (float)v[5], (floa
 
 // Rotate the four interleaved pairs of 8 dims starting at d0 (fp32), scale,
 // round to bf16.
-VH_DEVICE bf16x8 rope8_bf16(bf16x8 v, const float *cs, const float *sn, int pos, int d0, float scale) {
-    floatx4 a = rope4(lo4(v), cs, sn, pos, d0) * scale;
-    floatx4 b = rope4(hi4(v), cs, sn, pos, d0 + 4) * scale;
+VH_DEVICE bf16x8 rope8_bf16(bf16x8 v, const float *tab, int pos, int d0, float scale) {
+    floatx4 a = rope4(lo4(v), tab, pos, d0) * scale;
+    floatx4 b = rope4(hi4(v), tab, pos, d0 + 4) * scale;
     bf16x8 r;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -71,14 +71,16 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_bf16_kernel(AttnArgs 
 
     // Q of query q0+li, dims 16g + 8lh .. +7, rotated and scaled (log2 domain).
     bf16x8 qb[4];
+    float gate_logit = 0.0f;  // loaded with Q so the store does not wait on it
     {
         const int q = min(q0 + li, a.L - 1);
         const bf16 *qp = qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+        if (a.gate_col >= 0) gate_logit = (float)qkv[(size_t)attn_row(a, s, q) * a.ld + a.gate_col + h];
         const float qs = a.scale * 1.4426950408889634f;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const int d0 = 16 * g + 8 * lh;
-            qb[g] = rope8_bf16(*reinterpret_cast<const bf16x8 *>(qp + d0), a.rope_cos, a.rope_sin, q, d0, qs);
+            qb[g] = rope8_bf16(*reinterpret_cast<const bf16x8 *>(qp + d0), a.rope, q, d0, qs);
         }
     }
 
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_bf16_kernel(AttnArgs 
             const int pk = kb * ATT_KB + kk, pv = kb * ATT_KB + vk;
             if (pk < a.L) {
                 const bf16 *kp = qkv + (size_t)attn_row(a, s, pk) * a.ld + kcol + kd;
-                kreg[i] = rope8_bf16(*reinterpret_cast<const bf16x8 *>(kp), a.rope_cos, a.rope_sin, pk, kd, 1.0f);
+                kreg[i] = rope8_bf16(*reinterpret_cast<const bf16x8 *>(kp), a.rope, pk, kd, 1.0f);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; e++) kreg[i][e] = (bf16)0.0f;
@@ -148,22 +150,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_bf16_kernel(AttnArgs 
                 for (int r = 0; r < 16; r++)
                     if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
             }
-            float mb = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-            const float m_new = fmaxf(m_run, mb);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            float ls = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_new);
-                ls += sc[r];
-            }
-            l_run = l_run * alpha + ls;
-            m_run = m_new;
-            o[0] *= alpha;
-            o[1] *= alpha;
+            online_softmax_block(sc, m_run, l_run, o);
 #pragma unroll
             for (int st = 0; st < 2; st++) {
                 bf16x8 pb;
@@ -189,8 +176,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_bf16_kernel(AttnArgs 
     if (q >= a.L) return;
     const float inv = 1.0f / l_tot;
     const int row = attn_row(a, s, q);
-    float gate = 1.0f;
-    if (a.gate_col >= 0) gate = sigmoid_dev((float)qkv[(size_t)row * a.ld + a.gate_col + h]);
+    const float gate = a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f;
     TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
 #pragma unroll
     for (int t = 0; t < 2; t++)

@@ -32,6 +32,7 @@ struct GemmDesc {
 
 constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_BK = 16, GEMM_PITCH = GEMM_BK + 4;
 constexpr int GEMM_THREADS = 256;
+static_assert(GEMM_BM == 128 && GEMM_BN == 128 && GEMM_THREADS == 256, "the product tile is 2 x 2 waves");
 constexpr int GEMM_GROUP_M = 16;
 constexpr size_t GEMM_L2_RESIDENT_BYTES = 3u << 20;
 // Descriptors of a ragged batch travel in the kernel arguments (<= 4 KiB).
@@ -40,8 +41,11 @@ struct GemmBatch {
     GemmDesc d[GEMM_MAX_BATCH];
 };
 
-template <int EPI>
+// WM x WN wavefronts of 64x64 each (block tile 64*WM x 64*WN); the product
+// uses 2 x 2 (GEMM_BM x GEMM_BN).
+template <int EPI, int WM = 2, int WN = 2>
 __device__ __forceinline__ void gemm_f32_body(const GemmDesc &d, int tile) {
+    constexpr int GEMM_BM = 64 * WM, GEMM_BN = 64 * WN, GEMM_THREADS = 64 * WM * WN;
     __shared__ __attribute__((aligned(16))) float As[2][GEMM_BM][GEMM_PITCH];
     __shared__ __attribute__((aligned(16))) float Bs[2][GEMM_BN][GEMM_PITCH];
 
@@ -65,33 +69,36 @@ __device__ __forceinline__ void gemm_f32_body(const GemmDesc &d, int tile) {
 
     const int tid = (int)threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int li = lane & 31, lh = lane >> 5;
 
     // global -> register staging: a k-chunk row holds GEMM_BK/4 float4s;
     // thread covers rows ld_row + RSTEP*q and float4 ld_c4 of the chunk.
     constexpr int C4 = GEMM_BK / 4;                  // float4s per tile row
     constexpr int RSTEP = GEMM_THREADS / C4;         // rows covered per pass
-    constexpr int NQ = GEMM_BM / RSTEP;              // passes
+    constexpr int NQA = GEMM_BM / RSTEP, NQB = GEMM_BN / RSTEP;  // passes
+    static_assert(GEMM_BM % RSTEP == 0 && GEMM_BN % RSTEP == 0, "staging must tile the block");
     const int ld_row = tid / C4, ld_c4 = tid % C4;
-    floatx4 ra[NQ], rb[NQ];
+    floatx4 ra[NQA], rb[NQB];
     auto load = [&](int k0) {
         const int kk = k0 + 4 * ld_c4;
         const bool kin = kk < d.K;
 #pragma unroll
-        for (int q = 0; q < NQ; q++) {
+        for (int q = 0; q < NQA; q++) {
             int gm = min(m0 + ld_row + RSTEP * q, d.M - 1);
-            int gn = min(n0 + ld_row + RSTEP * q, d.N - 1);
             ra[q] = kin ? ld4(d.A + (size_t)gm * d.lda + kk) : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int q = 0; q < NQB; q++) {
+            int gn = min(n0 + ld_row + RSTEP * q, d.N - 1);
             rb[q] = kin ? ld4(d.B + (size_t)gn * d.ldb + kk) : floatx4{0.f, 0.f, 0.f, 0.f};
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < NQ; q++) {
-            st4(&As[buf][ld_row + RSTEP * q][4 * ld_c4], ra[q]);
-            st4(&Bs[buf][ld_row + RSTEP * q][4 * ld_c4], rb[q]);
-        }
+        for (int q = 0; q < NQA; q++) st4(&As[buf][ld_row + RSTEP * q][4 * ld_c4], ra[q]);
+#pragma unroll
+        for (int q = 0; q < NQB; q++) st4(&Bs[buf][ld_row + RSTEP * q][4 * ld_c4], rb[q]);
     };
 
     floatx16 acc[2][2];

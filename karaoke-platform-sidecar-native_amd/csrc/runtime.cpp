@@ -404,16 +404,15 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
     }
 }
 
-bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope_cos,
-               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t, bool out_bf16,
-               bool qkv_bf16) {
+bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
+               int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16) {
     if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
     }
     AttnArgs a;
     a.qkv = qkv; a.ld = ld; a.out = out; a.ld_out = ld_out;
-    a.rope_cos = rope_cos; a.rope_sin = rope_sin;
+    a.rope = rope;
     a.S = lay.S; a.L = lay.L; a.H = heads;
     a.group = lay.group; a.group_stride = lay.group_stride; a.seq_stride = lay.seq_stride; a.pos_stride = lay.pos_stride;
     a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
@@ -455,36 +454,43 @@ bool RopeCache::get(int length, int dim_head, hipStream_t s, const float **cs, c
     auto it = tables.find(length);
     if (it == tables.end()) {
         const int pairs = dim_head / 2;
-        std::vector<float> freq(pairs), hc((size_t)length * pairs), hs((size_t)length * pairs);
+        const size_t n = (size_t)length * pairs;
+        std::vector<float> freq(pairs), h(4 * n);
+        float *hc = h.data(), *hs = hc + n, *hi = hs + n;
         for (int i = 0; i < pairs; i++) freq[i] = 1.0f / powf(10000.0f, (float)(2 * i) / (float)dim_head);
         for (int p = 0; p < length; p++)
             for (int k = 0; k < pairs; k++) {
-                float angle = (float)p * freq[k];
-                hc[(size_t)p * pairs + k] = cosf(angle);
-                hs[(size_t)p * pairs + k] = sinf(angle);
+                const float angle = (float)p * freq[k];
+                const size_t e = (size_t)p * pairs + k;
+                hc[e] = cosf(angle);
+                hs[e] = sinf(angle);
+                hi[2 * e] = hc[e];
+                hi[2 * e + 1] = hs[e];
             }
-        float *dc = nullptr, *ds = nullptr;
-        size_t bytes = hc.size() * sizeof(float);
-        if (!check(hipMalloc((void **)&dc, bytes), "hipMalloc(rope cos)")) return false;
-        if (!check(hipMalloc((void **)&ds, bytes), "hipMalloc(rope sin)")) { (void)hipFree(dc); return false; }
-        if (!check(hipMemcpyAsync(dc, hc.data(), bytes, hipMemcpyHostToDevice, s), "hipMemcpy(rope cos)") ||
-            !check(hipMemcpyAsync(ds, hs.data(), bytes, hipMemcpyHostToDevice, s), "hipMemcpy(rope sin)") ||
+        float *d = nullptr;
+        const size_t bytes = h.size() * sizeof(float);
+        if (!check(hipMalloc((void **)&d, bytes), "hipMalloc(rope tables)")) return false;
+        if (!check(hipMemcpyAsync(d, h.data(), bytes, hipMemcpyHostToDevice, s), "hipMemcpy(rope tables)") ||
             !check(hipStreamSynchronize(s), "hipStreamSynchronize(rope)")) {
-            (void)hipFree(dc); (void)hipFree(ds);
+            (void)hipFree(d);
             return false;
         }
-        it = tables.emplace(length, std::make_pair(dc, ds)).first;
+        it = tables.emplace(length, Tables{d, d + n, d + 2 * n}).first;
     }
-    *cs = it->second.first;
-    *sn = it->second.second;
+    *cs = it->second.cos;
+    *sn = it->second.sin;
+    return true;
+}
+
+bool RopeCache::get_interleaved(int length, int dim_head, hipStream_t s, const float **cssn) {
+    const float *cs, *sn;
+    if (!get(length, dim_head, s, &cs, &sn)) return false;
+    *cssn = tables[length].interleaved;
     return true;
 }
 
 void RopeCache::release() {
-    for (auto &kv : tables) {
-        (void)hipFree(kv.second.first);
-        (void)hipFree(kv.second.second);
-    }
+    for (auto &kv : tables) (void)hipFree(kv.second.cos);  // one allocation per length
     tables.clear();
 }
 
@@ -500,8 +506,8 @@ bool BlockScratch::ensure(const Dims &d, int64_t tokens) {
 bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, float *x, int64_t tokens,
                        const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t, int precision) {
     if (!scr.ensure(d, tokens)) return false;
-    const float *cs = nullptr, *sn = nullptr;
-    if (!rope.get(lay.L, d.dim_head, s, &cs, &sn)) return false;
+    const float *rt = nullptr;
+    if (!rope.get_interleaved(lay.L, d.dim_head, s, &rt)) return false;
     const int D = d.dim, inner = d.inner(), nq = d.qkvg_dim();
     float *normed = scr.normed.f(), *qkvg = scr.qkvg.f(), *attn = scr.attn.f(), *hid = scr.hidden.f();
     const int gate = d.gated ? d.qkv_dim() : -1;
@@ -523,7 +529,7 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
         };
         if (!rmsnorm_bf16(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
         if (!lin(normed, D, w.wqkvg_h, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, true, "gemm_qkv")) return false;
-        if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, gate, t, true, true)) return false;
+        if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, true, true)) return false;
         if (!lin(attn, inner, w.wout_h, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;
         if (!rmsnorm_bf16(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
         if (!lin(normed, D, w.w1_h, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, true, "gemm_ff1")) return false;
@@ -533,7 +539,7 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
     if (!gemm(s, {normed, D, w.wqkvg, D, w.bqkvg, qkvg, nq, tokens, nq, D}, EPI_STORE, t, "gemm_qkv")) return false;
     // rotary + attention + gates
-    if (!attention(s, qkvg, nq, attn, inner, cs, sn, lay, d.heads, gate, t)) return false;
+    if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t)) return false;
     // out projection added to the residual stream
     if (!gemm(s, {attn, inner, w.wout, inner, nullptr, x, D, tokens, D, inner}, EPI_RESIDUAL, t, "gemm_out")) return false;
     // FFN

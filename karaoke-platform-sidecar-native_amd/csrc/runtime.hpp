@@ -128,10 +128,9 @@ struct AttnLayout {
     int group, group_stride, seq_stride, pos_stride;
 };
 // qkv fp32 (fp32 MFMA) or, with qkv_bf16, bf16 (bf16 MFMA); out fp32, or bf16
-// when out_bf16.
-bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope_cos,
-               const float *rope_sin, const AttnLayout &lay, int heads, int gate_col, KernelTimer *t = nullptr,
-               bool out_bf16 = false, bool qkv_bf16 = false);
+// when out_bf16.  rope: interleaved rotary table of length lay.L (or null).
+bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
+               int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {
@@ -166,9 +165,15 @@ enum Precision : int { PREC_FP32 = 0, PREC_BF16 = 1 };
 
 // Rotary cos/sin tables per sequence length, built on the host with the
 // reference's float expressions (native/vocalarc_separation.c:726-731,1312).
+// Rotary tables per sequence length, built on the host with the reference's
+// float expressions (native/vocalarc_separation.c:726-731): cos[L][Dh/2],
+// sin[L][Dh/2] and the same values interleaved as (cos, sin) pairs
+// [L][Dh/2][2], so one 16-byte load gives what four rotated dims need.
 struct RopeCache {
-    std::map<int, std::pair<float *, float *>> tables;
+    struct Tables { float *cos, *sin, *interleaved; };
+    std::map<int, Tables> tables;
     bool get(int length, int dim_head, hipStream_t s, const float **cs, const float **sn);
+    bool get_interleaved(int length, int dim_head, hipStream_t s, const float **cssn);
     void release();
     ~RopeCache() { release(); }
 };

@@ -155,10 +155,10 @@ extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *
 extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                             int apply_rotary, int flags) {
     if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16))) return 0;
-    const float *cs = nullptr, *sn = nullptr;
-    if (apply_rotary && !ctx->rope.get(length, 64, ctx->stream, &cs, &sn)) return 0;
+    const float *rt = nullptr;
+    if (apply_rotary && !ctx->rope.get_interleaved(length, 64, ctx->stream, &rt)) return 0;
     const int inner = heads * 64;
-    return attention(ctx->stream, qkv, 3 * inner, out, inner, cs, sn, contiguous_layout(sequences, length), heads, -1,
+    return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
                      &ctx->timer, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0)
                ? 1
                : 0;

@@ -193,7 +193,8 @@ def test_attention_bf16_out_is_rounded_fp32(ctx, rng, S, L):
 def _emulate_bf16_attention(qkv, S, L, H):
     """float64 statement of the bf16 attention kernel's algorithm: q and k
     rotated in fp32 and rounded to bf16 (q scaled by 0.125*log2 e first), keys
-    in blocks of 32 with the online softmax in the exp2 domain, probabilities
+    in blocks of 32 with the online softmax in the exp2 domain (running max
+    raised only when a block exceeds it by more than 2^8), probabilities
     rounded to bf16 for the P*V product, fp32-exact sums in float64."""
     cs, sn = O.rope_table(L, 64)
     qs = np.float32(0.125 * 1.4426950408889634)
@@ -221,12 +222,14 @@ def _emulate_bf16_attention(qkv, S, L, H):
             o = np.zeros((L, 64))
             for k0 in range(0, L, 32):
                 sc = qr @ kr[k0:k0 + 32].T
-                m_new = np.maximum(m, sc.max(axis=1))
+                mb = sc.max(axis=1)
+                grow = mb > m + 8.0  # the running max moves only when a block exceeds it by > 2^8
+                m_new = np.where(grow, mb, m)
                 alpha = np.exp2(m - m_new)
-                p = np.exp2(sc - m_new[:, None])
-                l = l * alpha + p.sum(axis=1)
-                o = o * alpha[:, None] + _round_bf16(p.astype(np.float32)).astype(np.float64) @ v[k0:k0 + 32]
-                m = m_new
+                l, o, m = l * alpha, o * alpha[:, None], m_new
+                p = np.exp2(sc - m[:, None])
+                l = l + p.sum(axis=1)
+                o = o + _round_bf16(p.astype(np.float32)).astype(np.float64) @ v[k0:k0 + 32]
             out[rows, c] = o / l[:, None]
     return out
 
