@@ -54,7 +54,7 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_bf16_kernel(AttnArgs 
 
     const bf16 *qkv = static_cast<const bf16 *>(a.qkv);
     const int qgroups = (a.L + 32 * WAVES - 1) / (32 * WAVES);
-    const int task = (int)blockIdx.x;
+    const int task = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);  // neighbouring tasks share K/V rows: same XCD
     const int qg = task % qgroups;
     const int sh = task / qgroups;
     const int h = sh % a.H;

@@ -417,7 +417,12 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     a.group = lay.group; a.group_stride = lay.group_stride; a.seq_stride = lay.seq_stride; a.pos_stride = lay.pos_stride;
     a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
-    if (lay.L <= 64) launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16);
+    if (lay.L <= 64 && !qkv_bf16) {
+        const unsigned grid = (unsigned)((int64_t)lay.S * heads);
+        if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attention_short_kernel<float>), dim3(grid), dim3(256), 0, s, a);
+    } else if (lay.L <= 64)
+        launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16);
     else launch_attention<4>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 127) / 128)), out_bf16, qkv_bf16);
     return sync_debug(s, "attention_kernel");
 }

@@ -162,7 +162,7 @@ def _rotate_qk(qkv: np.ndarray, length: int, heads: int) -> np.ndarray:
     return out
 
 
-@pytest.mark.parametrize("S,L", [(5, 62), (2, 801), (3, 33), (4, 1), (1, 65), (2, 130)])
+@pytest.mark.parametrize("S,L", [(5, 62), (2, 801), (3, 33), (4, 1), (1, 65), (2, 130), (7, 64), (2, 17)])
 def test_attention_core(ctx, rng, S, L):
     H = 8
     qkv = rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32)
