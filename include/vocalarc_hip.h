@@ -108,18 +108,26 @@ int vh_model_set_precision(vh_model *model, int precision);
 /* One axial transformer (native/vocalarc_separation.c:836-873) in place on
    device x[S][L][dim]; axis 0 = time weights, 1 = band weights. */
 int vh_transformer(vh_context *ctx, vh_model *model, int layer, int axis, float *x, int sequences, int length);
+/* Spectrum layouts (float (re, im) pairs): VH_SPEC_REFERENCE is the
+   reference's source/mask[F][C][T][2] (native/vocalarc_separation.c:1058,
+   1336); VH_SPEC_FRAME_MAJOR is [C][T][F][2], every frame's bins contiguous
+   (what the device pipeline uses internally). */
+#define VH_SPEC_REFERENCE 0
+#define VH_SPEC_FRAME_MAJOR 1
 /* STFT (native/vocalarc_separation.c:1044-1072): device audio[C][length] ->
-   device source[F][C][T][2], T = length/hop + 1. */
-int vh_stft(vh_context *ctx, vh_model *model, const float *audio, int length, float *source);
+   device source (layout), T = length/hop + 1. */
+int vh_stft(vh_context *ctx, vh_model *model, const float *audio, int length, float *source, int layout);
 /* Complex mask multiply + iSTFT + overlap-add
    (native/vocalarc_separation.c:1084-1136) -> device audio[C][length]. */
-int vh_istft(vh_context *ctx, vh_model *model, const float *source, const float *mask, int length, float *audio);
-/* Band split (native/vocalarc_separation.c:887-926): device source -> device
-   time_sequences[B][T][dim]. */
-int vh_band_split(vh_context *ctx, vh_model *model, const float *source, int frames, float *time_sequences);
+int vh_istft(vh_context *ctx, vh_model *model, const float *source, const float *mask, int length, float *audio,
+             int layout);
+/* Band split (native/vocalarc_separation.c:887-926): device source (layout)
+   -> device time_sequences[B][T][dim]. */
+int vh_band_split(vh_context *ctx, vh_model *model, const float *source, int frames, float *time_sequences,
+                  int layout);
 /* Mask estimator (native/vocalarc_separation.c:1316-1340, all bands) on
-   final-normed device features[T][B][dim] -> device mask[F][C][T][2]. */
-int vh_mask_estimate(vh_context *ctx, vh_model *model, const float *features, int frames, float *mask);
+   final-normed device features[T][B][dim] -> device mask (layout). */
+int vh_mask_estimate(vh_context *ctx, vh_model *model, const float *features, int frames, float *mask, int layout);
 /* Whole forward of one window (native/vocalarc_separation.c:1342-1445):
    device audio[C][length] -> device vocals[C][length]; when `instrumental`
    is not NULL it receives audio - vocals (native/vocalarc_separation.c:1589-1591). */

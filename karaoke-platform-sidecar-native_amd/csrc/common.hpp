@@ -32,6 +32,25 @@ VH_DEVICE float gelu_dev(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067
 VH_DEVICE floatx4 ld4(const float *p) { return *reinterpret_cast<const floatx4 *>(p); }
 VH_DEVICE void st4(float *p, floatx4 v) { *reinterpret_cast<floatx4 *>(p) = v; }
 
+// Complex spectrum element (chunk, frequency f, channel c, frame t) of a
+// float array of (re, im) pairs, at pair index
+// chunk*chunk_s + f*f_s + c*c_s + t*t_s.  The reference's layout is
+// [chunk][F][C][T] (native/vocalarc_separation.c:1058, 1336); the device
+// pipeline keeps spectra frame-major, [chunk][C][T][F], so every frame's bins
+// are contiguous for the FFTs, the band gather and the mask scatter.
+struct SpecLayout {
+    int64_t chunk_s, f_s, c_s, t_s;
+};
+inline SpecLayout spec_reference_layout(int F, int C, int T) {
+    return {(int64_t)F * C * T, (int64_t)C * T, (int64_t)T, 1};
+}
+inline SpecLayout spec_frame_major_layout(int F, int C, int T) {
+    return {(int64_t)C * T * F, 1, (int64_t)T * F, (int64_t)F};
+}
+VH_DEVICE int64_t spec_at(const SpecLayout &l, int chunk, int f, int c, int t) {
+    return chunk * l.chunk_s + f * l.f_s + c * l.c_s + t * l.t_s;
+}
+
 // bf16 storage (round to nearest even on conversion: v_cvt_pk_bf16_f32)
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -237,7 +237,7 @@ static __global__ __launch_bounds__(256) void transpose_rows_kernel(const float 
 
 // --------------------------------------------------------- band split gather
 // For band b and spectrogram row m (= chunk*T + t) gather the band's bins from
-// source[chunk][F][C][T][2] in (frequency, channel, re/im) order, RMS-normalise
+// source bins (layout lay) in (frequency, channel, re/im) order, RMS-normalise
 // with the band gamma and write row m of the band's input matrix
 // (native/vocalarc_separation.c:887-912).
 struct BandTable {
@@ -248,9 +248,8 @@ struct BandTable {
 };
 
 static __global__ __launch_bounds__(256) void band_gather_norm_kernel(const float *__restrict__ source,
-                                                               const BandTable *__restrict__ tab,
-                                                               float *__restrict__ bandin, int M, int T, int F,
-                                                               int C) {
+                                                               SpecLayout lay, const BandTable *__restrict__ tab,
+                                                               float *__restrict__ bandin, int M, int T, int C) {
     const int b = (int)blockIdx.y;
     const int m = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
     const int lane = (int)threadIdx.x & 63;
@@ -259,7 +258,6 @@ static __global__ __launch_bounds__(256) void band_gather_norm_kernel(const floa
     const int w = tab->width[b], ff = tab->first_freq[b];
     const int in_dim = w * C * 2;
     const int pairs = w * C;
-    const float *src = source + (size_t)chunk * F * C * T * 2;
     float *dst = bandin + tab->in_offset[b] + (size_t)m * in_dim;
     const float *gamma = tab->gamma[b];
     constexpr int MAXP = 5;  // up to 320 (frequency, channel) pairs per band
@@ -270,7 +268,7 @@ static __global__ __launch_bounds__(256) void band_gather_norm_kernel(const floa
         const int j = lane + 64 * k;
         if (j < pairs) {
             const int f = j / C, c = j % C;
-            v[k] = *reinterpret_cast<const float2 *>(src + (((size_t)(ff + f) * C + c) * T + t) * 2);
+            v[k] = *reinterpret_cast<const float2 *>(source + 2 * spec_at(lay, chunk, ff + f, c, t));
             ss += v[k].x * v[k].x + v[k].y * v[k].y;
         }
     }
@@ -289,7 +287,7 @@ static __global__ __launch_bounds__(256) void band_gather_norm_kernel(const floa
 }
 
 // ------------------------------------------------------ mask GLU + scatter
-// proj_b[m][2*dim] (bias included) -> mask[chunk][F][C][T][2]:
+// proj_b[m][2*dim] (bias included) -> mask bins (layout lay):
 // m_i = p_i * sigmoid(p_{dim+i}), i -> (frequency i/(2C), channel (i/2)%C,
 // component i%2) (native/vocalarc_separation.c:1330-1338).
 struct MaskTable {
@@ -300,7 +298,7 @@ struct MaskTable {
 
 static __global__ __launch_bounds__(256) void mask_glu_scatter_kernel(const float *__restrict__ proj,
                                                                const MaskTable *__restrict__ tab,
-                                                               float *__restrict__ mask, int M, int T, int F,
+                                                               float *__restrict__ mask, SpecLayout lay, int M, int T,
                                                                int C) {
     const int b = (int)blockIdx.y;
     const int dim = tab->dim[b];
@@ -312,7 +310,7 @@ static __global__ __launch_bounds__(256) void mask_glu_scatter_kernel(const floa
     const float val = p[i] * (1.0f / (1.0f + __expf(-p[dim + i])));
     const int f = tab->first_freq[b] + i / (2 * C);
     const int c = (i / 2) % C, comp = i & 1;
-    mask[(size_t)chunk * F * C * T * 2 + (((size_t)f * C + c) * T + t) * 2 + comp] = val;
+    mask[2 * spec_at(lay, chunk, f, c, t) + comp] = val;
 }
 
 }  // namespace vh

@@ -448,8 +448,8 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
          check(hipMemcpyAsync(gpu->tables.ptr, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(mask table)");
     if (ok) {
         hipLaunchKernelGGL(mask_glu_scatter_kernel, dim3((unsigned)(((int64_t)M * maxdim + 255) / 256), B), dim3(256), 0,
-                           s, gpu->proj.f(), (const MaskTable *)gpu->tables.ptr, gpu->mask.f(), M, frames,
-                           d.freq_bins(), d.channels);
+                           s, gpu->proj.f(), (const MaskTable *)gpu->tables.ptr, gpu->mask.f(),
+                           spec_reference_layout(d.freq_bins(), d.channels, frames), M, frames, d.channels);
         ok = sync_debug(s, "mask_glu_scatter_kernel") &&
              check(hipMemcpyAsync(mask, gpu->mask.ptr, mask_floats * sizeof(float), hipMemcpyDeviceToHost, s),
                    "hipMemcpy(mask)") &&

@@ -402,20 +402,21 @@ int log2i(int n) {
 }
 
 bool stage_stft(vh_model *m, const float *audio, int64_t audio_len, const int64_t *starts_dev, int sig_len, int chunks,
-                int T, float *source) {
+                int T, float *source, const SpecLayout &lay) {
     const Dims &d = m->d;
     StftArgs a;
     a.audio = audio; a.audio_len = audio_len; a.starts = starts_dev; a.sig_len = sig_len;
     a.C = d.channels; a.T = T; a.F = d.freq_bins(); a.n_fft = d.n_fft; a.log2n = log2i(d.n_fft); a.hop = d.hop;
-    a.window = m->window.f(); a.tw = static_cast<const double2_t *>(m->twiddle.ptr); a.source = source;
+    a.window = m->window.f(); a.tw = static_cast<const double2_t *>(m->twiddle.ptr); a.source = source; a.out = lay;
     Scope sc(&m->ctx->timer, m->ctx->stream, "stft");
-    hipLaunchKernelGGL(stft_kernel, dim3(T, chunks * d.channels), dim3(256), d.n_fft * sizeof(double2_t), m->ctx->stream, a);
+    hipLaunchKernelGGL(stft_kernel, dim3(T, chunks * d.channels), dim3(256), fft_lds_bytes(d.n_fft), m->ctx->stream, a);
     return sync_debug(m->ctx->stream, "stft_kernel");
 }
 
-// source[chunks][F][C][T][2] -> rows of out: band-major (time_sequences,
-// row b*M + m) or frame-major (row m*B + b).
-bool stage_band_split(vh_model *m, const float *source, int chunks, int T, float *out, bool frame_major) {
+// source bins (layout lay) -> rows of out: band-major (time_sequences, row
+// b*M + m) or frame-major (row m*B + b).
+bool stage_band_split(vh_model *m, const float *source, const SpecLayout &lay, int chunks, int T, float *out,
+                      bool frame_major) {
     const Dims &d = m->d;
     hipStream_t s = m->ctx->stream;
     const int M = chunks * T, B = d.bands, D = d.dim;
@@ -440,8 +441,8 @@ bool stage_band_split(vh_model *m, const float *source, int chunks, int T, float
         return false;
     {
         Scope sc(&m->ctx->timer, s, "band_gather");
-        hipLaunchKernelGGL(band_gather_norm_kernel, dim3((M + 3) / 4, B), dim3(256), 0, s, source,
-                           (const BandTable *)m->tables.ptr, m->bandin.f(), M, T, d.freq_bins(), d.channels);
+        hipLaunchKernelGGL(band_gather_norm_kernel, dim3((M + 3) / 4, B), dim3(256), 0, s, source, lay,
+                           (const BandTable *)m->tables.ptr, m->bandin.f(), M, T, d.channels);
         if (!sync_debug(s, "band_gather_norm_kernel")) return false;
     }
     // The table must stay intact until the gather has read it.
@@ -450,8 +451,9 @@ bool stage_band_split(vh_model *m, const float *source, int chunks, int T, float
 }
 
 // final-normed features (frame-major rows m*B + b; fp32, or bf16 when
-// normed_bf16) -> mask[chunks][F][C][T][2]
-bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, int T, float *mask) {
+// normed_bf16) -> mask bins (layout lay)
+bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, int T, float *mask,
+                const SpecLayout &lay) {
     const Dims &d = m->d;
     hipStream_t s = m->ctx->stream;
     const int M = chunks * T, B = d.bands, D = d.dim, Hm = d.mask_hidden;
@@ -508,25 +510,25 @@ bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, i
     {
         Scope sc(&m->ctx->timer, s, "mask_glu");
         hipLaunchKernelGGL(mask_glu_scatter_kernel, dim3((unsigned)(((int64_t)M * maxdim + 255) / 256), B), dim3(256), 0, s,
-                           m->proj.f(), dtab, mask, M, T, d.freq_bins(), d.channels);
+                           m->proj.f(), dtab, mask, lay, M, T, d.channels);
         if (!sync_debug(s, "mask_glu_scatter_kernel")) return false;
     }
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(mask table)");
 }
 
-// source, mask -> out[chunks*C][pitch] (first `length` samples of each)
-bool stage_istft(vh_model *m, const float *source, const float *mask, int chunks, int T, int length, float *out,
-                 int64_t pitch) {
+// source, mask (layout lay) -> out[chunks*C][pitch] (first `length` samples of each)
+bool stage_istft(vh_model *m, const float *source, const float *mask, const SpecLayout &lay, int chunks, int T,
+                 int length, float *out, int64_t pitch) {
     const Dims &d = m->d;
     hipStream_t s = m->ctx->stream;
     const int sigs = chunks * d.channels;
     if (!m->frames.ensure((size_t)sigs * T * d.n_fft * sizeof(float), "hipMalloc(istft frames)")) return false;
     IstftArgs a;
-    a.source = source; a.mask = mask; a.C = d.channels; a.T = T; a.F = d.freq_bins(); a.n_fft = d.n_fft;
+    a.source = source; a.mask = mask; a.in = lay; a.C = d.channels; a.T = T; a.F = d.freq_bins(); a.n_fft = d.n_fft;
     a.log2n = log2i(d.n_fft); a.window = m->window.f(); a.tw = static_cast<const double2_t *>(m->twiddle.ptr);
     a.frames = m->frames.f();
     Scope sc(&m->ctx->timer, s, "istft");
-    hipLaunchKernelGGL(istft_frames_kernel, dim3(T, sigs), dim3(256), d.n_fft * sizeof(double2_t), s, a);
+    hipLaunchKernelGGL(istft_frames_kernel, dim3(T, sigs), dim3(256), fft_lds_bytes(d.n_fft), s, a);
     if (!sync_debug(s, "istft_frames_kernel")) return false;
     OlaArgs o;
     o.frames = m->frames.f(); o.window = m->window.f(); o.T = T; o.n_fft = d.n_fft; o.hop = d.hop; o.length = length;
@@ -563,8 +565,10 @@ bool run_windows(vh_model *m, const float *audio, int64_t audio_len, const int64
         !m->x.ensure((size_t)tokens * d.dim * sizeof(float), "hipMalloc(features)") ||
         !m->normed.ensure((size_t)tokens * d.dim * sizeof(float), "hipMalloc(normed features)"))
         return false;
-    if (!stage_stft(m, audio, audio_len, starts_dev, sig_len, chunks, T, m->source.f())) return false;
-    if (!stage_band_split(m, m->source.f(), chunks, T, m->x.f(), true)) return false;
+    // spectra stay frame-major on the device: each frame's bins contiguous
+    const SpecLayout lay = spec_frame_major_layout(d.freq_bins(), d.channels, T);
+    if (!stage_stft(m, audio, audio_len, starts_dev, sig_len, chunks, T, m->source.f(), lay)) return false;
+    if (!stage_band_split(m, m->source.f(), lay, chunks, T, m->x.f(), true)) return false;
     if (!stage_stack(m, m->x.f(), chunks, T)) return false;
     const bool h = m->precision == PREC_BF16;
     if (h ? !rmsnorm_bf16(m->ctx->stream, m->x.f(), d.dim, m->final_gamma, m->normed.ptr, d.dim, tokens, d.dim,
@@ -572,8 +576,8 @@ bool run_windows(vh_model *m, const float *audio, int64_t audio_len, const int64
           : !rmsnorm(m->ctx->stream, m->x.f(), d.dim, m->final_gamma, m->normed.f(), d.dim, tokens, d.dim,
                      &m->ctx->timer))
         return false;
-    if (!stage_mask(m, m->normed.ptr, h, chunks, T, m->mask.f())) return false;
-    return stage_istft(m, m->source.f(), m->mask.f(), chunks, T, sig_len, out, pitch);
+    if (!stage_mask(m, m->normed.ptr, h, chunks, T, m->mask.f(), lay)) return false;
+    return stage_istft(m, m->source.f(), m->mask.f(), lay, chunks, T, sig_len, out, pitch);
 }
 
 }  // namespace
@@ -620,24 +624,47 @@ extern "C" int vh_transformer(vh_context *ctx, vh_model *m, int layer, int axis,
                : 0;
 }
 
-extern "C" int vh_stft(vh_context *ctx, vh_model *m, const float *audio, int length, float *source) {
+static bool spec_layout_of(int layout, const Dims &d, int T, SpecLayout *out) {
+    if (layout == VH_SPEC_REFERENCE) *out = spec_reference_layout(d.freq_bins(), d.channels, T);
+    else if (layout == VH_SPEC_FRAME_MAJOR) *out = spec_frame_major_layout(d.freq_bins(), d.channels, T);
+    else {
+        set_error("unknown spectrum layout %d", layout);
+        return false;
+    }
+    return true;
+}
+
+extern "C" int vh_stft(vh_context *ctx, vh_model *m, const float *audio, int length, float *source, int layout) {
     if (!ctx || !m || length <= 0) return 0;
-    return stage_stft(m, audio, length, nullptr, length, 1, m->d.frames(length), source) ? 1 : 0;
+    const int T = m->d.frames(length);
+    SpecLayout lay;
+    if (!spec_layout_of(layout, m->d, T, &lay)) return 0;
+    return stage_stft(m, audio, length, nullptr, length, 1, T, source, lay) ? 1 : 0;
 }
 
-extern "C" int vh_istft(vh_context *ctx, vh_model *m, const float *source, const float *mask, int length, float *audio) {
+extern "C" int vh_istft(vh_context *ctx, vh_model *m, const float *source, const float *mask, int length, float *audio,
+                        int layout) {
     if (!ctx || !m || length <= 0) return 0;
-    return stage_istft(m, source, mask, 1, m->d.frames(length), length, audio, length) ? 1 : 0;
+    const int T = m->d.frames(length);
+    SpecLayout lay;
+    if (!spec_layout_of(layout, m->d, T, &lay)) return 0;
+    return stage_istft(m, source, mask, lay, 1, T, length, audio, length) ? 1 : 0;
 }
 
-extern "C" int vh_band_split(vh_context *ctx, vh_model *m, const float *source, int frames, float *time_sequences) {
+extern "C" int vh_band_split(vh_context *ctx, vh_model *m, const float *source, int frames, float *time_sequences,
+                             int layout) {
     if (!ctx || !m || frames <= 0) return 0;
-    return stage_band_split(m, source, 1, frames, time_sequences, false) ? 1 : 0;
+    SpecLayout lay;
+    if (!spec_layout_of(layout, m->d, frames, &lay)) return 0;
+    return stage_band_split(m, source, lay, 1, frames, time_sequences, false) ? 1 : 0;
 }
 
-extern "C" int vh_mask_estimate(vh_context *ctx, vh_model *m, const float *features, int frames, float *mask) {
+extern "C" int vh_mask_estimate(vh_context *ctx, vh_model *m, const float *features, int frames, float *mask,
+                                int layout) {
     if (!ctx || !m || frames <= 0) return 0;
-    return stage_mask(m, features, false, 1, frames, mask) ? 1 : 0;
+    SpecLayout lay;
+    if (!spec_layout_of(layout, m->d, frames, &lay)) return 0;
+    return stage_mask(m, features, false, 1, frames, mask, lay) ? 1 : 0;
 }
 
 extern "C" int vh_forward(vh_context *ctx, vh_model *m, const float *audio, int length, float *vocals,

@@ -6,8 +6,9 @@ Isolated kernels (fp32, inputs N(0,1), gammas N(1,0.02)):
   [49662, 384].
 One axial layer at dim 384 (weights N(0,0.02), activations N(0,1)):
   time transformer (62 sequences x 801), band transformer (801 x 62).
-Front/back end on 60 s of audio (hop 441, n_fft 2048, 62 bands):
-  STFT, complex mask multiply + iSTFT + overlap-add, band split, mask estimator.
+Front/back end on 60 s of audio (hop 441, n_fft 2048, 62 bands), spectra in
+the pipeline's frame-major layout: STFT, complex mask multiply + iSTFT +
+overlap-add, band split, mask estimator.
 
 Work per launch is algorithmic (each tensor read and written once; 2*M*K*N
 per GEMM); time is the mean over repetitions measured with HIP events on the
@@ -178,20 +179,22 @@ def main() -> int:
             x = torch.from_numpy(audio.sine_mix(60.0, 60)).to(dev)
             length = x.shape[1]
             Tf = d.frames(length)
-            src = torch.empty(d.freq_bins, d.channels, Tf, 2, device=dev)
-            _emit("stft", _event_time(lambda: model.stft(x, length, src), reps),
+            # spectra in the pipeline's frame-major layout [C][T][F][2]
+            fm = native.SPEC_FRAME_MAJOR
+            src = torch.empty(d.channels, Tf, d.freq_bins, 2, device=dev)
+            _emit("stft", _event_time(lambda: model.stft(x, length, src, fm), reps),
                   gbytes=(x.numel() + src.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}")
             mask = torch.randn_like(src)
             out = torch.empty_like(x)
-            _emit("istft", _event_time(lambda: model.istft(src, mask, length, out), reps),
+            _emit("istft", _event_time(lambda: model.istft(src, mask, length, out, fm), reps),
                   gbytes=(2 * src.numel() + out.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}")
             seq = torch.empty(d.bands, Tf, D, device=dev)
-            _emit("band_split", _event_time(lambda: model.band_split(src, Tf, seq), reps),
+            _emit("band_split", _event_time(lambda: model.band_split(src, Tf, seq, fm), reps),
                   gflop=2.0 * Tf * sum(d.input_dims()) * D / 1e9, shape=f"T={Tf}, 62 bands")
             feats = torch.randn(Tf, d.bands, D, device=dev, generator=g)
             mout = torch.empty_like(src)
             gf = 2.0 * Tf * (d.bands * D * d.mask_hidden + d.mask_hidden * 2 * sum(d.input_dims())) / 1e9
-            _emit("mask_estimator", _event_time(lambda: model.mask_estimate(feats, Tf, mout), max(3, reps // 4)),
+            _emit("mask_estimator", _event_time(lambda: model.mask_estimate(feats, Tf, mout, fm), max(3, reps // 4)),
                   gflop=gf, shape=f"T={Tf}, 62 bands")
         model.close()
     ctx.close()

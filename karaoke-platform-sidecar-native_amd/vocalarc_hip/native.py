@@ -34,6 +34,7 @@ EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16 = 0, 1
 BF16_A, BF16_C = 1, 2  # vh_gemm_bf16 operand flags
 ATT_OUT_BF16, ATT_BF16 = 1, 2  # vh_attention flags
+SPEC_REFERENCE, SPEC_FRAME_MAJOR = 0, 1  # spectrum layouts: [F][C][T][2] / [C][T][F][2]
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -68,10 +69,10 @@ def lib():
         "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
         "vh_model_free": (None, [_P]), "vh_model_set_precision": (_I, [_P, _I]),
         "vh_transformer": (_I, [_P, _P, _I, _I, _P, _I, _I]),
-        "vh_stft": (_I, [_P, _P, _P, _I, _P]),
-        "vh_istft": (_I, [_P, _P, _P, _P, _I, _P]),
-        "vh_band_split": (_I, [_P, _P, _P, _I, _P]),
-        "vh_mask_estimate": (_I, [_P, _P, _P, _I, _P]),
+        "vh_stft": (_I, [_P, _P, _P, _I, _P, _I]),
+        "vh_istft": (_I, [_P, _P, _P, _P, _I, _P, _I]),
+        "vh_band_split": (_I, [_P, _P, _P, _I, _P, _I]),
+        "vh_mask_estimate": (_I, [_P, _P, _P, _I, _P, _I]),
         "vh_forward": (_I, [_P, _P, _P, _I, _P, _P]),
         "vh_separate": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
         "vh_timing_enable": (_I, [_P, ctypes.c_char_p]), "vh_timing_reset": (_I, [_P]),
@@ -231,17 +232,17 @@ class Model:
     def transformer(self, layer: int, axis: int, x, sequences: int, length: int):
         _ok(lib().vh_transformer(self.ctx.h, self.h, layer, axis, ptr(x), sequences, length), "vh_transformer")
 
-    def stft(self, audio, length: int, source):
-        _ok(lib().vh_stft(self.ctx.h, self.h, ptr(audio), length, ptr(source)), "vh_stft")
+    def stft(self, audio, length: int, source, layout: int = SPEC_REFERENCE):
+        _ok(lib().vh_stft(self.ctx.h, self.h, ptr(audio), length, ptr(source), layout), "vh_stft")
 
-    def istft(self, source, mask, length: int, audio):
-        _ok(lib().vh_istft(self.ctx.h, self.h, ptr(source), ptr(mask), length, ptr(audio)), "vh_istft")
+    def istft(self, source, mask, length: int, audio, layout: int = SPEC_REFERENCE):
+        _ok(lib().vh_istft(self.ctx.h, self.h, ptr(source), ptr(mask), length, ptr(audio), layout), "vh_istft")
 
-    def band_split(self, source, frames: int, out):
-        _ok(lib().vh_band_split(self.ctx.h, self.h, ptr(source), frames, ptr(out)), "vh_band_split")
+    def band_split(self, source, frames: int, out, layout: int = SPEC_REFERENCE):
+        _ok(lib().vh_band_split(self.ctx.h, self.h, ptr(source), frames, ptr(out), layout), "vh_band_split")
 
-    def mask_estimate(self, features, frames: int, mask):
-        _ok(lib().vh_mask_estimate(self.ctx.h, self.h, ptr(features), frames, ptr(mask)), "vh_mask_estimate")
+    def mask_estimate(self, features, frames: int, mask, layout: int = SPEC_REFERENCE):
+        _ok(lib().vh_mask_estimate(self.ctx.h, self.h, ptr(features), frames, ptr(mask), layout), "vh_mask_estimate")
 
     def forward(self, audio, length: int, vocals, instrumental=None):
         _ok(lib().vh_forward(self.ctx.h, self.h, ptr(audio), length, ptr(vocals),

@@ -66,23 +66,36 @@ def test_transformer_block_reference_shape(ref_models, rng, axis, S, L):
     assert_close(ref, from_dev(dx), rtol=1e-4, atol=1e-4, min_snr=100, what="transformer (reference)")
 
 
+def _to_layout(spec: np.ndarray, layout: int) -> np.ndarray:
+    """[F][C][T][2] -> the device layout (frame-major: [C][T][F][2])."""
+    return spec if layout == native.SPEC_REFERENCE else np.ascontiguousarray(spec.transpose(1, 2, 0, 3))
+
+
+def _from_layout(spec: np.ndarray, layout: int) -> np.ndarray:
+    return spec if layout == native.SPEC_REFERENCE else np.ascontiguousarray(spec.transpose(2, 0, 1, 3))
+
+
+LAYOUTS = [0, 1]  # SPEC_REFERENCE, SPEC_FRAME_MAJOR
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("which", ["config", "reference"])
-def test_stft_istft(ctx, cfg2_models, ref_models, which):
+def test_stft_istft(ctx, cfg2_models, ref_models, which, layout):
     om, dm = cfg2_models if which == "config" else ref_models
     d = om.d
     x = audio.sine_mix(0.5, 3)
     length = x.shape[1]
     T = d.frames(length)
     src = O.stft(d, x)
-    dsrc = empty_dev(src.shape)
-    dm.stft(to_dev(x), length, dsrc)
-    gsrc = from_dev(dsrc)
+    dsrc = empty_dev(_to_layout(src, layout).shape)
+    dm.stft(to_dev(x), length, dsrc, layout)
+    gsrc = _from_layout(from_dev(dsrc), layout)
     assert_close(src, gsrc, rtol=1e-6, atol=2e-6, min_snr=120, what="stft")
     rng = np.random.default_rng(5)
     mask = rng.standard_normal(src.shape).astype(np.float32)
     ref = O.istft(d, src, mask, length)
     dout = empty_dev((d.channels, length))
-    dm.istft(to_dev(src), to_dev(mask), length, dout)
+    dm.istft(to_dev(_to_layout(src, layout)), to_dev(_to_layout(mask, layout)), length, dout, layout)
     assert_close(ref, from_dev(dout), rtol=1e-5, atol=1e-6, min_snr=120, what="istft")
     assert T == src.shape[2]
 
@@ -103,8 +116,9 @@ def test_istft_perfect_reconstruction(ctx, cfg2_models):
     assert_close(x, from_dev(dout), rtol=0, atol=2e-6, what="istft(stft(x))")
 
 
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("which", ["config", "reference"])
-def test_band_split_and_mask(ctx, cfg2_models, ref_models, which, rng):
+def test_band_split_and_mask(ctx, cfg2_models, ref_models, which, rng, layout):
     om, dm = cfg2_models if which == "config" else ref_models
     d = om.d
     x = audio.sine_mix(0.3, 4)
@@ -112,13 +126,14 @@ def test_band_split_and_mask(ctx, cfg2_models, ref_models, which, rng):
     T = src.shape[2]
     ref = om.band_split(src)
     dout = empty_dev(ref.shape)
-    dm.band_split(to_dev(src), T, dout)
+    dm.band_split(to_dev(_to_layout(src, layout)), T, dout, layout)
     assert_close(ref, from_dev(dout), rtol=1e-4, atol=2e-5, min_snr=110, what="band split")
     feats = rng.standard_normal((T, d.bands, d.dim), dtype=np.float32)
     mref = om.mask_estimate(feats)
-    dmask = empty_dev(mref.shape)
-    dm.mask_estimate(to_dev(feats), T, dmask)
-    assert_close(mref, from_dev(dmask), rtol=1e-4, atol=1e-5, min_snr=110, what="mask estimator")
+    dmask = empty_dev(_to_layout(mref, layout).shape)
+    dm.mask_estimate(to_dev(feats), T, dmask, layout)
+    assert_close(mref, _from_layout(from_dev(dmask), layout), rtol=1e-4, atol=1e-5, min_snr=110,
+                 what="mask estimator")
 
 
 def test_forward_config_shape(cfg2_models):
