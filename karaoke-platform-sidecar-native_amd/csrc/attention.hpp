@@ -245,22 +245,26 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(AttnArgs a) {
         }
 }
 
-// Short sequences (L <= 64: the band axis).  One (sequence, head) per
-// workgroup with all of its keys staged in LDS at once (one load round trip),
-// four wavefronts of 16 queries on v_mfma_f32_16x16x4f32 (operand lane
-// (i, k) = element [i = lane%16][k = lane/16]; result lane (j, g), register r
-// = row 4g + r, column j), and a single-pass softmax over the 64 keys.
+// Short sequences (L <= 64: the band axis).  A persistent workgroup loops
+// over (sequence, head) tasks; each task has all of its keys staged in LDS
+// at once, and the next task's q/k/v loads are in flight while the current
+// one computes.  Four wavefronts of 16 queries run v_mfma_f32_16x16x4f32
+// (operand lane (i, k) = element [i = lane%16][k = lane/16]; result lane
+// (j, g), register r = row 4g + r, column j) and a single-pass softmax.
 //   S^T tile kt (16 keys x 16 queries) = K * Q^T over 16 steps: k-slot g of
-//     step ds is head dim 16g + ds, so lane (m, g) streams dims 16g..16g+15 of
-//     key row 16kt + m (four 16-byte LDS reads) and holds the same dims of
-//     its own query.  Lane (n, g) receives query n, keys 16kt + 4g + r.
+//     step 4j + e is head dim 16j + 4g + e, so one 16-byte read gives lane
+//     (m, g) the next four steps of key row 16kt + m, and the wave's q
+//     loads read 64 contiguous bytes per 4 lanes.  Lane (n, g) receives
+//     query n, keys 16kt + 4g + r.
 //   O^T tile dt (16 dims x 16 queries) += V^T * P^T: step (kt, r) uses k-slot
-//     g = key 16kt + 4g + r, which is the lane's own probability register;
-//     tile dt holds dims 4m + dt, so one 16-byte read of V row 16kt + 4g + r
-//     (dims 4m..4m+3) feeds all four tiles, and the result lane (n, g) holds
-//     dims 16g + 4r + dt: four 16-byte stores per lane.
-// K and V keep their natural row layout in LDS (pitch 68 floats: the 16 rows
-// or 16 columns of each read phase fall on distinct banks).
+//     g = key 16kt + 4g + r, the lane's own probability register; tile row m
+//     is dim 4*sigma(m) + dt with sigma(4a + b) = 4b + a, so one 16-byte read
+//     of V row 16kt + 4g + r feeds all four tiles, and lane (n, g) ends with
+//     dims 16r + 4g + dt: its four 16-byte stores line up with its neighbours'.
+// K and V keep their natural row layout in LDS (pitch 68 floats: the rows
+// or columns of each 8-lane read phase fall on distinct banks).
+VH_DEVICE int short_sigma(int m) { return 4 * (m & 3) + (m >> 2); }
+
 template <typename TO>
 __global__ __launch_bounds__(256, 4) void attention_short_kernel(AttnArgs a) {
     constexpr int PITCH = ATT_DH + 4;
@@ -269,104 +273,115 @@ __global__ __launch_bounds__(256, 4) void attention_short_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float Vs[KEYS][PITCH];
 
     const float *qkv = static_cast<const float *>(a.qkv);
-    // the heads of one sequence read adjacent slices of the same rows: keep them on one XCD
-    const int task = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);
-    const int h = task % a.H;
-    const int s = task / a.H;
+    const int tasks = a.S * a.H;
     const int tid = (int)threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int kcol = a.inner + h * ATT_DH;
-    const int vcol = 2 * a.inner + h * ATT_DH;
+    const int q = 16 * wave + n;
+    const int qc = min(q, a.L - 1);
+    const int d_st = 4 * (tid & 15);  // staging: keys tid/16 + 16i, dims d_st..d_st+3
 
-    // Stage K (rotated) and V: thread covers keys tid/16 + 16i, dims 4*(tid%16).
-    {
-        const int d0 = 4 * (tid & 15);
+    floatx4 kpre[4], vpre[4], qpre[4];
+    float gpre = 0.0f;
+    auto prefetch = [&](int task) {
+        const int h = task % a.H, s = task / a.H;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int key = (tid >> 4) + 16 * i;
-            floatx4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            kpre[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            vpre[i] = floatx4{0.f, 0.f, 0.f, 0.f};
             if (key < a.L) {
                 const size_t row = (size_t)attn_row(a, s, key) * a.ld;
-                kv = rope4(ld4(qkv + row + kcol + d0), a.rope, key, d0);
-                vv = ld4(qkv + row + vcol + d0);
+                kpre[i] = ld4(qkv + row + a.inner + h * ATT_DH + d_st);
+                vpre[i] = ld4(qkv + row + 2 * a.inner + h * ATT_DH + d_st);
             }
-            st4(&Ks[key][d0], kv);
-            st4(&Vs[key][d0], vv);
         }
-    }
-    // Q of query 16*wave + n, dims 16g .. 16g+15, rotated and scaled to the
-    // log2 domain; the gate logit with it.
-    const int q = 16 * wave + n;
-    const int qc = min(q, a.L - 1);
-    const size_t qrow = (size_t)attn_row(a, s, qc) * a.ld;
-    floatx4 qr[4];
-    {
-        const float qs = a.scale * 1.4426950408889634f;
+        const size_t qrow = (size_t)attn_row(a, s, qc) * a.ld;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int d0 = 16 * g + 4 * j;
-            qr[j] = rope4(ld4(qkv + qrow + h * ATT_DH + d0), a.rope, qc, d0) * qs;
-        }
-    }
-    const float gate_logit = a.gate_col >= 0 ? qkv[qrow + a.gate_col + h] : 0.0f;
-    __syncthreads();
+        for (int j = 0; j < 4; j++) qpre[j] = ld4(qkv + qrow + h * ATT_DH + 16 * j + 4 * g);
+        if (a.gate_col >= 0) gpre = qkv[qrow + a.gate_col + h];
+    };
 
-    floatx4 sc[4];
+    int task = (int)blockIdx.x;
+    if (task < tasks) prefetch(task);
+    for (; task < tasks; task += (int)gridDim.x) {
+        const int h = task % a.H, s = task / a.H;
+        // this task's keys into LDS (K rotated), its queries into registers
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++) {
-        const float *kr = &Ks[16 * kt + n][16 * g];
-        floatx4 k4[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) k4[j] = ld4(kr + 4 * j);
-        sc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ds = 0; ds < 16; ds++)
-            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[ds >> 2][ds & 3], qr[ds >> 2][ds & 3], sc[kt], 0, 0, 0);
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            if (16 * kt + 4 * g + r >= a.L) sc[kt][r] = -INFINITY;
-            m = fmaxf(m, sc[kt][r]);
+        for (int i = 0; i < 4; i++) {
+            const int key = (tid >> 4) + 16 * i;
+            st4(&Ks[key][d_st], rope4(kpre[i], a.rope, key, d_st));
+            st4(&Vs[key][d_st], vpre[i]);
         }
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-    float l = 0.0f;
+        floatx4 qr[4];
+        {
+            const float qs = a.scale * 1.4426950408889634f;
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            sc[kt][r] = __builtin_amdgcn_exp2f(sc[kt][r] - m);
-            l += sc[kt][r];
+            for (int j = 0; j < 4; j++) qr[j] = rope4(qpre[j], a.rope, qc, 16 * j + 4 * g) * qs;
         }
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+        const float gate_logit = gpre;
+        __syncthreads();
+        if (task + (int)gridDim.x < tasks) prefetch(task + (int)gridDim.x);
 
-    floatx4 o[4];
+        floatx4 sc[4];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < 4; kt++) {
+            const float *kr = &Ks[16 * kt + n][4 * g];
+            floatx4 k4[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++)
+            for (int j = 0; j < 4; j++) k4[j] = ld4(kr + 16 * j);
+            sc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const floatx4 vv = ld4(&Vs[16 * kt + 4 * g + r][4 * n]);
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[dt], sc[kt][r], o[dt], 0, 0, 0);
+            for (int ds = 0; ds < 16; ds++)
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[ds >> 2][ds & 3], qr[ds >> 2][ds & 3], sc[kt], 0, 0, 0);
         }
+        float m = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                if (16 * kt + 4 * g + r >= a.L) sc[kt][r] = -INFINITY;
+                m = fmaxf(m, sc[kt][r]);
+            }
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float l = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sc[kt][r] = __builtin_amdgcn_exp2f(sc[kt][r] - m);
+                l += sc[kt][r];
+            }
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
 
-    if (q >= a.L) return;
-    const float f = (1.0f / l) * (a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f);
-    TO *op = static_cast<TO *>(a.out) + (size_t)attn_row(a, s, q) * a.ld_out + h * ATT_DH + 16 * g;
+        floatx4 o[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        floatx4 v;
+        for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const int vcol = 4 * short_sigma(n);
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) v[dt] = o[dt][r] * f;
-        st4(op + 4 * r, v);
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const floatx4 vv = ld4(&Vs[16 * kt + 4 * g + r][vcol]);
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++)
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[dt], sc[kt][r], o[dt], 0, 0, 0);
+            }
+
+        if (q < a.L) {
+            const float f = (1.0f / l) * (a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f);
+            TO *op = static_cast<TO *>(a.out) + (size_t)attn_row(a, s, q) * a.ld_out + h * ATT_DH + 4 * g;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                floatx4 v;
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++) v[dt] = o[dt][r] * f;
+                st4(op + 16 * r, v);
+            }
+        }
+        __syncthreads();  // LDS is refilled for the next task
     }
 }
 

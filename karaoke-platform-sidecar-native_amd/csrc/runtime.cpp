@@ -418,7 +418,10 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
     if (lay.L <= 64 && !qkv_bf16) {
-        const unsigned grid = (unsigned)((int64_t)lay.S * heads);
+        // persistent: four workgroups per CU loop over the (sequence, head) tasks
+        static int cus = 0;
+        if (cus == 0 && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
+        const unsigned grid = (unsigned)std::min<int64_t>((int64_t)lay.S * heads, 4 * (int64_t)cus);
         if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((attention_short_kernel<float>), dim3(grid), dim3(256), 0, s, a);
     } else if (lay.L <= 64)
