@@ -12,36 +12,42 @@ from __future__ import annotations
 
 import csv
 import json
+import re
 import sys
 from pathlib import Path
 
-# kernel-name fragments -> what the launch computes in the separation pass
+# kernel-name patterns (demangled or mangled) -> what the launch computes in
+# the separation pass
 ROLES = [
-    ("gemm_f32_kernel<4", "FFN up-projection + GELU-GLU (fp32)"),
-    ("gemm_f32_kernel<3", "out projection / FFN down-projection + residual (fp32)"),
-    ("gemm_f32_kernel<0", "fused QKV + gate projection (fp32)"),
-    ("gemm_f32_batched_kernel<2", "mask estimator layer 1 + tanh, batched over bands (fp32)"),
-    ("gemm_f32_batched_kernel<0", "band split / mask estimator layer 2, batched over bands (fp32)"),
-    ("gemm_bf16_kernel<4", "FFN up-projection + GELU-GLU (bf16 variant)"),
-    ("gemm_bf16_kernel<3", "out / FFN down-projection + residual (bf16 variant)"),
-    ("gemm_bf16_kernel<0", "fused QKV + gate projection (bf16 variant)"),
-    ("gemm_bf16_batched_kernel<2", "mask layer 1 (bf16 variant)"),
-    ("gemm_bf16_batched_kernel<0", "band split / mask layer 2 (bf16 variant)"),
-    ("attention_kernel<4>", "time-axis attention, L = 801"),
-    ("attention_kernel<2>", "band-axis attention, L = 62"),
-    ("rmsnorm_kernel", "pre-norms and final norm"),
-    ("stft_kernel", "STFT"),
-    ("istft_frames_kernel", "mask multiply + inverse FFT"),
-    ("ola_kernel", "overlap-add"),
-    ("band_gather_norm_kernel", "band gather + RMSNorm"),
-    ("mask_glu_scatter_kernel", "mask GLU + bin scatter"),
-    ("crossfade_kernel", "window cross-fade"),
+    (r"gemm_f32_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32)"),
+    (r"gemm_f32_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32)"),
+    (r"gemm_f32_kernel(<|ILi)0", "fused QKV + gate projection (fp32)"),
+    (r"gemm_f32_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32)"),
+    (r"gemm_f32_batched_kernel(<|ILi)0", "band split / mask estimator layer 2, batched over bands (fp32)"),
+    (r"gemm_bf16_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (bf16 variant)"),
+    (r"gemm_bf16_kernel(<|ILi)3", "out / FFN down-projection + residual (bf16 variant)"),
+    (r"gemm_bf16_kernel(<|ILi)0", "fused QKV + gate projection (bf16 variant)"),
+    (r"gemm_bf16_batched_kernel(<|ILi)2", "mask layer 1 (bf16 variant)"),
+    (r"gemm_bf16_batched_kernel(<|ILi)0", "band split / mask layer 2 (bf16 variant)"),
+    (r"attention_bf16_kernel(<|ILi)4", "time-axis attention, L = 801 (bf16 variant)"),
+    (r"attention_bf16_kernel(<|ILi)2", "band-axis attention, L = 62 (bf16 variant)"),
+    (r"attention_kernel(<|ILi)4", "time-axis attention, L = 801"),
+    (r"attention_short_kernel", "band-axis attention, L = 62"),
+    (r"rmsnorm_kernel", "pre-norms and final norm"),
+    (r"istft_frames_kernel", "mask multiply + inverse FFT"),
+    (r"stft_kernel", "STFT"),
+    (r"ola_kernel", "overlap-add"),
+    (r"band_gather_norm_kernel", "band gather + RMSNorm"),
+    (r"mask_glu_scatter_kernel", "mask GLU + bin scatter"),
+    (r"crossfade_kernel", "window cross-fade"),
+    (r"to_bf16_kernel", "bf16 weight copies (once per model)"),
+    (r"unpack_weight_kernel", "weight upload (once per model)"),
 ]
 
 
 def role(name: str) -> str:
-    for frag, what in ROLES:
-        if frag in name.replace(", ", ",").replace("vh::", ""):
+    for pat, what in ROLES:
+        if re.search(pat, name):
             return what
     return ""
 
@@ -68,7 +74,7 @@ def main() -> int:
                      f"{float(r['AverageNs']) / 1e6:.4f} | {float(r['Percentage']):.2f} |")
     if bench:
         rf = bench["roofline"]
-        dom = next((r for r in rows if "gemm_f32_kernel<4" in r["Name"]), None)
+        dom = next((r for r in rows if re.search(ROLES[0][0], r["Name"])), None)
         lines += ["", f"Dominant kernel: live HIP-event average in bench.py {rf['avg_launch_ms']} ms over "
                       f"{rf['launches']} launches of the timed region; rocprofv3 average over all its launches "
                       f"{float(dom['AverageNs']) / 1e6:.4f} ms ({dom['Calls']} launches)." if dom else "",
