@@ -149,7 +149,7 @@ def bf16_variant(ctx, model, dx, dv, ref_out, length, chunk, step, args, d) -> d
         "ms_per_step": round(wall / args.steps * 1e3, 2),
         "dtype": "bf16 MFMA operands, fp32 accumulation",
         "snr_db_vs_fp32": round(float(snr), 2),
-        "dominant_kernel": {"kernel": "gemm_bf16_kernel<GELU-GLU>", "achieved": round(tf, 2),
+        "dominant_kernel": {"kernel": "gemm_bf16_dma_kernel<GELU-GLU>", "achieved": round(tf, 2),
                             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                             "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
                             "avg_launch_ms": round(ms / max(launches, 1), 4)},

@@ -74,9 +74,12 @@ int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, c
    A is fp32, rounded to bf16 (nearest even) as it is staged, or bf16 with
    VH_BF16_A (then K and lda multiples of 8); C is fp32, or bf16 with
    VH_BF16_C (not with the residual epilogue).  K and lda multiples of 4,
-   A and Wh 16-byte aligned. */
+   A and Wh 16-byte aligned.  bf16 A with K a multiple of 32 runs the
+   pipelined kernel (direct global->LDS loads); VH_BF16_STAGED forces the
+   register-staged kernel instead (same results, bit for bit). */
 #define VH_BF16_A 1
 #define VH_BF16_C 2
+#define VH_BF16_STAGED 4
 int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int lda, const void *Wh, int ldw,
                  const float *bias, void *C, int ldc, int epilogue, int flags);
 /* fp32 src[rows][cols] -> bf16 dst[rows][ld] (round to nearest even). */

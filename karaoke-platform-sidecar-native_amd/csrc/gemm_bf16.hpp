@@ -43,6 +43,57 @@ VH_DEVICE void store_out(T *p, float v) {
     else *p = (bf16)v;
 }
 
+// Fused epilogue of a wave's FM x FN accumulators whose tile starts at
+// (row0, col0).  Accumulator layout as for the fp32 32x32 MFMA: lane (li,
+// lh), register r holds row 8*(r/4) + 4*lh + r%4, column li.
+template <int EPI, typename TC, int FM, int FN>
+VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[FM][FN], int row0, int col0, int li,
+                                  int lh) {
+    TC *C = static_cast<TC *>(d.C);
+    if constexpr (EPI == EPI_GEGLU) {
+        // accumulator pair (2p, 2p+1) = value and gate columns of one 64-wide group
+#pragma unroll
+        for (int p = 0; p < FN / 2; p++) {
+            const int nv = col0 + 64 * p + li;
+            const int ng = nv + 32;
+            const int oc = (col0 + 64 * p) / 2 + li;
+            if (ng >= d.N) continue;
+            const float bv = d.bias ? d.bias[nv] : 0.0f;
+            const float bg = d.bias ? d.bias[ng] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    if (row < d.M)
+                        store_out(C + (size_t)row * d.ldc + oc,
+                                  (acc[i][2 * p][r] + bv) * gelu_dev(acc[i][2 * p + 1][r] + bg));
+                }
+        }
+    } else {
+        static_assert(EPI != EPI_RESIDUAL || std::is_same<TC, float>::value, "residual output is fp32");
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = col0 + j * 32 + li;
+            if (col >= d.N) continue;
+            const float bc = d.bias ? d.bias[col] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    if (row >= d.M) continue;
+                    const float v = acc[i][j][r] + bc;
+                    TC *p = C + (size_t)row * d.ldc + col;
+                    if constexpr (EPI == EPI_STORE) store_out(p, v);
+                    else if constexpr (EPI == EPI_GELU) store_out(p, gelu_dev(v));
+                    else if constexpr (EPI == EPI_TANH) store_out(p, tanhf(v));
+                    else if constexpr (EPI == EPI_RESIDUAL) *p = *p + v;
+                }
+        }
+    }
+}
+
 template <int WM, int WN, int FM, int FN>
 struct BF16Tile {
     static constexpr int BM = 32 * WM * FM, BN = 32 * WN * FN, THREADS = 64 * WM * WN;
@@ -163,55 +214,9 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
         __syncthreads();
     }
 
-    // Accumulator layout as for the fp32 32x32 MFMA: lane (li, lh), register r
-    // holds row 8*(r/4) + 4*lh + r%4, column li.
-    TC *C = static_cast<TC *>(d.C);
-    if constexpr (EPI == EPI_GEGLU) {
-        // accumulator pair (2p, 2p+1) = value and gate columns of one 64-wide group
-#pragma unroll
-        for (int p = 0; p < FN / 2; p++) {
-            const int nv = n0 + wn * 32 * FN + 64 * p + li;
-            const int ng = nv + 32;
-            const int oc = (n0 + wn * 32 * FN + 64 * p) / 2 + li;
-            if (ng >= d.N) continue;
-            const float bv = d.bias ? d.bias[nv] : 0.0f;
-            const float bg = d.bias ? d.bias[ng] : 0.0f;
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * 32 * FM + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (row < d.M)
-                        store_out(C + (size_t)row * d.ldc + oc,
-                                  (acc[i][2 * p][r] + bv) * gelu_dev(acc[i][2 * p + 1][r] + bg));
-                }
-        }
-    } else {
-        static_assert(EPI != EPI_RESIDUAL || std::is_same<TC, float>::value, "residual output is fp32");
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int col = n0 + wn * 32 * FN + j * 32 + li;
-            if (col >= d.N) continue;
-            const float bc = d.bias ? d.bias[col] : 0.0f;
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * 32 * FM + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (row >= d.M) continue;
-                    const float v = acc[i][j][r] + bc;
-                    TC *p = C + (size_t)row * d.ldc + col;
-                    if constexpr (EPI == EPI_STORE) store_out(p, v);
-                    else if constexpr (EPI == EPI_GELU) store_out(p, gelu_dev(v));
-                    else if constexpr (EPI == EPI_TANH) store_out(p, tanhf(v));
-                    else if constexpr (EPI == EPI_RESIDUAL) *p = *p + v;
-                }
-        }
-    }
+    gemm_bf16_epilogue<EPI, TC, FM, FN>(d, acc, m0 + wm * 32 * FM, n0 + wn * 32 * FN, li, lh);
 }
 
-// Second launch-bound argument: workgroups per CU the register budget must
-// allow (OCC * waves per workgroup / 4 waves per SIMD).
 template <int EPI, typename TA, typename TC, int BK, int WM, int WN, int FM, int FN, int OCC>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_kernel(GemmDescBF16 d) {
     gemm_bf16_body<EPI, TA, TC, BK, WM, WN, FM, FN>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
@@ -220,6 +225,145 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_kernel(GemmDescBF
 template <int EPI, typename TA, typename TC, int BK, int WM, int WN, int FM, int FN, int OCC>
 __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_batched_kernel(GemmBatchBF16 b) {
     gemm_bf16_body<EPI, TA, TC, BK, WM, WN, FM, FN>(b.d[blockIdx.z], (int)blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined variant for bf16 A with K % 32 == 0 (every bf16-variant GEMM but
+// the band split): the same 256x128 block of 8 waves x (64x64), but operands
+// reach LDS by direct global->LDS loads (global_load_lds_dwordx4) into a ring
+// of 3 K-chunks, two chunks in flight while the third is multiplied -- about
+// twice the bytes in flight of the register-staged kernel, with no registers
+// spent on staging.  Each wave's load instruction fills 1 KB of LDS: 16 rows
+// of 64 B, lane l carrying row l/4, 16-byte position l%4.  Position p of row
+// r holds K-chunk p ^ ((r / 4) % 4), so the 16-byte operand reads (32 rows,
+// one chunk) fall on distinct banks.  Identical operands and MFMA order to
+// the register-staged kernel, so results are bit-identical.
+//
+// The loads are issued from inline assembly and waited for with explicit
+// s_waitcnt vmcnt(N) + barrier: the compiler's own wait insertion treats any
+// LDS read after an LDS DMA as dependent on all of them (vmcnt(0)), which
+// would serialise the ring.  The asm sets m0 (the LDS base of the DMA) right
+// before each load; these kernels make no other use of m0 (checked on the
+// built library by the boundary tests).
+VH_DEVICE void lds_dma16(const void *gaddr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gaddr), "s"(lds_base) : "memory");
+}
+
+template <int N>
+VH_DEVICE void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+constexpr int GBD_BM = 256, GBD_BN = 128, GBD_BK = 32, GBD_STAGES = 3, GBD_THREADS = 512;
+
+template <int EPI, typename TC>
+__device__ __forceinline__ void gemm_bf16_dma_body(const GemmDescBF16 &d, int tile) {
+    constexpr int BM = GBD_BM, BN = GBD_BN, BK = GBD_BK, STAGES = GBD_STAGES, W = GBD_THREADS / 64;
+    constexpr int A_BYTES = BM * BK * 2, STAGE_BYTES = A_BYTES + BN * BK * 2;
+    constexpr int NA = BM / 16 / W, NB = BN / 16 / W;  // load instructions per wave per chunk
+    static_assert(NA * 16 * W == BM && NB * 16 * W == BN, "loads must tile the chunk");
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[STAGES * STAGE_BYTES];
+
+    const int tiles_n = (d.N + BN - 1) / BN;
+    const int tiles_m = (d.M + BM - 1) / BM;
+    if (tile >= tiles_m * tiles_n) return;
+    const int gsz = (size_t)d.N * d.K * sizeof(bf16) <= (3u << 20) ? 1 : 8;
+    const int group = tile / (gsz * tiles_n);
+    const int in_group = tile % (gsz * tiles_n);
+    const int group_rows = min(gsz, tiles_m - group * gsz);
+    const int m0 = (group * gsz + in_group % group_rows) * BM;
+    const int n0 = (in_group / group_rows) * BN;
+
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves of 64 x 64
+    const int li = lane & 31, lh = lane >> 5;
+    const bf16 *A = static_cast<const bf16 *>(d.A);
+    const uint32_t ring_base = (uint32_t)(uintptr_t)ring;
+    auto swz = [](int r) { return (r >> 2) & 3; };
+
+    const int dr = lane >> 2, dp = lane & 3;
+    const bf16 *a_src[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+        const int r = 16 * (NA * wave + j) + dr;
+        a_src[j] = A + (size_t)min(m0 + r, d.M - 1) * d.lda + 8 * (dp ^ swz(r));
+    }
+    const bf16 *b_src[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const int r = 16 * (NB * wave + j) + dr;
+        b_src[j] = d.B + (size_t)min(n0 + r, d.N - 1) * d.ldb + 8 * (dp ^ swz(r));
+    }
+    auto issue = [&](int kt) {
+        const uint32_t sb = ring_base + (kt % STAGES) * STAGE_BYTES;
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int j = 0; j < NA; j++)
+            lds_dma16(a_src[j] + k0, __builtin_amdgcn_readfirstlane(sb + (NA * wave + j) * 1024));
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+            lds_dma16(b_src[j] + k0, __builtin_amdgcn_readfirstlane(sb + A_BYTES + (NB * wave + j) * 1024));
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // chunk kt lives in slot kt % 3; chunks kt+1 and kt+2 are in flight while
+    // kt is multiplied.  Slot (kt+2) % 3 was last read in iteration kt-1,
+    // which every wave finished before the barrier that ends it.
+    const int nk = d.K / BK;
+    issue(0);
+    if (nk > 1) {
+        issue(1);
+        wait_vmcnt<NA + NB>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        if (kt + 2 < nk) issue(kt + 2);
+        const unsigned char *sbuf = ring + (kt % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int st = 0; st < BK / 16; st++) {
+            bf16x8 a[2], b[2];
+            const int c = 2 * st + lh;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int r = wm * 64 + 32 * i + li;
+                a[i] = *reinterpret_cast<const bf16x8 *>(sbuf + r * 64 + 16 * (c ^ swz(r)));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int r = wn * 64 + 32 * j + li;
+                b[j] = *reinterpret_cast<const bf16x8 *>(sbuf + A_BYTES + r * 64 + 16 * (c ^ swz(r)));
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 2 < nk) wait_vmcnt<NA + NB>();  // chunk kt+1 has landed; kt+2 may still fly
+        else wait_vmcnt<0>();
+        __syncthreads();
+    }
+    gemm_bf16_epilogue<EPI, TC, 2, 2>(d, acc, m0 + wm * 64, n0 + wn * 64, li, lh);
+}
+
+template <int EPI, typename TC>
+__global__ __launch_bounds__(GBD_THREADS, 2) void gemm_bf16_dma_kernel(GemmDescBF16 d) {
+    gemm_bf16_dma_body<EPI, TC>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+}
+
+template <int EPI, typename TC>
+__global__ __launch_bounds__(GBD_THREADS, 2) void gemm_bf16_dma_batched_kernel(GemmBatchBF16 b) {
+    gemm_bf16_dma_body<EPI, TC>(b.d[blockIdx.z], (int)blockIdx.x);
 }
 
 // fp32 [rows][cols] -> bf16 [rows][ld] (weights at upload; padding untouched)

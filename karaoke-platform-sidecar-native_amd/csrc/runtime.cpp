@@ -212,17 +212,35 @@ static GemmDescBF16 to_desc_bf16(const GemmArgsBF16 &g) {
 
 // bf16 GEMM tiling: 8 waves in a 4 x 2 grid, 2 x 2 accumulators (64 x 64) per
 // wave, a 256 x 128 block, K chunks of 32; two workgroups per CU (60 KB of LDS
-// each) = 4 waves per SIMD (122 VGPRs).
+// each) = 4 waves per SIMD (122 VGPRs).  With bf16 A and K % 32 == 0 the same
+// block runs as the global->LDS DMA ring (gemm_bf16_dma_kernel: 72 KB of LDS,
+// two workgroups per CU), which keeps twice the bytes in flight.
 constexpr int BF_WM = 4, BF_WN = 2, BF_FM = 2, BF_FN = 2, BF_BK = 32, BF_OCC = 2;
 using BFTile = BF16Tile<BF_WM, BF_WN, BF_FM, BF_FN>;
+static_assert(BFTile::BM == GBD_BM && BFTile::BN == GBD_BN && BFTile::THREADS == GBD_THREADS,
+              "the DMA ring runs the register-staged kernel's block");
 
 static int64_t tiles_bf16(const GemmArgsBF16 &g) {
     return ((g.M + BFTile::BM - 1) / BFTile::BM) * ((g.N + BFTile::BN - 1) / BFTile::BN);
 }
 
+// The DMA ring takes whole 32-element K chunks of bf16 A (16-byte aligned
+// rows, which gemm_bf16_ok already requires of bf16 A).
+static bool dma_ok(const GemmArgsBF16 &g) { return g.a_bf16 && g.K % GBD_BK == 0 && !g.staged; }
+
 template <int EPI, typename TA, typename TC>
 static void launch_bf16_typed(hipStream_t s, const GemmDescBF16 *single, const GemmBatchBF16 *batch, unsigned tiles,
-                              unsigned n) {
+                              unsigned n, bool dma) {
+    if constexpr (std::is_same<TA, bf16>::value) {
+        if (dma) {
+            if (single)
+                hipLaunchKernelGGL((gemm_bf16_dma_kernel<EPI, TC>), dim3(tiles), dim3(GBD_THREADS), 0, s, *single);
+            else
+                hipLaunchKernelGGL((gemm_bf16_dma_batched_kernel<EPI, TC>), dim3(tiles, 1, n), dim3(GBD_THREADS), 0,
+                                   s, *batch);
+            return;
+        }
+    }
     if (single)
         hipLaunchKernelGGL((gemm_bf16_kernel<EPI, TA, TC, BF_BK, BF_WM, BF_WN, BF_FM, BF_FN, BF_OCC>), dim3(tiles),
                            dim3(BFTile::THREADS), 0, s, *single);
@@ -233,29 +251,29 @@ static void launch_bf16_typed(hipStream_t s, const GemmDescBF16 *single, const G
 
 template <int EPI>
 static void launch_bf16_epi(hipStream_t s, bool a16, bool c16, const GemmDescBF16 *single, const GemmBatchBF16 *batch,
-                            unsigned tiles, unsigned n) {
+                            unsigned tiles, unsigned n, bool dma) {
     if constexpr (EPI == EPI_RESIDUAL) {
-        if (a16) launch_bf16_typed<EPI, bf16, float>(s, single, batch, tiles, n);
-        else launch_bf16_typed<EPI, float, float>(s, single, batch, tiles, n);
+        if (a16) launch_bf16_typed<EPI, bf16, float>(s, single, batch, tiles, n, dma);
+        else launch_bf16_typed<EPI, float, float>(s, single, batch, tiles, n, dma);
     } else {
-        if (a16 && c16) launch_bf16_typed<EPI, bf16, bf16>(s, single, batch, tiles, n);
-        else if (a16) launch_bf16_typed<EPI, bf16, float>(s, single, batch, tiles, n);
-        else if (c16) launch_bf16_typed<EPI, float, bf16>(s, single, batch, tiles, n);
-        else launch_bf16_typed<EPI, float, float>(s, single, batch, tiles, n);
+        if (a16 && c16) launch_bf16_typed<EPI, bf16, bf16>(s, single, batch, tiles, n, dma);
+        else if (a16) launch_bf16_typed<EPI, bf16, float>(s, single, batch, tiles, n, dma);
+        else if (c16) launch_bf16_typed<EPI, float, bf16>(s, single, batch, tiles, n, dma);
+        else launch_bf16_typed<EPI, float, float>(s, single, batch, tiles, n, dma);
     }
 }
 
 static bool launch_bf16(hipStream_t s, int epi, bool a16, bool c16, const GemmDescBF16 *single,
-                        const GemmBatchBF16 *batch, unsigned tiles, unsigned n) {
+                        const GemmBatchBF16 *batch, unsigned tiles, unsigned n, bool dma) {
     switch (epi) {
-        case EPI_STORE: launch_bf16_epi<EPI_STORE>(s, a16, c16, single, batch, tiles, n); break;
-        case EPI_GELU: launch_bf16_epi<EPI_GELU>(s, a16, c16, single, batch, tiles, n); break;
-        case EPI_TANH: launch_bf16_epi<EPI_TANH>(s, a16, c16, single, batch, tiles, n); break;
-        case EPI_RESIDUAL: launch_bf16_epi<EPI_RESIDUAL>(s, a16, c16, single, batch, tiles, n); break;
-        case EPI_GEGLU: launch_bf16_epi<EPI_GEGLU>(s, a16, c16, single, batch, tiles, n); break;
+        case EPI_STORE: launch_bf16_epi<EPI_STORE>(s, a16, c16, single, batch, tiles, n, dma); break;
+        case EPI_GELU: launch_bf16_epi<EPI_GELU>(s, a16, c16, single, batch, tiles, n, dma); break;
+        case EPI_TANH: launch_bf16_epi<EPI_TANH>(s, a16, c16, single, batch, tiles, n, dma); break;
+        case EPI_RESIDUAL: launch_bf16_epi<EPI_RESIDUAL>(s, a16, c16, single, batch, tiles, n, dma); break;
+        case EPI_GEGLU: launch_bf16_epi<EPI_GEGLU>(s, a16, c16, single, batch, tiles, n, dma); break;
         default: set_error("unknown GEMM epilogue %d", epi); return false;
     }
-    return sync_debug(s, "gemm_bf16_kernel");
+    return sync_debug(s, dma ? "gemm_bf16_dma_kernel" : "gemm_bf16_kernel");
 }
 
 bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *t, const char *name) {
@@ -266,7 +284,8 @@ bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *
     }
     GemmDescBF16 d = to_desc_bf16(g);
     Scope sc(t, s, name);
-    return launch_bf16(s, epilogue, g.a_bf16, g.c_bf16, &d, nullptr, (unsigned)tiles_bf16(g), 1);
+    return launch_bf16(s, epilogue, g.a_bf16, g.c_bf16, &d, nullptr, (unsigned)tiles_bf16(g), 1,
+                       dma_ok(g));
 }
 
 bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &gs, int epilogue, KernelTimer *t,
@@ -277,6 +296,7 @@ bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &gs, int e
         GemmBatchBF16 b;
         memset(&b, 0, sizeof(b));
         int64_t max_tiles = 0;
+        bool dma = true;
         for (size_t i = 0; i < count; i++) {
             const GemmArgsBF16 &g = gs[first + i];
             if (!gemm_bf16_ok(g, epilogue) || g.a_bf16 != gs[first].a_bf16 || g.c_bf16 != gs[first].c_bf16) {
@@ -286,9 +306,10 @@ bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &gs, int e
             }
             b.d[i] = to_desc_bf16(g);
             max_tiles = std::max(max_tiles, tiles_bf16(g));
+            dma = dma && dma_ok(g);
         }
         if (!launch_bf16(s, epilogue, gs[first].a_bf16, gs[first].c_bf16, nullptr, &b, (unsigned)max_tiles,
-                         (unsigned)count))
+                         (unsigned)count, dma))
             return false;
     }
     return true;

@@ -99,6 +99,7 @@ struct GemmArgsBF16 {
     void *C; int ldc;        // fp32, or bf16 when c_bf16 (not with the residual epilogue)
     int64_t M; int N, K;
     bool a_bf16 = false, c_bf16 = false;
+    bool staged = false;     // bf16 A with K % 32 == 0: force the register-staged kernel over the DMA ring
 };
 bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *t = nullptr,
                const char *name = "gemm_bf16");

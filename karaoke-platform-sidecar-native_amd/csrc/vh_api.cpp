@@ -140,10 +140,11 @@ extern "C" int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A,
 
 extern "C" int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int lda, const void *Wh, int ldw,
                             const float *bias, void *C, int ldc, int epilogue, int flags) {
-    if (!ctx || (flags & ~(VH_BF16_A | VH_BF16_C))) return 0;
+    if (!ctx || (flags & ~(VH_BF16_A | VH_BF16_C | VH_BF16_STAGED))) return 0;
     GemmArgsBF16 g{A, lda, Wh, ldw, bias, C, ldc, M, N, K};
     g.a_bf16 = (flags & VH_BF16_A) != 0;
     g.c_bf16 = (flags & VH_BF16_C) != 0;
+    g.staged = (flags & VH_BF16_STAGED) != 0;
     return gemm_bf16(ctx->stream, g, epilogue, &ctx->timer, "gemm_bf16") ? 1 : 0;
 }
 

@@ -24,11 +24,11 @@ ROLES = [
     (r"gemm_f32_kernel(<|ILi)0", "fused QKV + gate projection (fp32)"),
     (r"gemm_f32_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32)"),
     (r"gemm_f32_batched_kernel(<|ILi)0", "band split / mask estimator layer 2, batched over bands (fp32)"),
-    (r"gemm_bf16_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (bf16 variant)"),
-    (r"gemm_bf16_kernel(<|ILi)3", "out / FFN down-projection + residual (bf16 variant)"),
-    (r"gemm_bf16_kernel(<|ILi)0", "fused QKV + gate projection (bf16 variant)"),
-    (r"gemm_bf16_batched_kernel(<|ILi)2", "mask layer 1 (bf16 variant)"),
-    (r"gemm_bf16_batched_kernel(<|ILi)0", "band split / mask layer 2 (bf16 variant)"),
+    (r"gemm_bf16_(dma_)?kernel(<|ILi)4", "FFN up-projection + GELU-GLU (bf16 variant)"),
+    (r"gemm_bf16_(dma_)?kernel(<|ILi)3", "out / FFN down-projection + residual (bf16 variant)"),
+    (r"gemm_bf16_(dma_)?kernel(<|ILi)0", "fused QKV + gate projection (bf16 variant)"),
+    (r"gemm_bf16_(dma_)?batched_kernel(<|ILi)2", "mask layer 1 (bf16 variant)"),
+    (r"gemm_bf16_(dma_)?batched_kernel(<|ILi)0", "band split / mask layer 2 (bf16 variant)"),
     (r"attention_bf16_kernel(<|ILi)4", "time-axis attention, L = 801 (bf16 variant)"),
     (r"attention_bf16_kernel(<|ILi)2", "band-axis attention, L = 62 (bf16 variant)"),
     (r"attention_kernel(<|ILi)4", "time-axis attention, L = 801"),

@@ -32,7 +32,7 @@ ABI_SYMBOLS = [
 
 EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16 = 0, 1
-BF16_A, BF16_C = 1, 2  # vh_gemm_bf16 operand flags
+BF16_A, BF16_C, BF16_STAGED = 1, 2, 4  # vh_gemm_bf16 operand flags; STAGED forces the register-staged kernel
 ATT_OUT_BF16, ATT_BF16 = 1, 2  # vh_attention flags
 SPEC_REFERENCE, SPEC_FRAME_MAJOR = 0, 1  # spectrum layouts: [F][C][T][2] / [C][T][F][2]
 
@@ -173,7 +173,7 @@ class Context:
 
     def gemm_bf16(self, A, Wh, C, M: int, N: int, K: int, ldw: int, bias=None, epilogue: int = EPI_STORE,
                   lda: int | None = None, ldc: int | None = None, flags: int = 0):
-        """Wh: bf16 weight copy [N][ldw] (see to_bf16); flags: BF16_A / BF16_C operand types."""
+        """Wh: bf16 weight copy [N][ldw] (see to_bf16); flags: BF16_A / BF16_C operand types, BF16_STAGED."""
         _ok(lib().vh_gemm_bf16(self.h, M, N, K, ptr(A), lda or K, ptr(Wh), ldw,
                                ptr(bias) if bias is not None else None, ptr(C),
                                ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue, flags), "vh_gemm_bf16")

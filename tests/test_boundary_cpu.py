@@ -73,3 +73,49 @@ def test_pack_sizes():
     # native/assets/manifest.json:6
     assert pack.pack_bytes(REFERENCE_DIMS) == 267_386_408
     assert pack.pack_bytes(CONFIG_DIMS) > pack.pack_bytes(CONFIG_DIMS.with_depth(1))
+
+
+LLVM_BIN = Path("/opt/rocm/llvm/bin")
+
+
+def _gfx950_disassembly(tmp_path: Path) -> dict[str, list[str]]:
+    """Instructions per kernel of the library's own gfx950 code object."""
+    for tool in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump"):
+        if not (LLVM_BIN / tool).exists():
+            pytest.skip(f"{tool} not available")
+    fatbin, code = tmp_path / "fatbin", tmp_path / "gfx950.o"
+    subprocess.run([str(LLVM_BIN / "llvm-objcopy"), f"--dump-section=.hip_fatbin={fatbin}", str(native.LIB_PATH),
+                    str(tmp_path / "host.so")], check=True)
+    subprocess.run([str(LLVM_BIN / "clang-offload-bundler"), "--unbundle", "--type=o",
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={fatbin}", f"--output={code}"], check=True)
+    text = subprocess.run([str(LLVM_BIN / "llvm-objdump"), "-d", "--mcpu=gfx950", str(code)], capture_output=True,
+                          text=True, check=True).stdout
+    funcs: dict[str, list[str]] = {}
+    cur = None
+    for line in text.splitlines():
+        m = re.match(r"^[0-9a-f]+ <(.+)>:", line)
+        if m:
+            cur = funcs.setdefault(m.group(1), [])
+        elif cur is not None and line.strip() and not line.startswith("Disassembly"):
+            cur.append(line.split("//")[0].strip())
+    return funcs
+
+
+def test_lds_dma_owns_m0(tmp_path):
+    """The pipelined bf16 GEMM sets m0 (the LDS base of a global->LDS load)
+    from inline assembly, unseen by the compiler: every m0 write in those
+    kernels must directly feed its load, and nothing else may use m0 there."""
+    if not native.LIB_PATH.exists():
+        pytest.skip("library not built")
+    funcs = _gfx950_disassembly(tmp_path)
+    dma = [f for f in funcs if "gemm_bf16_dma" in f]
+    assert len(dma) >= 2, "pipelined bf16 GEMM kernels missing from the library"
+    for f in dma:
+        ins = funcs[f]
+        loads = [i for i, x in enumerate(ins) if x.startswith("global_load_lds")]
+        assert loads, f
+        for i, x in enumerate(ins):
+            if re.search(r"\bm0\b", x):
+                assert re.fullmatch(r"s_mov_b32 m0, s\d+", x), (f, x)
+                assert ins[i + 1].startswith("global_load_lds_dwordx4"), (f, x, ins[i + 1])
+        assert all(re.fullmatch(r"s_mov_b32 m0, s\d+", ins[i - 1]) for i in loads), f

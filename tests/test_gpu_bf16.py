@@ -158,6 +158,45 @@ def test_gemm_bf16_operand_types_exact(ctx, rng, epi):
         assert torch.equal(c16.view(torch.int16), c32.to(torch.bfloat16).view(torch.int16)), f"flags {flags}"
 
 
+DMA_CASES = [
+    # M, N, K, epilogue, output bf16: K = 32 / 64 / 96 give rings of 1 / 2 / 3 chunks
+    (300, 200, 32, 0, False),
+    (257, 130, 64, 1, True),
+    (513, 384, 96, 3, False),
+    (1000, 1536, 384, 4, True),
+    (77, 384, 1536, 2, False),
+    (4097, 768, 384, 0, True),
+    (1, 8, 32, 0, False),
+]
+
+
+@pytest.mark.parametrize("M,N,K,epi,c16", DMA_CASES)
+def test_gemm_bf16_dma_matches_staged(ctx, rng, M, N, K, epi, c16):
+    """bf16 A with K % 32 == 0 runs the global->LDS DMA ring; it must equal
+    the register-staged kernel (same operands, same MFMA order) bit for bit."""
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    b = to_dev(rng.standard_normal(N).astype(np.float32))
+    wh, ld = _dev_bf16(ctx, w)
+    xh = torch.empty(M, K, dtype=torch.bfloat16, device="cuda:0")
+    ctx.to_bf16(to_dev(x), xh, M, K, K)
+    cols = N // 2 if epi == native.EPI_GEGLU else N
+    c0 = rng.standard_normal((M, cols), dtype=np.float32)
+    flags = native.BF16_A | (native.BF16_C if c16 else 0)
+    outs = []
+    for extra in (0, native.BF16_STAGED):
+        c = to_dev(c0).to(torch.bfloat16) if c16 else to_dev(c0)
+        ctx.gemm_bf16(xh, wh, c, M, N, K, ld, bias=b, epilogue=epi, flags=flags | extra)
+        outs.append(c)
+    torch.cuda.synchronize()
+    view = torch.int16 if c16 else torch.int32
+    assert torch.equal(outs[0].view(view), outs[1].view(view)), f"{M}x{N}x{K} epi{epi}"
+    ref = _ref_linear(x, w, from_dev(b))
+    if epi == native.EPI_STORE and not c16:
+        assert_close(ref.astype(np.float32), from_dev(outs[0]), rtol=1e-5, atol=1e-5 * (np.sqrt(K) * 0.2 + 1),
+                     what="dma gemm")
+
+
 def test_gemm_bf16_operand_alignment_checks(ctx):
     wh = torch.zeros(64, 24, dtype=torch.bfloat16, device="cuda:0")
     xh = torch.zeros(8, 20, dtype=torch.bfloat16, device="cuda:0")
