@@ -82,6 +82,19 @@ int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, c
 #define VH_BF16_STAGED 4
 int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int lda, const void *Wh, int ldw,
                  const float *bias, void *C, int ldc, int epilogue, int flags);
+/* vh_gemm in fp32 accuracy on bf16 matrix cores: every fp32 value is the
+   exact sum of three bf16 pieces (h = bf16(x), m = bf16(x - h),
+   l = x - h - m) and the six piece products that reach 2^-24 of a product
+   are accumulated in fp32.  Ws: the weight's pieces from vh_split_weights,
+   three planes [3][N][ldw] (plane stride N * ldw, ldw a multiple of 8 and
+   >= K).  K a multiple of 16, lda a multiple of 4, A and Ws 16-byte aligned.
+   The token-wise linear of native/vocalarc_separation.c:631-636, as vh_gemm. */
+int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws, int ldw,
+                  const float *bias, float *C, int ldc, int epilogue);
+/* fp32 W[N][ldw_in] -> the three bf16 planes of vh_gemm_split, [3][N][ld]:
+   plane p holds piece p (h, m, l) of W[n][k] at n * ld + slot(k), where
+   within every group of 16 k the slots are k 0-3, 8-11, 4-7, 12-15. */
+int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Ws, int ld);
 /* fp32 src[rows][cols] -> bf16 dst[rows][ld] (round to nearest even). */
 int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld);
 /* Fused attention core over qkv[S*L][3*H*64] (rotary applied here):
@@ -100,13 +113,20 @@ int vh_attention(vh_context *ctx, int sequences, int length, int heads, const vo
 vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const void *pack, size_t bytes);
 void vh_model_free(vh_model *model);
 /* Arithmetic of the model's matrix products (every linear of the transformer
-   stack, band split and mask estimator): VH_PRECISION_FP32 (default; fp32
-   MFMA, the parity path) or VH_PRECISION_BF16 (activations rounded to bf16
-   as they enter the matrix cores, bf16 weight copies made on the first
-   switch, fp32 accumulation, normalisation, softmax and DSP).  The reference
-   CUDA provider's counterpart is its TF32 switch (native/native_gpu_cuda.cu:566-570). */
+   stack, band split and mask estimator):
+   VH_PRECISION_FP32 (default, the parity path): fp32 accuracy.  The
+     transformer linears run on bf16 matrix cores by exact operand splitting
+     (vh_gemm_split; split planes made at load), every other product on the
+     fp32 MFMA instruction.
+   VH_PRECISION_FP32_MFMA: every product on the fp32 MFMA instruction.
+   VH_PRECISION_BF16: activations rounded to bf16 as they enter the matrix
+     cores, bf16 weight copies made on the first switch, fp32 accumulation,
+     normalisation, softmax and DSP (separately reported variant).
+   The reference CUDA provider's counterpart is its TF32 switch
+   (native/native_gpu_cuda.cu:566-570). */
 #define VH_PRECISION_FP32 0
 #define VH_PRECISION_BF16 1
+#define VH_PRECISION_FP32_MFMA 2
 int vh_model_set_precision(vh_model *model, int precision);
 /* One axial transformer (native/vocalarc_separation.c:836-873) in place on
    device x[S][L][dim]; axis 0 = time weights, 1 = band weights. */

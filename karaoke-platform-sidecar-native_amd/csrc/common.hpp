@@ -8,6 +8,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 #define VH_DEVICE __device__ __forceinline__
+#define VH_HOST_DEVICE __host__ __device__
 
 // 64-lane wavefront reductions through cross-lane permutes.
 VH_DEVICE float wave_sum(float v) {

@@ -1,0 +1,210 @@
+// fp32 token-wise linear on bf16 matrix cores by exact operand splitting:
+// C[M][N] (op)= A[M][K] * W[N][K]^T with fp32 inputs, fp32 accumulation and
+// the fused epilogues of the fp32 GEMM (gemm.hpp).
+//
+// Splitting.  Every fp32 x is the exact sum of three bf16 values
+//   h = bf16(x),  m = bf16(x - h),  l = x - h - m
+// (round to nearest even at each step; x - h and x - h - m are exact in fp32
+// by Sterbenz, and the last remainder has at most 8 significant bits, so l
+// holds it exactly: 3 x 8 bits cover fp32's 24).  With |m| <= 2^-8 |x| and
+// |l| <= 2^-16 |x|, the product a*w = sum of nine bf16 x bf16 products, each
+// exact in fp32.  The kernel accumulates the six that can reach 2^-24 |a||w|
+// (hh, hm, mh, mm, hl, lh) in fp32 and drops ml, lm and ll (together at most
+// 2^-23 |a||w|, below the rounding of the fp32 accumulation itself).  Six
+// v_mfma_f32_32x32x16_bf16 products per 16 k-values cost 6/16 of a bf16 MFMA
+// each, i.e. 2.67x the fp32 MFMA rate (v_mfma_f32_32x32x2f32) per fp32 MAC;
+// measured error against fp64 is at or below the fp32 MFMA GEMM's.
+//
+// Operands.  W is split once, at upload, into three bf16 planes [3][N][ld]
+// with k permuted inside every group of 16 (16-byte slot 0 holds k 0-3 and
+// 8-11, slot 1 holds k 4-7 and 12-15) so a lane's eight k-values for the
+// MFMA are one 16-byte read.  A stays fp32 in memory (no producer changes);
+// each wave splits the A values it reads from LDS in registers.
+//
+// Pipeline.  256x128 block, 8 waves in a 4x2 grid of 64x64 (2x2 32x32
+// accumulators), K in chunks of 16.  Operands go straight from global memory
+// to LDS (global_load_lds_dwordx4, as gemm_bf16_dma_kernel) into a 2-chunk
+// ring: A as fp32 rows of 64 B (4 slots, slot c of row r at c ^ (r/4)%4),
+// each W plane as rows of 32 B (2 slots, slot s of row r at s ^ (r/8)%2), so
+// the operand reads are conflict-free.  56 KB of LDS, two workgroups per CU.
+#pragma once
+
+#include "gemm_bf16.hpp"
+
+namespace vh {
+
+struct GemmDescSplit {
+    const float *A;     // fp32 [M][lda]
+    const bf16 *W;      // three bf16 planes [3][N][ldw], k-permuted
+    const float *bias;  // fp32, may be null
+    float *C;           // fp32 [M][ldc]
+    int M, N, K;
+    int lda, ldw, ldc;
+    int64_t plane;      // elements between planes (>= N * ldw)
+};
+
+constexpr int GS_BM = 256, GS_BN = 128, GS_BK = 16, GS_THREADS = 512;
+
+// Index of k inside its W plane row (the 16-group permutation above).
+VH_HOST_DEVICE inline int split_k_slot(int k) {
+    const int r = k & 15;
+    return (k & ~15) + 8 * ((r >> 2) & 1) + (r & 3) + 4 * (r >> 3);
+}
+
+VH_DEVICE void split3(float x, bf16 &h, bf16 &m, bf16 &l) {
+    h = (bf16)x;
+    const float r1 = x - (float)h;
+    m = (bf16)r1;
+    l = (bf16)(r1 - (float)m);
+}
+
+// Eight fp32 values (two float4) -> their h, m, l bf16 pieces.
+VH_DEVICE void split8(floatx4 lo, floatx4 hi, bf16x8 &h, bf16x8 &m, bf16x8 &l) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        bf16 a, b, c;
+        split3(lo[e], a, b, c);
+        h[e] = a; m[e] = b; l[e] = c;
+        split3(hi[e], a, b, c);
+        h[4 + e] = a; m[4 + e] = b; l[4 + e] = c;
+    }
+}
+
+template <int EPI>
+__device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile) {
+    constexpr int A_BYTES = GS_BM * GS_BK * 4;  // 16 KB: fp32 rows of 64 B
+    constexpr int P_BYTES = GS_BN * GS_BK * 2;  // 4 KB per W plane: bf16 rows of 32 B
+    constexpr int STAGE_BYTES = A_BYTES + 3 * P_BYTES;
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[2 * STAGE_BYTES];
+
+    const int tiles_n = (d.N + GS_BN - 1) / GS_BN;
+    const int tiles_m = (d.M + GS_BM - 1) / GS_BM;
+    if (tile >= tiles_m * tiles_n) return;
+    // column-fastest order within groups of row tiles (see gemm.hpp)
+    const int gsz = (size_t)d.N * d.K * 6 <= (3u << 20) ? 1 : 8;
+    const int group = tile / (gsz * tiles_n);
+    const int in_group = tile % (gsz * tiles_n);
+    const int group_rows = min(gsz, tiles_m - group * gsz);
+    const int m0 = (group * gsz + in_group % group_rows) * GS_BM;
+    const int n0 = (in_group / group_rows) * GS_BN;
+
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 31, lh = lane >> 5;
+    const uint32_t ring_base = (uint32_t)(uintptr_t)ring;
+    auto swz_a = [](int r) { return (r >> 2) & 3; };
+    auto swz_w = [](int r) { return (r >> 3) & 1; };
+
+    // Each load instruction fills 1 KB of the stage.  A: 16 blocks of 16 rows
+    // (lane -> row l/4, slot l%4); wave w loads blocks w and w+8.  W: 12
+    // blocks of 32 rows (plane b/4; lane -> row l/2, slot l%2); wave w loads
+    // block w, and waves 0-3 also block w+8.
+    const float *a_src[2];
+    uint32_t a_off[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int q = wave + 8 * j;
+        const int r = 16 * q + (lane >> 2);
+        a_src[j] = d.A + (size_t)min(m0 + r, d.M - 1) * d.lda + 4 * ((lane & 3) ^ swz_a(r));
+        a_off[j] = q * 1024;
+    }
+    const bf16 *w_src[2];
+    uint32_t w_off[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int b = min(wave + 8 * j, 11);
+        const int r = 32 * (b & 3) + (lane >> 1);
+        w_src[j] = d.W + (b >> 2) * d.plane + (size_t)min(n0 + r, d.N - 1) * d.ldw + 8 * ((lane & 1) ^ swz_w(r));
+        w_off[j] = A_BYTES + b * 1024;
+    }
+    const bool two_w = wave < 4;
+    auto issue = [&](int kt) {
+        const uint32_t sb = ring_base + (kt & 1) * STAGE_BYTES;
+        const int k0 = kt * GS_BK;
+        lds_dma16(a_src[0] + k0, __builtin_amdgcn_readfirstlane(sb + a_off[0]));
+        lds_dma16(a_src[1] + k0, __builtin_amdgcn_readfirstlane(sb + a_off[1]));
+        lds_dma16(w_src[0] + k0, __builtin_amdgcn_readfirstlane(sb + w_off[0]));
+        if (two_w) lds_dma16(w_src[1] + k0, __builtin_amdgcn_readfirstlane(sb + w_off[1]));
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // Accumulator columns past N (the ragged last column tile) are skipped
+    // as a whole: one wave-uniform branch per chunk, not one per MFMA.
+    const bool live1 = n0 + wn * 64 + 32 < d.N;
+    const bool live0 = n0 + wn * 64 < d.N;
+    const int nk = d.K / GS_BK;
+    issue(0);
+    wait_vmcnt<0>();
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        // chunk kt+1 goes to the slot chunk kt-1 used: every wave finished
+        // reading it before the barrier that ended the previous iteration
+        if (kt + 1 < nk) issue(kt + 1);
+        const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
+        bf16x8 ah[2], am[2], al[2], wh[2], wmd[2], wl[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int r = wm * 64 + 32 * i + li;
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * (lh ^ swz_a(r)));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * ((2 + lh) ^ swz_a(r)));
+            split8(lo, hi, ah[i], am[i], al[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int r = wn * 64 + 32 * j + li;
+            const unsigned char *wp = sbuf + A_BYTES + r * 32 + 16 * (lh ^ swz_w(r));
+            wh[j] = *reinterpret_cast<const bf16x8 *>(wp);
+            wmd[j] = *reinterpret_cast<const bf16x8 *>(wp + P_BYTES);
+            wl[j] = *reinterpret_cast<const bf16x8 *>(wp + 2 * P_BYTES);
+        }
+        // small products first: (l,h) (h,l) (m,m) (m,h) (h,m) (h,h)
+        const bf16x8 *pa[6] = {al, ah, am, am, ah, ah};
+        const bf16x8 *pw[6] = {wh, wl, wmd, wh, wmd, wh};
+        auto products = [&](auto nj) {
+#pragma unroll
+            for (int t = 0; t < 6; t++)
+#pragma unroll
+                for (int j = 0; j < decltype(nj)::value; j++)
+#pragma unroll
+                    for (int i = 0; i < 2; i++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[t][i], pw[t][j], acc[i][j], 0, 0, 0);
+        };
+        if (live1) products(std::integral_constant<int, 2>());
+        else if (live0) products(std::integral_constant<int, 1>());
+        wait_vmcnt<0>();  // chunk kt+1 has landed
+        __syncthreads();
+    }
+    GemmDescBF16 e{};
+    e.bias = d.bias; e.C = d.C; e.M = d.M; e.N = d.N; e.K = d.K; e.ldc = d.ldc;
+    gemm_bf16_epilogue<EPI, float, 2, 2>(e, acc, m0 + wm * 64, n0 + wn * 64, li, lh);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(GS_THREADS, 2) void gemm_split_kernel(GemmDescSplit d) {
+    gemm_split_body<EPI>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+}
+
+// fp32 W [N][ldw_in] -> its h, m, l planes [3][N][ld] (k permuted as above;
+// columns K..ld-1 of every plane are left untouched).
+static __global__ __launch_bounds__(256) void split_weight_kernel(const float *__restrict__ W, int N, int K, int ldw_in,
+                                                                 bf16 *__restrict__ planes, int ld, int64_t plane) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)N * K) return;
+    const int n = (int)(idx / K), k = (int)(idx % K);
+    bf16 h, m, l;
+    split3(W[(size_t)n * ldw_in + k], h, m, l);
+    const size_t o = (size_t)n * ld + split_k_slot(k);
+    planes[o] = h;
+    planes[plane + o] = m;
+    planes[2 * plane + o] = l;
+}
+
+}  // namespace vh

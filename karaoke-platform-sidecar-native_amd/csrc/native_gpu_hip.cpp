@@ -77,6 +77,7 @@ struct CacheEntry {
     uint64_t fp;
     float *dev;
     float *dev_bias;   // fused QKV+gate bias
+    void *dev_split = nullptr;  // split planes of dev (made on first use)
 };
 
 }  // namespace
@@ -115,6 +116,7 @@ struct native_gpu {
                 // same address, different contents: a reloaded pack
                 (void)hipFree(e.dev);
                 if (e.dev_bias) (void)hipFree(e.dev_bias);
+                if (e.dev_split) (void)hipFree(e.dev_split);
                 e = cache.back();
                 cache.pop_back();
                 return nullptr;
@@ -133,6 +135,30 @@ struct native_gpu {
         }
         cache.push_back({host, nullptr, in, out, mode, fp, dev, nullptr});
         return dev;
+    }
+
+    // Split planes (gemm_split) of a cached device matrix [out][in]; null
+    // when `in` is not a multiple of 16 (the fp32 MFMA GEMM serves it).
+    // VOCALARC_GPU_SPLIT=0 keeps every product on the fp32 MFMA instruction.
+    const void *split(const float *dev, int in, int out) {
+        static const bool off = [] {
+            const char *v = getenv("VOCALARC_GPU_SPLIT");
+            return v && strcmp(v, "0") == 0;
+        }();
+        if (off || !dev || in % SPLIT_K_MULTIPLE) return nullptr;
+        for (auto &e : cache) {
+            if (e.dev != dev) continue;
+            if (e.dev_split) return e.dev_split;
+            void *p = nullptr;
+            if (!check(hipMalloc(&p, split_bytes(out, in)), "hipMalloc(split weight)")) return nullptr;
+            if (!split_weights(stream, dev, out, in, in, p, split_pitch(in))) {
+                (void)hipFree(p);
+                return nullptr;
+            }
+            e.dev_split = p;
+            return p;
+        }
+        return nullptr;
     }
 
     const float *vector(const float *host, int n) {
@@ -193,7 +219,12 @@ struct native_gpu {
         L.b1 = const_cast<float *>(vector(w->ff1_bias, d.ff_dim));
         L.w2 = const_cast<float *>(matrix(w->ff2_weight, d.ff_dim, D));
         L.b2 = const_cast<float *>(vector(w->ff2_bias, D));
-        return L.gamma && L.ff_gamma && L.wout && L.w1 && L.b1 && L.w2 && L.b2;
+        if (!(L.gamma && L.ff_gamma && L.wout && L.w1 && L.b1 && L.w2 && L.b2)) return false;
+        L.wqkvg_s = const_cast<void *>(split(L.wqkvg, D, d.qkvg_dim()));
+        L.wout_s = const_cast<void *>(split(L.wout, d.inner(), D));
+        L.w1_s = const_cast<void *>(split(L.w1, D, d.ff1_out()));
+        L.w2_s = const_cast<void *>(split(L.w2, d.ff_dim, D));
+        return true;
     }
 
     // ---- resident layout ----------------------------------------------------
@@ -255,6 +286,7 @@ extern "C" void native_gpu_destroy(native_gpu *gpu) {
     for (auto &e : gpu->cache) {
         (void)hipFree(e.dev);
         if (e.dev_bias) (void)hipFree(e.dev_bias);
+        if (e.dev_split) (void)hipFree(e.dev_split);
     }
     gpu->cache.clear();
     hipStream_t s = gpu->stream;
@@ -308,11 +340,18 @@ extern "C" int native_gpu_matmul(native_gpu *gpu, int64_t rows, int in, int out,
     const float *W = gpu->matrix(packed_weight, in, out);
     const float *B = bias ? gpu->vector(bias, out) : nullptr;
     if (!W || (bias && !B)) return gpu->fail("weight upload");
+    const void *Ws = gpu->split(W, in, out);
     const size_t ib = (size_t)rows * in * sizeof(float), ob = (size_t)rows * out * sizeof(float);
     hipStream_t s = gpu->stream;
+    auto product = [&]() {
+        if (Ws)
+            return gemm_split(s, {gpu->io_in.f(), in, Ws, split_pitch(in), (int64_t)out * split_pitch(in), B,
+                                  gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
+        return gemm(s, {gpu->io_in.f(), in, W, in, B, gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
+    };
     bool ok = gpu->io_in.ensure(ib, "hipMalloc(matmul input)") && gpu->io_out.ensure(ob, "hipMalloc(matmul output)") &&
               check(hipMemcpyAsync(gpu->io_in.ptr, input, ib, hipMemcpyHostToDevice, s), "hipMemcpy(matmul input)") &&
-              gemm(s, {gpu->io_in.f(), in, W, in, B, gpu->io_out.f(), out, rows, out, in}, EPI_STORE) &&
+              product() &&
               check(hipMemcpyAsync(output, gpu->io_out.ptr, ob, hipMemcpyDeviceToHost, s), "hipMemcpy(matmul output)") &&
               check(hipStreamSynchronize(s), "hipStreamSynchronize(matmul)");
     if (!ok) return gpu->fail("matmul");

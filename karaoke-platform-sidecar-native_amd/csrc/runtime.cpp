@@ -14,6 +14,7 @@
 #include "elementwise.hpp"
 #include "gemm.hpp"
 #include "gemm_bf16.hpp"
+#include "gemm_split.hpp"
 
 namespace vh {
 
@@ -315,6 +316,57 @@ bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &gs, int e
     return true;
 }
 
+// ------------------------------------------------------------ split GEMM
+static_assert(GS_BK == SPLIT_K_MULTIPLE, "split GEMM K chunk");
+
+static bool gemm_split_ok(const GemmArgsSplit &g, int epilogue) {
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2) return false;
+    if (g.K % GS_BK || g.lda % 4 || g.lda < g.K || g.ldw % 8 || g.ldw < g.K) return false;
+    if (g.plane < (int64_t)g.N * g.ldw) return false;
+    if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
+    if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return false;
+    return true;
+}
+
+template <int EPI>
+static void launch_split(hipStream_t s, const GemmDescSplit &d, unsigned tiles) {
+    hipLaunchKernelGGL(gemm_split_kernel<EPI>, dim3(tiles), dim3(GS_THREADS), 0, s, d);
+}
+
+bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer *t, const char *name) {
+    if (!gemm_split_ok(g, epilogue)) {
+        set_error("gemm_split: unsupported shape M=%lld N=%d K=%d lda=%d ldw=%d", (long long)g.M, g.N, g.K, g.lda,
+                  g.ldw);
+        return false;
+    }
+    GemmDescSplit d;
+    d.A = g.A; d.W = static_cast<const bf16 *>(g.W); d.bias = g.bias; d.C = g.C;
+    d.M = (int)g.M; d.N = g.N; d.K = g.K;
+    d.lda = g.lda; d.ldw = g.ldw; d.ldc = g.ldc; d.plane = g.plane;
+    const unsigned tiles = (unsigned)(((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
+    Scope sc(t, s, name);
+    switch (epilogue) {
+        case EPI_STORE: launch_split<EPI_STORE>(s, d, tiles); break;
+        case EPI_GELU: launch_split<EPI_GELU>(s, d, tiles); break;
+        case EPI_TANH: launch_split<EPI_TANH>(s, d, tiles); break;
+        case EPI_RESIDUAL: launch_split<EPI_RESIDUAL>(s, d, tiles); break;
+        case EPI_GEGLU: launch_split<EPI_GEGLU>(s, d, tiles); break;
+        default: set_error("unknown GEMM epilogue %d", epilogue); return false;
+    }
+    return sync_debug(s, "gemm_split_kernel");
+}
+
+bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *planes, int ld) {
+    if (N <= 0 || K <= 0 || ldw < K || ld < K || (int64_t)N * ld > INT32_MAX) {
+        set_error("split_weights: bad shape N=%d K=%d ldw=%d ld=%d", N, K, ldw, ld);
+        return false;
+    }
+    const int64_t n = (int64_t)N * K;
+    hipLaunchKernelGGL(split_weight_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, W, N, K, ldw,
+                       static_cast<bf16 *>(planes), ld, (int64_t)N * ld);
+    return sync_debug(s, "split_weight_kernel");
+}
+
 bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst, int ld) {
     const int64_t n = (int64_t)rows * cols;
     hipLaunchKernelGGL(to_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, src, static_cast<bf16 *>(dst),
@@ -564,19 +616,25 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
         if (!lin(normed, D, w.w1_h, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, true, "gemm_ff1")) return false;
         return lin(hid, d.ff_dim, w.w2_h, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, false, "gemm_ff2");
     }
+    // fp32 linears: split planes on bf16 matrix cores, or the fp32 MFMA GEMM
+    auto lin = [&](const float *A, int lda, const float *W, const void *Ws, const float *bias, float *C, int ldc, int N,
+                   int K, int epi, const char *name) {
+        if (Ws && precision == PREC_FP32 && K % SPLIT_K_MULTIPLE == 0)
+            return gemm_split(s, {A, lda, Ws, split_pitch(K), (int64_t)N * split_pitch(K), bias, C, ldc, tokens, N, K},
+                              epi, t, name);
+        return gemm(s, {A, lda, W, K, bias, C, ldc, tokens, N, K}, epi, t, name);
+    };
     // pre-norm -> fused QKV (+gate logits with their bias)
     if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
-    if (!gemm(s, {normed, D, w.wqkvg, D, w.bqkvg, qkvg, nq, tokens, nq, D}, EPI_STORE, t, "gemm_qkv")) return false;
+    if (!lin(normed, D, w.wqkvg, w.wqkvg_s, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
     // rotary + attention + gates
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t)) return false;
     // out projection added to the residual stream
-    if (!gemm(s, {attn, inner, w.wout, inner, nullptr, x, D, tokens, D, inner}, EPI_RESIDUAL, t, "gemm_out")) return false;
+    if (!lin(attn, inner, w.wout, w.wout_s, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;
     // FFN
     if (!rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
-    if (!gemm(s, {normed, D, w.w1, D, w.b1, hid, d.ff_dim, tokens, d.ff1_out(), D}, ff1_epi, t, "gemm_ff1")) return false;
-    if (!gemm(s, {hid, d.ff_dim, w.w2, d.ff_dim, w.b2, x, D, tokens, D, d.ff_dim}, EPI_RESIDUAL, t, "gemm_ff2"))
-        return false;
-    return true;
+    if (!lin(normed, D, w.w1, w.w1_s, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, "gemm_ff1")) return false;
+    return lin(hid, d.ff_dim, w.w2, w.w2_s, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, "gemm_ff2");
 }
 
 // ---------------------------------------------------------------- upload

@@ -105,6 +105,27 @@ bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *
                const char *name = "gemm_bf16");
 bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &g, int epilogue, KernelTimer *t = nullptr,
                        const char *name = "gemm_bf16_batched");
+// fp32-accurate linear on bf16 matrix cores (gemm_split.hpp): A fp32, W as
+// three bf16 planes [3][N][ldw] from split_weights, C fp32.  K a multiple of
+// 16; lda a multiple of 4 and ldw of 8; A and W 16-byte aligned.
+struct GemmArgsSplit {
+    const float *A; int lda;
+    const void *W; int ldw; int64_t plane;
+    const float *bias;
+    float *C; int ldc;
+    int64_t M; int N, K;
+};
+bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer *t = nullptr,
+                const char *name = "gemm_split");
+// K granularity of gemm_split; row pitch of split planes for K columns, and
+// the bytes of the three planes.
+constexpr int SPLIT_K_MULTIPLE = 16;
+inline int split_pitch(int K) { return (K + 15) / 16 * 16; }
+inline size_t split_bytes(int N, int K) { return (size_t)3 * N * split_pitch(K) * 2; }
+// fp32 W [N][ldw] -> three bf16 planes [3][N][ld], plane stride N * ld
+// (h = bf16(w), m = bf16(w - h), l = w - h - m; k permuted within groups of 16).
+bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *planes, int ld);
+
 // fp32 [rows][cols] -> bf16 [rows][ld] (ld >= cols, padding zeroed by the caller)
 bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst, int ld);
 inline int bf16_pitch(int k) { return (k + 7) & ~7; }
@@ -158,11 +179,17 @@ struct LayerWeights {
     float *w2 = nullptr, *b2 = nullptr;        // [D][ff_dim]
     // bf16 copies for the reduced-precision variant (null: fp32 only)
     void *wqkvg_h = nullptr, *wout_h = nullptr, *w1_h = nullptr, *w2_h = nullptr;
+    // split planes (split_weights) for the fp32 path on bf16 matrix cores
+    // (null: the fp32 MFMA GEMM runs instead)
+    void *wqkvg_s = nullptr, *wout_s = nullptr, *w1_s = nullptr, *w2_s = nullptr;
 };
 
-// Arithmetic of the matrix products: fp32 MFMA (parity path) or bf16 MFMA
-// with fp32 accumulation (separately reported variant).
-enum Precision : int { PREC_FP32 = 0, PREC_BF16 = 1 };
+// Arithmetic of the matrix products.  PREC_FP32 (the parity path): fp32
+// accuracy, the transformer linears on bf16 matrix cores by exact operand
+// splitting where split planes exist, the fp32 MFMA GEMM elsewhere.
+// PREC_FP32_MFMA: every product on the fp32 MFMA instruction.  PREC_BF16:
+// bf16 operands with fp32 accumulation (separately reported variant).
+enum Precision : int { PREC_FP32 = 0, PREC_BF16 = 1, PREC_FP32_MFMA = 2 };
 
 // Rotary cos/sin tables per sequence length, built on the host with the
 // reference's float expressions (native/vocalarc_separation.c:726-731,1312).

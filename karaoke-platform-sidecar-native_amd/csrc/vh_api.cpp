@@ -47,6 +47,8 @@ struct vh_model {
     // bf16 copies of every matrix (built on the first switch to bf16)
     int precision = PREC_FP32;
     DeviceBuffer weights_h;
+    // split planes of the transformer matrices (built at load)
+    DeviceBuffer weights_s;
     std::vector<void *> band_w_h, mask_w1_h, mask_w2_h;
     // DSP constants
     DeviceBuffer window, twiddle;
@@ -146,6 +148,21 @@ extern "C" int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void
     g.c_bf16 = (flags & VH_BF16_C) != 0;
     g.staged = (flags & VH_BF16_STAGED) != 0;
     return gemm_bf16(ctx->stream, g, epilogue, &ctx->timer, "gemm_bf16") ? 1 : 0;
+}
+
+extern "C" int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws, int ldw,
+                             const float *bias, float *C, int ldc, int epilogue) {
+    if (!ctx) return 0;
+    GemmArgsSplit g{A, lda, Ws, ldw, (int64_t)N * ldw, bias, C, ldc, M, N, K};
+    return gemm_split(ctx->stream, g, epilogue, &ctx->timer, "gemm_split") ? 1 : 0;
+}
+
+extern "C" int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Ws, int ld) {
+    if (!ctx || !W || !Ws || ld % 8) {
+        set_error("vh_split_weights: bad arguments (ld a multiple of 8)");
+        return 0;
+    }
+    return split_weights(ctx->stream, W, N, K, ldw_in, Ws, ld) ? 1 : 0;
 }
 
 extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld) {
@@ -380,6 +397,33 @@ bool prepare_bf16(vh_model *m) {
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(bf16 weights)");
 }
 
+// Split planes (three bf16 pieces) of the transformer matrices whose K is a
+// multiple of 16: the fp32 path's linears on bf16 matrix cores.
+bool prepare_split(vh_model *m) {
+    if (m->weights_s.ptr) return true;
+    const Dims &d = m->d;
+    hipStream_t s = m->ctx->stream;
+    const int D = d.dim;
+    auto bytes = [](int N, int K) { return K % SPLIT_K_MULTIPLE ? 0 : (split_bytes(N, K) + 255) & ~(size_t)255; };
+    const size_t per_layer = bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) + bytes(D, d.ff_dim);
+    const size_t total = per_layer * m->layers.size();
+    if (total == 0) return true;
+    if (!m->weights_s.ensure(total, "hipMalloc(split weights)")) return false;
+    char *cur = static_cast<char *>(m->weights_s.ptr);
+    auto split = [&](const float *src, int N, int K, void **dst) {
+        if (K % SPLIT_K_MULTIPLE) return true;  // the fp32 MFMA GEMM serves this matrix
+        *dst = cur;
+        cur += bytes(N, K);
+        return split_weights(s, src, N, K, K, *dst, split_pitch(K));
+    };
+    for (LayerWeights &w : m->layers) {
+        if (!split(w.wqkvg, d.qkvg_dim(), D, &w.wqkvg_s) || !split(w.wout, D, d.inner(), &w.wout_s) ||
+            !split(w.w1, d.ff1_out(), D, &w.w1_s) || !split(w.w2, D, d.ff_dim, &w.w2_s))
+            return false;
+    }
+    return check(hipStreamSynchronize(s), "hipStreamSynchronize(split weights)");
+}
+
 // Batched token-wise linears of one pipeline stage in the model's precision
 // (fp32 activations; the bf16 variant rounds them as they are staged).
 bool stage_gemms(vh_model *m, const std::vector<GemmArgs> &gs, const std::vector<void *> &wh, int epi,
@@ -594,7 +638,7 @@ extern "C" vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const v
         delete m;
         return nullptr;
     }
-    if (!upload_pack(m, pack, bytes)) {
+    if (!upload_pack(m, pack, bytes) || !prepare_split(m)) {
         delete m;
         return nullptr;
     }
@@ -602,12 +646,14 @@ extern "C" vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const v
 }
 
 extern "C" int vh_model_set_precision(vh_model *m, int precision) {
-    if (!m || (precision != VH_PRECISION_FP32 && precision != VH_PRECISION_BF16)) {
+    if (!m || (precision != VH_PRECISION_FP32 && precision != VH_PRECISION_BF16 &&
+               precision != VH_PRECISION_FP32_MFMA)) {
         set_error("vh_model_set_precision: unknown precision %d", precision);
         return 0;
     }
     if (precision == VH_PRECISION_BF16 && !prepare_bf16(m)) return 0;
-    m->precision = precision == VH_PRECISION_BF16 ? PREC_BF16 : PREC_FP32;
+    m->precision = precision == VH_PRECISION_BF16 ? PREC_BF16 : precision == VH_PRECISION_FP32_MFMA ? PREC_FP32_MFMA
+                                                                                                     : PREC_FP32;
     return 1;
 }
 

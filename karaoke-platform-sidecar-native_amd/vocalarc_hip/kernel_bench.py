@@ -44,7 +44,7 @@ def _event_time(fn, reps: int) -> float:
 
 
 def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | None = None, shape: str = "",
-          peak_tflops: float = FP32_TFLOPS) -> dict:
+          peak_tflops: float = FP32_TFLOPS, extra: dict | None = None) -> dict:
     rec = {"kernel": name, "shape": shape, "ms": round(ms, 4)}
     if gbytes is not None:
         gbs = gbytes / (ms * 1e-3)
@@ -54,6 +54,8 @@ def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | N
         tf = gflop / (ms * 1e-3) / 1e3
         rec.update({"algorithmic_GFLOP": round(gflop, 2), "TFLOP_per_s": round(tf, 2),
                     "bound": "mfma", "frac_of_peak": round(tf / peak_tflops, 4)})
+    if extra:
+        rec.update(extra)
     print(json.dumps(rec), flush=True)
     return rec
 
@@ -61,9 +63,9 @@ def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | N
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,attn,bf16")
+    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,split,attn,bf16")
     args = ap.parse_args()
-    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "attn", "bf16"}
+    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "split", "attn", "bf16"}
 
     import torch
 
@@ -129,6 +131,28 @@ def main() -> int:
             _emit(name, _event_time(lambda: ctx.gemm(a, w, c, M, N, K, bias=b, epilogue=epi), max(3, reps // 4)),
                   gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}")
             del a, w, b, c
+
+    if "split" in groups:
+        # the same four GEMMs in fp32 accuracy on the bf16 matrix cores (three
+        # bf16 pieces per fp32 operand, six piece products): algorithmic fp32
+        # FLOPs against the fp32 MFMA peak, and the matrix-core work (6x)
+        # against the bf16 peak
+        M = 8 * 801 * 62
+        for name, K, N, epi, ocols in (("gemm_split_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
+                                       ("gemm_split_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
+                                       ("gemm_split_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
+                                       ("gemm_split_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384)):
+            a = torch.randn(M, K, device=dev, generator=g)
+            w = 0.05 * torch.randn(N, K, device=dev, generator=g)
+            ws = torch.empty(3, N, K, dtype=torch.bfloat16, device=dev)
+            ctx.split_weights(w, ws, N, K, K)
+            b = torch.randn(N, device=dev, generator=g)
+            c = torch.zeros(M, ocols, device=dev)
+            ms = _event_time(lambda: ctx.gemm_split(a, ws, c, M, N, K, K, bias=b, epilogue=epi), max(3, reps // 4))
+            gflop = 2.0 * M * K * N / 1e9
+            _emit(name, ms, gflop=gflop, shape=f"M={M} K={K} N={N}",
+                  extra={"bf16_matrix_core_frac": round(6 * gflop / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
+            del a, w, ws, b, c
 
     if "bf16" in groups:
         # the same four GEMMs on bf16 matrix-core operands, with the operand

@@ -19,6 +19,10 @@ from pathlib import Path
 # kernel-name patterns (demangled or mangled) -> what the launch computes in
 # the separation pass
 ROLES = [
+    (r"gemm_split_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via split bf16)"),
+    (r"gemm_split_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via split bf16)"),
+    (r"gemm_split_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via split bf16)"),
+    (r"split_weight_kernel", "weight split into bf16 pieces (model load)"),
     (r"gemm_f32_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32)"),
     (r"gemm_f32_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32)"),
     (r"gemm_f32_kernel(<|ILi)0", "fused QKV + gate projection (fp32)"),

@@ -102,14 +102,16 @@ def _gfx950_disassembly(tmp_path: Path) -> dict[str, list[str]]:
 
 
 def test_lds_dma_owns_m0(tmp_path):
-    """The pipelined bf16 GEMM sets m0 (the LDS base of a global->LDS load)
-    from inline assembly, unseen by the compiler: every m0 write in those
-    kernels must directly feed its load, and nothing else may use m0 there."""
+    """The pipelined GEMMs (bf16 and split) set m0 (the LDS base of a
+    global->LDS load) from inline assembly, unseen by the compiler: in every
+    kernel that loads straight into LDS, each m0 write must directly feed its
+    load, and nothing else may use m0."""
     if not native.LIB_PATH.exists():
         pytest.skip("library not built")
     funcs = _gfx950_disassembly(tmp_path)
-    dma = [f for f in funcs if "gemm_bf16_dma" in f]
-    assert len(dma) >= 2, "pipelined bf16 GEMM kernels missing from the library"
+    dma = [f for f in funcs if any(x.startswith("global_load_lds") for x in funcs[f])]
+    assert any("gemm_bf16_dma" in f for f in dma), "pipelined bf16 GEMM kernels missing from the library"
+    assert any("gemm_split" in f for f in dma), "split GEMM kernels missing from the library"
     for f in dma:
         ins = funcs[f]
         loads = [i for i, x in enumerate(ins) if x.startswith("global_load_lds")]
