@@ -108,7 +108,7 @@ def measured_traffic() -> tuple[int | None, str | None]:
     """HBM bytes per launch of the dominant kernel, from the committed
     calibrated rocprofv3 counter summary (FETCH_SIZE/WRITE_SIZE scaled by a
     plain copy); None if that summary is absent."""
-    path = ROOT / "profiles" / "gemm-ff1-geglu_traffic.md"
+    path = ROOT / "profiles" / "gemm-split-ff1-geglu_traffic.md"
     if not path.exists():
         return None, None
     for line in path.read_text().splitlines():
@@ -279,7 +279,7 @@ def main() -> int:
                 "algorithmic 2*M*K*N fp32 FLOPs, so frac can exceed 1 against the fp32 MFMA instruction peak",
         "bf16_matrix_core_frac": round(6 * achieved / MFMA_BF16_PEAK_TFLOPS, 4),
         "traffic": traffic,
-        "traffic_unit": "bytes per full 8-window launch (beyond L2; algorithmic 3.056e9)",
+        "traffic_unit": "bytes per full 8-window launch (beyond L2; algorithmic 3.058e9)",
         "traffic_source": traffic_src,
         "launches": launches,
         "avg_launch_ms": round(ms / max(launches, 1), 4),

@@ -45,11 +45,16 @@ VH_DEVICE void store_out(T *p, float v) {
 
 // Fused epilogue of a wave's FM x FN accumulators whose tile starts at
 // (row0, col0).  Accumulator layout as for the fp32 32x32 MFMA: lane (li,
-// lh), register r holds row 8*(r/4) + 4*lh + r%4, column li.
+// lh), register r holds row 8*(r/4) + 4*lh + r%4, column li.  Tiles whose
+// rows all lie inside M (all but the last row of tiles) take a path without
+// per-element row checks, so the residual epilogue issues its 16 loads of C
+// together instead of one load-wait-store per element.
 template <int EPI, typename TC, int FM, int FN>
 VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[FM][FN], int row0, int col0, int li,
                                   int lh) {
     TC *C = static_cast<TC *>(d.C);
+    const bool rows_full = row0 + 32 * FM <= d.M;
+    auto row_of = [&](int i, int r) { return row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3); };
     if constexpr (EPI == EPI_GEGLU) {
         // accumulator pair (2p, 2p+1) = value and gate columns of one 64-wide group
 #pragma unroll
@@ -64,8 +69,8 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int row = row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (row < d.M)
+                    const int row = row_of(i, r);
+                    if (rows_full || row < d.M)
                         store_out(C + (size_t)row * d.ldc + oc,
                                   (acc[i][2 * p][r] + bv) * gelu_dev(acc[i][2 * p + 1][r] + bg));
                 }
@@ -78,18 +83,35 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
             if (col >= d.N) continue;
             const float bc = d.bias ? d.bias[col] : 0.0f;
 #pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    if (row >= d.M) continue;
+            for (int i = 0; i < FM; i++) {
+                auto value = [&](int r) {
                     const float v = acc[i][j][r] + bc;
-                    TC *p = C + (size_t)row * d.ldc + col;
-                    if constexpr (EPI == EPI_STORE) store_out(p, v);
-                    else if constexpr (EPI == EPI_GELU) store_out(p, gelu_dev(v));
-                    else if constexpr (EPI == EPI_TANH) store_out(p, tanhf(v));
-                    else if constexpr (EPI == EPI_RESIDUAL) *p = *p + v;
+                    if constexpr (EPI == EPI_GELU) return gelu_dev(v);
+                    else if constexpr (EPI == EPI_TANH) return tanhf(v);
+                    else return v;
+                };
+                if (rows_full) {
+                    if constexpr (EPI == EPI_RESIDUAL) {
+                        float old[16];
+#pragma unroll
+                        for (int r = 0; r < 16; r++) old[r] = C[(size_t)row_of(i, r) * d.ldc + col];
+#pragma unroll
+                        for (int r = 0; r < 16; r++) C[(size_t)row_of(i, r) * d.ldc + col] = old[r] + value(r);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) store_out(C + (size_t)row_of(i, r) * d.ldc + col, value(r));
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = row_of(i, r);
+                        if (row >= d.M) continue;
+                        TC *p = C + (size_t)row * d.ldc + col;
+                        if constexpr (EPI == EPI_RESIDUAL) *p = *p + value(r);
+                        else store_out(p, value(r));
+                    }
                 }
+            }
         }
     }
 }

@@ -58,16 +58,33 @@ VH_DEVICE void split3(float x, bf16 &h, bf16 &m, bf16 &l) {
     l = (bf16)(r1 - (float)m);
 }
 
-// Eight fp32 values (two float4) -> their h, m, l bf16 pieces.
+// Two fp32 -> two bf16 (nearest even) in one dword: one v_cvt_pk_bf16_f32.
+VH_DEVICE uint32_t pack_bf16x2(float a, float b) {
+    typedef float floatx2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, bf16x2));
+}
+
+// Eight fp32 values (two float4) -> their h, m, l bf16 pieces.  Each piece
+// pair is converted once, packed as the MFMA operand wants it, and read back
+// as fp32 from the packed dword (low half << 16, high half masked): 5.5 VALU
+// instructions per value.
 VH_DEVICE void split8(floatx4 lo, floatx4 hi, bf16x8 &h, bf16x8 &m, bf16x8 &l) {
+    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    uint32_t ph[4], pm[4], pl[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        bf16 a, b, c;
-        split3(lo[e], a, b, c);
-        h[e] = a; m[e] = b; l[e] = c;
-        split3(hi[e], a, b, c);
-        h[4 + e] = a; m[4 + e] = b; l[4 + e] = c;
+        const float a = x[2 * e], b = x[2 * e + 1];
+        ph[e] = pack_bf16x2(a, b);
+        const float ra = a - __uint_as_float(ph[e] << 16), rb = b - __uint_as_float(ph[e] & 0xffff0000u);
+        pm[e] = pack_bf16x2(ra, rb);
+        const float sa = ra - __uint_as_float(pm[e] << 16), sb = rb - __uint_as_float(pm[e] & 0xffff0000u);
+        pl[e] = pack_bf16x2(sa, sb);
     }
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    h = __builtin_bit_cast(bf16x8, (u32x4){ph[0], ph[1], ph[2], ph[3]});
+    m = __builtin_bit_cast(bf16x8, (u32x4){pm[0], pm[1], pm[2], pm[3]});
+    l = __builtin_bit_cast(bf16x8, (u32x4){pl[0], pl[1], pl[2], pl[3]});
 }
 
 template <int EPI>

@@ -114,15 +114,14 @@ def main() -> int:
               gbytes=3 * rows * dim * 4 / 1e9, shape="[49662,384]")
         del x, y, r
 
-    if "gemm" in groups or "ff1" in groups:
+    if "gemm" in groups:
         # the transformer GEMMs of one 8-window pass (M = 8 * 801 * 62 tokens)
+        # on the fp32 MFMA instruction
         M = 8 * 801 * 62
         shapes = (("gemm_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
                   ("gemm_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
                   ("gemm_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
                   ("gemm_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384))
-        if "gemm" not in groups:
-            shapes = shapes[2:3]
         for name, K, N, epi, ocols in shapes:
             a = torch.randn(M, K, device=dev, generator=g)
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
@@ -132,16 +131,19 @@ def main() -> int:
                   gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}")
             del a, w, b, c
 
-    if "split" in groups:
+    if "split" in groups or "ff1" in groups:
         # the same four GEMMs in fp32 accuracy on the bf16 matrix cores (three
         # bf16 pieces per fp32 operand, six piece products): algorithmic fp32
         # FLOPs against the fp32 MFMA peak, and the matrix-core work (6x)
         # against the bf16 peak
         M = 8 * 801 * 62
-        for name, K, N, epi, ocols in (("gemm_split_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
-                                       ("gemm_split_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
-                                       ("gemm_split_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
-                                       ("gemm_split_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384)):
+        shapes = (("gemm_split_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
+                  ("gemm_split_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
+                  ("gemm_split_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
+                  ("gemm_split_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384))
+        if "split" not in groups:
+            shapes = shapes[2:3]  # the dominant kernel alone (counter runs)
+        for name, K, N, epi, ocols in shapes:
             a = torch.randn(M, K, device=dev, generator=g)
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
             ws = torch.empty(3, N, K, dtype=torch.bfloat16, device=dev)

@@ -65,10 +65,10 @@ def main() -> int:
         if line.startswith("{"):
             bench = json.loads(line)
     lines = [
-        "# Kernel time of the 5-minute separation (fp32 timed region, then the bf16 variant)",
+        "# Kernel time of the 5-minute separation (bench.py, command below)",
         "", "Command (repository root, MI355X box):", "", "```", command.strip(), "```", "",
-        f"Source: `{path.name}` written by rocprofv3 (durations in ms). The run covers the warm-up, the timed steps and "
-        "the bf16 variant's warm-up and timed steps of bench.py.", "",
+        f"Source: `{path.name}` written by rocprofv3 (durations in ms). The run covers model load, the warm-up and "
+        "the timed steps of bench.py (and those of the precision variants when the command runs them).", "",
         "| kernel | role | calls | total ms | avg ms | % |", "|---|---|---:|---:|---:|---:|",
     ]
     for r in rows:
