@@ -137,6 +137,27 @@ def test_geglu(ctx, rng, rows, width):
     assert_close(ref, from_dev(dy), rtol=2e-6, atol=2e-6, what="geglu")
 
 
+def test_gelu_accuracy_sweep(ctx):
+    """The device GELU (polynomial-in-t erf form) against float64 over a dense
+    sweep of [-10, 10]: within 1.5e-7 * max(|x|, 1), what a GELU built on a
+    correctly rounded fp32 erf achieves (1.04e-7 over the same sweep)."""
+    from scipy.special import erf
+    g = np.linspace(-10.0, 10.0, 1 << 20).astype(np.float32)
+    g[:4] = [0.0, -0.0, 1e-30, -1e-30]
+    x = np.empty((1, 2 * g.size), np.float32)
+    x[0, :g.size] = 1.0  # value half: GELU-GLU then returns GELU(gate)
+    x[0, g.size:] = g
+    dy = empty_dev((1, g.size))
+    ctx.geglu(to_dev(x), dy, 1, g.size)
+    out = from_dev(dy)[0].astype(np.float64)
+    gd = g.astype(np.float64)
+    ref = 0.5 * gd * (1.0 + erf(gd / np.sqrt(2.0)))
+    err = np.abs(out - ref) / np.maximum(np.abs(gd), 1.0)
+    print(f"GELU sweep: max |d| / max(|x|, 1) = {err.max():.3e}")
+    assert err.max() <= 1.5e-7
+    assert np.all(out[gd < -9.5] <= 0) and np.all(np.abs(out[gd > 9.5] - gd[gd > 9.5]) <= 2e-6)
+
+
 def test_residual_add(ctx, rng):
     n = 49662 * 384
     x = rng.standard_normal(n, dtype=np.float32)
