@@ -101,9 +101,13 @@ int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *
    native/vocalarc_separation.c:692-793.  out[S*L][H*64].  flags:
    VH_ATT_OUT_BF16 writes out as bf16 (round to nearest even); VH_ATT_BF16
    takes qkv as bf16 and runs the bf16-MFMA kernel (q, k, v and the
-   probabilities as bf16 operands, fp32 softmax statistics). */
+   probabilities as bf16 operands, fp32 softmax statistics); VH_ATT_SPLIT
+   (fp32 qkv, length > 64) runs the products in fp32 accuracy as exact
+   three-piece bf16 splits on the bf16 matrix cores (the default fp32 path's
+   time-axis attention). */
 #define VH_ATT_OUT_BF16 1
 #define VH_ATT_BF16 2
+#define VH_ATT_SPLIT 4
 int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                  int apply_rotary, int flags);
 

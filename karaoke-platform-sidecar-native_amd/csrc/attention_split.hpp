@@ -1,0 +1,194 @@
+// Fused axial attention in fp32 accuracy on bf16 matrix cores: the time-axis
+// attention of the default fp32 path.  Same task decomposition, layout,
+// rotary, online softmax and gate as attention_kernel (attention.hpp); the
+// two products run as exact three-piece bf16 splits (gemm_split.hpp):
+//   S^T = K * Q^T: q (rotated, scaled to the log2 domain) is split once per
+//     task in registers; k (rotated) and v are split as they are staged, so
+//     LDS holds their h, m, l pieces as three planes.  Per 32-key block and
+//     16 head dims: six v_mfma_f32_32x32x16_bf16 (kl.qh, kh.ql, km.qm,
+//     km.qh, kh.qm, kh.qh), small products first.
+//   O^T += V^T * P^T: the lane's fp32 probabilities of keys
+//     {16st + 4lh + 0..3, 16st + 8 + 4lh + 0..3} (registers 8st..8st+7, the
+//     bf16 kernel's key order) are split in registers; V^T pieces are read in
+//     the same key order; six products per 16 keys and 32 dims.
+// The probabilities, statistics, normalisation and gate are fp32 as in the
+// fp32 kernel; the dropped piece products are below 2^-23 of each term.
+#pragma once
+
+#include "attention.hpp"
+#include "attention_bf16.hpp"
+#include "gemm_split.hpp"
+
+namespace vh {
+
+template <int WAVES, typename TO>
+__global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs a) {
+    constexpr int NT = 64 * WAVES;
+    constexpr int CHUNKS = ATT_KB * ATT_DH / 8;  // 8-element chunks per K (or V) tile: 256
+    constexpr int PER_T = CHUNKS / NT;
+    static_assert(CHUNKS % NT == 0, "tile must divide evenly");
+    __shared__ __attribute__((aligned(16))) bf16 Ks[2][3][ATT_KB][ATB_KPITCH];
+    __shared__ __attribute__((aligned(16))) bf16 Vt[2][3][ATT_DH][ATB_VPITCH];
+
+    const float *qkv = static_cast<const float *>(a.qkv);
+    const int qgroups = (a.L + 32 * WAVES - 1) / (32 * WAVES);
+    const int task = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);  // neighbouring tasks share K/V rows: same XCD
+    const int qg = task % qgroups;
+    const int sh = task / qgroups;
+    const int h = sh % a.H;
+    const int s = sh / a.H;
+
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int q0 = (qg * WAVES + wave) * 32;
+    const bool wave_active = q0 < a.L;
+
+    const int kcol = a.inner + h * ATT_DH;
+    const int vcol = 2 * a.inner + h * ATT_DH;
+
+    // Q of query q0+li, dims 16g + 8lh .. +7, rotated, scaled (log2 domain), split.
+    bf16x8 qh[4], qm[4], ql[4];
+    float gate_logit = 0.0f;  // loaded with Q so the store does not wait on it
+    {
+        const int q = min(q0 + li, a.L - 1);
+        const float *qp = qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+        if (a.gate_col >= 0) gate_logit = qkv[(size_t)attn_row(a, s, q) * a.ld + a.gate_col + h];
+        const float qs = a.scale * 1.4426950408889634f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int d0 = 16 * g + 8 * lh;
+            const floatx4 lo = rope4(ld4(qp + d0), a.rope, q, d0) * qs;
+            const floatx4 hi = rope4(ld4(qp + d0 + 4), a.rope, q, d0 + 4) * qs;
+            split8(lo, hi, qh[g], qm[g], ql[g]);
+        }
+    }
+
+    // Staging: chunk c of the K tile is key c/8, dims 8*(c%8); chunk c of the
+    // V tile is key c%32, dims 8*(c/32) (the bf16 kernel's maps).
+    floatx4 kreg[PER_T][2], vreg[PER_T][2];
+    auto load = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) {
+            const int c = tid + NT * i;
+            const int kk = c >> 3, kd = 8 * (c & 7);
+            const int vk = c & 31, vd = 8 * (c >> 5);
+            const int pk = kb * ATT_KB + kk, pv = kb * ATT_KB + vk;
+            if (pk < a.L) {
+                const float *kp = qkv + (size_t)attn_row(a, s, pk) * a.ld + kcol + kd;
+                kreg[i][0] = rope4(ld4(kp), a.rope, pk, kd);
+                kreg[i][1] = rope4(ld4(kp + 4), a.rope, pk, kd + 4);
+            } else {
+                kreg[i][0] = kreg[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+            if (pv < a.L) {
+                const float *vp = qkv + (size_t)attn_row(a, s, pv) * a.ld + vcol + vd;
+                vreg[i][0] = ld4(vp);
+                vreg[i][1] = ld4(vp + 4);
+            } else {
+                vreg[i][0] = vreg[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) {
+            const int c = tid + NT * i;
+            bf16x8 p[3];
+            split8(kreg[i][0], kreg[i][1], p[0], p[1], p[2]);
+#pragma unroll
+            for (int k = 0; k < 3; k++) *reinterpret_cast<bf16x8 *>(&Ks[buf][k][c >> 3][8 * (c & 7)]) = p[k];
+            split8(vreg[i][0], vreg[i][1], p[0], p[1], p[2]);
+            const int vk = c & 31, vd = 8 * (c >> 5);
+#pragma unroll
+            for (int k = 0; k < 3; k++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) Vt[buf][k][vd + e][vk] = p[k][e];
+        }
+    };
+
+    floatx16 o[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[t][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int nkb = (a.L + ATT_KB - 1) / ATT_KB;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb++) {
+        const int buf = kb & 1;
+        if (kb + 1 < nkb) load(kb + 1);
+        if (wave_active) {
+            floatx16 sc;
+#pragma unroll
+            for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&Ks[buf][0][li][16 * g + 8 * lh]);
+                const bf16x8 km = *reinterpret_cast<const bf16x8 *>(&Ks[buf][1][li][16 * g + 8 * lh]);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&Ks[buf][2][li][16 * g + 8 * lh]);
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[g], sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[g], sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, qm[g], sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, qh[g], sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qm[g], sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[g], sc, 0, 0, 0);
+            }
+            const int valid = a.L - kb * ATT_KB;
+            if (valid < ATT_KB) {
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
+            }
+            online_softmax_block(sc, m_run, l_run, o);
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                bf16x8 ph, pm, pl;
+                split8(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
+                       floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, ph, pm, pl);
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    bf16x8 v[3];
+#pragma unroll
+                    for (int k = 0; k < 3; k++) {
+                        const bf16 *vr = &Vt[buf][k][32 * t + li][16 * st + 4 * lh];
+                        const bf16x4 v0 = *reinterpret_cast<const bf16x4 *>(vr);
+                        const bf16x4 v1 = *reinterpret_cast<const bf16x4 *>(vr + 8);
+                        v[k] = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    }
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[2], ph, o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pl, o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], pm, o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], ph, o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pm, o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], ph, o[t], 0, 0, 0);
+                }
+            }
+        }
+        if (kb + 1 < nkb) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (!wave_active) return;
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const int q = q0 + li;
+    if (q >= a.L) return;
+    const float inv = 1.0f / l_tot;
+    const int row = attn_row(a, s, q);
+    const float gate = a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f;
+    TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            floatx4 v;
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = (o[t][4 * rq + r] * inv) * gate;
+            st4(op + 32 * t + 8 * rq + 4 * lh, v);
+        }
+}
+
+}  // namespace vh

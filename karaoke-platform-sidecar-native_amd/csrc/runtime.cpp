@@ -11,6 +11,7 @@
 
 #include "attention.hpp"
 #include "attention_bf16.hpp"
+#include "attention_split.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
 #include "gemm_bf16.hpp"
@@ -466,8 +467,16 @@ bool transpose_rows(hipStream_t s, const float *src, float *dst, int outer, int 
 }
 
 template <int WAVES>
-static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bool out_bf16, bool qkv_bf16) {
+static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bool out_bf16, bool qkv_bf16,
+                             bool split) {
     const dim3 block(64 * WAVES);
+    if constexpr (WAVES == 4) {
+        if (split) {
+            if (out_bf16) hipLaunchKernelGGL((attention_split_kernel<WAVES, bf16>), dim3(grid), block, 0, s, a);
+            else hipLaunchKernelGGL((attention_split_kernel<WAVES, float>), dim3(grid), block, 0, s, a);
+            return;
+        }
+    }
     if (qkv_bf16) {
         if (out_bf16) hipLaunchKernelGGL((attention_bf16_kernel<WAVES, bf16>), dim3(grid), block, 0, s, a);
         else hipLaunchKernelGGL((attention_bf16_kernel<WAVES, float>), dim3(grid), block, 0, s, a);
@@ -478,7 +487,7 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
 }
 
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
-               int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16) {
+               int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split) {
     if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
@@ -498,8 +507,10 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
         if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((attention_short_kernel<float>), dim3(grid), dim3(256), 0, s, a);
     } else if (lay.L <= 64)
-        launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16);
-    else launch_attention<4>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 127) / 128)), out_bf16, qkv_bf16);
+        launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16,
+                            split && !qkv_bf16);
+    else launch_attention<4>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 127) / 128)), out_bf16, qkv_bf16,
+                             split && !qkv_bf16);
     return sync_debug(s, "attention_kernel");
 }
 
@@ -627,8 +638,10 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     // pre-norm -> fused QKV (+gate logits with their bias)
     if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
     if (!lin(normed, D, w.wqkvg, w.wqkvg_s, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
-    // rotary + attention + gates
-    if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t)) return false;
+    // rotary + attention + gates (long sequences: products as split bf16 on
+    // the default fp32 path)
+    if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32))
+        return false;
     // out projection added to the residual stream
     if (!lin(attn, inner, w.wout, w.wout_s, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;
     // FFN

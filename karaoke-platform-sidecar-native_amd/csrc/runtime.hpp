@@ -150,9 +150,12 @@ struct AttnLayout {
     int group, group_stride, seq_stride, pos_stride;
 };
 // qkv fp32 (fp32 MFMA) or, with qkv_bf16, bf16 (bf16 MFMA); out fp32, or bf16
-// when out_bf16.  rope: interleaved rotary table of length lay.L (or null).
+// when out_bf16.  split (fp32 qkv, L > 64): the products in fp32 accuracy as
+// exact three-piece bf16 splits on the bf16 matrix cores.  rope: interleaved
+// rotary table of length lay.L (or null).
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
-               int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false);
+               int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false,
+               bool split = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {

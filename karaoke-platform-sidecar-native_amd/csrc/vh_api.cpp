@@ -172,12 +172,13 @@ extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *
 
 extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                             int apply_rotary, int flags) {
-    if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16))) return 0;
+    if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16 | VH_ATT_SPLIT))) return 0;
     const float *rt = nullptr;
     if (apply_rotary && !ctx->rope.get_interleaved(length, 64, ctx->stream, &rt)) return 0;
     const int inner = heads * 64;
     return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
-                     &ctx->timer, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0)
+                     &ctx->timer, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0,
+                     (flags & VH_ATT_SPLIT) != 0)
                ? 1
                : 0;
 }

@@ -182,6 +182,12 @@ def main() -> int:
             o = torch.empty(S * L, 512, device=dev)
             _emit("attention", _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True), max(3, reps // 4)),
                   gflop=4.0 * S * 8 * L * L * 64 / 1e9, shape=f"S={S} L={L} H=8")
+            if L > 64:
+                # the default fp32 path's time-axis attention: split bf16 products
+                gf = 4.0 * S * 8 * L * L * 64 / 1e9
+                ms = _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True, split=True), max(3, reps // 4))
+                _emit("attention_split", ms, gflop=gf, shape=f"S={S} L={L} H=8",
+                      extra={"bf16_matrix_core_frac": round(6 * gf / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
             del qkv, o
 
     if "c2" in groups or "c3" in groups:

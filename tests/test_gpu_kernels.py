@@ -193,3 +193,34 @@ def test_attention_core(ctx, rng, S, L):
     out = from_dev(dout)
     assert_close(ref, out, rtol=2e-5, atol=2e-5, what=f"attention S={S} L={L}")
     assert snr_db(ref, out) > 100
+
+
+@pytest.mark.parametrize("S,L", [(2, 801), (1, 65), (2, 130), (3, 97), (1, 1000)])
+def test_attention_split(ctx, rng, S, L):
+    """Time-axis attention with both products as exact three-piece bf16
+    splits: the fp32 bar against the oracle, and an error against a float64
+    statement no larger than the fp32 MFMA kernel's on the same inputs."""
+    H = 8
+    qkv = rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32)
+    rot = _rotate_qk(qkv, L, H)
+    ref = O.attention(REFERENCE_DIMS, rot, S, L)
+    # float64 attention of the same rotated fp32 inputs
+    q = rot[:, :H * 64].reshape(S, L, H, 64).astype(np.float64)
+    k = rot[:, H * 64:2 * H * 64].reshape(S, L, H, 64).astype(np.float64)
+    v = rot[:, 2 * H * 64:].reshape(S, L, H, 64).astype(np.float64)
+    sc = np.einsum("slhd,smhd->shlm", q, k) * 0.125
+    p = np.exp(sc - sc.max(axis=-1, keepdims=True))
+    ref64 = np.einsum("shlm,smhd->slhd", p / p.sum(axis=-1, keepdims=True), v).reshape(S * L, H * 64)
+    outs = {}
+    for split in (True, False):
+        dout = empty_dev((S * L, H * 64))
+        ctx.attention(to_dev(qkv), dout, S, L, H, rotary=True, split=split)
+        outs[split] = from_dev(dout).astype(np.float64)
+    assert_close(ref, outs[True].astype(np.float32), rtol=2e-5, atol=2e-5, what=f"split attention S={S} L={L}")
+    e_split, e_fp32 = np.abs(outs[True] - ref64), np.abs(outs[False] - ref64)
+    print(f"attention S={S} L={L}: split max|d| {e_split.max():.3e} rms {np.sqrt(np.mean(e_split ** 2)):.3e} | "
+          f"fp32 MFMA max|d| {e_fp32.max():.3e} rms {np.sqrt(np.mean(e_fp32 ** 2)):.3e}")
+    # the rms pins the error level; the single worst element of ~10^6 is a
+    # noisier statistic and gets a looser factor
+    assert np.sqrt(np.mean(e_split ** 2)) <= 1.25 * np.sqrt(np.mean(e_fp32 ** 2)) + 1e-9
+    assert e_split.max() <= 2.0 * e_fp32.max() + 1e-8
