@@ -85,16 +85,20 @@ int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int ld
 /* vh_gemm in fp32 accuracy on bf16 matrix cores: every fp32 value is the
    exact sum of three bf16 pieces (h = bf16(x), m = bf16(x - h),
    l = x - h - m) and the six piece products that reach 2^-24 of a product
-   are accumulated in fp32.  Ws: the weight's pieces from vh_split_weights,
-   three planes [3][N][ldw] (plane stride N * ldw, ldw a multiple of 8 and
-   >= K).  K a multiple of 16, lda a multiple of 4, A and Ws 16-byte aligned.
-   The token-wise linear of native/vocalarc_separation.c:631-636, as vh_gemm. */
-int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws, int ldw,
+   are accumulated in fp32.  Ws: the weight's pieces from vh_split_weights.
+   K a multiple of 16, lda a multiple of 4, A and Ws 16-byte aligned.  The
+   token-wise linear of native/vocalarc_separation.c:631-636, as vh_gemm. */
+int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws,
                   const float *bias, float *C, int ldc, int epilogue);
-/* fp32 W[N][ldw_in] -> the three bf16 planes of vh_gemm_split, [3][N][ld]:
-   plane p holds piece p (h, m, l) of W[n][k] at n * ld + slot(k), where
-   within every group of 16 k the slots are k 0-3, 8-11, 4-7, 12-15. */
-int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Ws, int ld);
+/* Bytes of the pieces of an N x K weight (N rounded up to 128 rows). */
+size_t vh_split_bytes(int N, int K);
+/* fp32 W[N][ldw_in] (K a multiple of 16) -> its bf16 pieces for
+   vh_gemm_split, vh_split_bytes(N, K) bytes, tile-major: piece p (h, m, l)
+   of W[n][k] at bf16 index
+     ((n/128 * K/16 + k/16) * 3 + p) * 2048 + (n%128) * 16 + 8 * (s ^ (n/8)%2) + e
+   where within every group of 16 k the (slot s, element e) order is
+   k 0-3, 8-11 (s = 0), 4-7, 12-15 (s = 1); rows past N are zero. */
+int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Ws);
 /* fp32 src[rows][cols] -> bf16 dst[rows][ld] (round to nearest even). */
 int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld);
 /* Fused attention core over qkv[S*L][3*H*64] (rotary applied here):

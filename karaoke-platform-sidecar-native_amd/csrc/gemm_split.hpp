@@ -15,11 +15,16 @@
 // each, i.e. 2.67x the fp32 MFMA rate (v_mfma_f32_32x32x2f32) per fp32 MAC;
 // measured error against fp64 is at or below the fp32 MFMA GEMM's.
 //
-// Operands.  W is split once, at upload, into three bf16 planes [3][N][ld]
-// with k permuted inside every group of 16 (16-byte slot 0 holds k 0-3 and
-// 8-11, slot 1 holds k 4-7 and 12-15) so a lane's eight k-values for the
-// MFMA are one 16-byte read.  A stays fp32 in memory (no producer changes);
-// each wave splits the A values it reads from LDS in registers.
+// Operands.  W is split once, at upload, into its three bf16 pieces, stored
+// tile-major: for every 128-row tile of W and every 16-wide K chunk, one
+// 12 KB block that is exactly the LDS image of that chunk's W part --
+// [piece][128 rows][2 slots][8], k permuted inside every group of 16
+// (logical slot 0 holds k 0-3 and 8-11, slot 1 holds k 4-7 and 12-15, so a
+// lane's eight k-values for the MFMA are one 16-byte read) and slot s of row
+// r stored at s ^ (r/8)%2 (conflict-free operand reads); rows past N are
+// zero.  Each W load instruction then reads 1 KB contiguous.  A stays fp32
+// in memory (no producer changes); each wave splits the A values it reads
+// from LDS in registers.
 //
 // Pipeline.  256x128 block, 8 waves in a 4x2 grid of 64x64 (2x2 32x32
 // accumulators), K in chunks of 16.  Operands go straight from global memory
@@ -35,15 +40,15 @@ namespace vh {
 
 struct GemmDescSplit {
     const float *A;     // fp32 [M][lda]
-    const bf16 *W;      // three bf16 planes [3][N][ldw], k-permuted
+    const bf16 *W;      // pieces, tile-major (split_weight_kernel)
     const float *bias;  // fp32, may be null
     float *C;           // fp32 [M][ldc]
     int M, N, K;
-    int lda, ldw, ldc;
-    int64_t plane;      // elements between planes (>= N * ldw)
+    int lda, ldc;
 };
 
 constexpr int GS_BM = 256, GS_BN = 128, GS_BK = 16, GS_THREADS = 512;
+constexpr int GS_WBLOCK = 3 * GS_BN * GS_BK;  // bf16 per (row tile, K chunk) block of W pieces
 
 // Index of k inside its W plane row (the 16-group permutation above).
 VH_HOST_DEVICE inline int split_k_slot(int k) {
@@ -114,9 +119,9 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
     auto swz_w = [](int r) { return (r >> 3) & 1; };
 
     // Each load instruction fills 1 KB of the stage.  A: 16 blocks of 16 rows
-    // (lane -> row l/4, slot l%4); wave w loads blocks w and w+8.  W: 12
-    // blocks of 32 rows (plane b/4; lane -> row l/2, slot l%2); wave w loads
-    // block w, and waves 0-3 also block w+8.
+    // (lane -> row l/4, slot l%4); wave w loads blocks w and w+8.  W: the 12
+    // 1 KB blocks of the chunk's tile-major image, lane l the l-th 16 bytes;
+    // wave w loads block w, and waves 0-3 also block w+8.
     const float *a_src[2];
     uint32_t a_off[2];
 #pragma unroll
@@ -131,8 +136,7 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int b = min(wave + 8 * j, 11);
-        const int r = 32 * (b & 3) + (lane >> 1);
-        w_src[j] = d.W + (b >> 2) * d.plane + (size_t)min(n0 + r, d.N - 1) * d.ldw + 8 * ((lane & 1) ^ swz_w(r));
+        w_src[j] = d.W + (size_t)(n0 / GS_BN) * (d.K / GS_BK) * GS_WBLOCK + b * 512 + 8 * lane;
         w_off[j] = A_BYTES + b * 1024;
     }
     const bool two_w = wave < 4;
@@ -141,8 +145,9 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
         const int k0 = kt * GS_BK;
         lds_dma16(a_src[0] + k0, __builtin_amdgcn_readfirstlane(sb + a_off[0]));
         lds_dma16(a_src[1] + k0, __builtin_amdgcn_readfirstlane(sb + a_off[1]));
-        lds_dma16(w_src[0] + k0, __builtin_amdgcn_readfirstlane(sb + w_off[0]));
-        if (two_w) lds_dma16(w_src[1] + k0, __builtin_amdgcn_readfirstlane(sb + w_off[1]));
+        const int wk = kt * GS_WBLOCK;
+        lds_dma16(w_src[0] + wk, __builtin_amdgcn_readfirstlane(sb + w_off[0]));
+        if (two_w) lds_dma16(w_src[1] + wk, __builtin_amdgcn_readfirstlane(sb + w_off[1]));
     };
 
     floatx16 acc[2][2];
@@ -209,19 +214,25 @@ __global__ __launch_bounds__(GS_THREADS, 2) void gemm_split_kernel(GemmDescSplit
     gemm_split_body<EPI>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
-// fp32 W [N][ldw_in] -> its h, m, l planes [3][N][ld] (k permuted as above;
-// columns K..ld-1 of every plane are left untouched).
+// fp32 W [N][ldw_in] (K a multiple of 16) -> its h, m, l pieces, tile-major:
+// element (n, k) of piece p at
+//   ((n/128 * K/16 + k/16) * 3 + p) * 2048 + (n%128) * 16 + 8 * (s ^ (n/8)%2) + e
+// where slot s and element e come from split_k_slot(k) % 16 = 8 s + e.  One
+// thread per (padded row, k); rows past N are written as zero.
 static __global__ __launch_bounds__(256) void split_weight_kernel(const float *__restrict__ W, int N, int K, int ldw_in,
-                                                                 bf16 *__restrict__ planes, int ld, int64_t plane) {
+                                                                 bf16 *__restrict__ tiles) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)N * K) return;
+    const int rows = (N + GS_BN - 1) / GS_BN * GS_BN;
+    if (idx >= (int64_t)rows * K) return;
     const int n = (int)(idx / K), k = (int)(idx % K);
-    bf16 h, m, l;
-    split3(W[(size_t)n * ldw_in + k], h, m, l);
-    const size_t o = (size_t)n * ld + split_k_slot(k);
-    planes[o] = h;
-    planes[plane + o] = m;
-    planes[2 * plane + o] = l;
+    bf16 h = (bf16)0.0f, m = (bf16)0.0f, l = (bf16)0.0f;
+    if (n < N) split3(W[(size_t)n * ldw_in + k], h, m, l);
+    const int r = n % GS_BN, pos = split_k_slot(k) & 15;
+    const int phys = (pos >> 3) ^ ((r >> 3) & 1);
+    const size_t o = ((size_t)(n / GS_BN) * (K / GS_BK) + k / GS_BK) * GS_WBLOCK + (size_t)r * GS_BK + 8 * phys + (pos & 7);
+    tiles[o] = h;
+    tiles[o + GS_BN * GS_BK] = m;
+    tiles[o + 2 * GS_BN * GS_BK] = l;
 }
 
 }  // namespace vh

@@ -151,7 +151,7 @@ struct native_gpu {
             if (e.dev_split) return e.dev_split;
             void *p = nullptr;
             if (!check(hipMalloc(&p, split_bytes(out, in)), "hipMalloc(split weight)")) return nullptr;
-            if (!split_weights(stream, dev, out, in, in, p, split_pitch(in))) {
+            if (!split_weights(stream, dev, out, in, in, p)) {
                 (void)hipFree(p);
                 return nullptr;
             }
@@ -345,8 +345,7 @@ extern "C" int native_gpu_matmul(native_gpu *gpu, int64_t rows, int in, int out,
     hipStream_t s = gpu->stream;
     auto product = [&]() {
         if (Ws)
-            return gemm_split(s, {gpu->io_in.f(), in, Ws, split_pitch(in), (int64_t)out * split_pitch(in), B,
-                                  gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
+            return gemm_split(s, {gpu->io_in.f(), in, Ws, B, gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
         return gemm(s, {gpu->io_in.f(), in, W, in, B, gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
     };
     bool ok = gpu->io_in.ensure(ib, "hipMalloc(matmul input)") && gpu->io_out.ensure(ob, "hipMalloc(matmul output)") &&

@@ -322,8 +322,7 @@ static_assert(GS_BK == SPLIT_K_MULTIPLE, "split GEMM K chunk");
 
 static bool gemm_split_ok(const GemmArgsSplit &g, int epilogue) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2) return false;
-    if (g.K % GS_BK || g.lda % 4 || g.lda < g.K || g.ldw % 8 || g.ldw < g.K) return false;
-    if (g.plane < (int64_t)g.N * g.ldw) return false;
+    if (g.K % GS_BK || g.lda % 4 || g.lda < g.K) return false;
     if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return false;
     return true;
@@ -336,14 +335,13 @@ static void launch_split(hipStream_t s, const GemmDescSplit &d, unsigned tiles) 
 
 bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer *t, const char *name) {
     if (!gemm_split_ok(g, epilogue)) {
-        set_error("gemm_split: unsupported shape M=%lld N=%d K=%d lda=%d ldw=%d", (long long)g.M, g.N, g.K, g.lda,
-                  g.ldw);
+        set_error("gemm_split: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K, g.lda);
         return false;
     }
     GemmDescSplit d;
     d.A = g.A; d.W = static_cast<const bf16 *>(g.W); d.bias = g.bias; d.C = g.C;
     d.M = (int)g.M; d.N = g.N; d.K = g.K;
-    d.lda = g.lda; d.ldw = g.ldw; d.ldc = g.ldc; d.plane = g.plane;
+    d.lda = g.lda; d.ldc = g.ldc;
     const unsigned tiles = (unsigned)(((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
     Scope sc(t, s, name);
     switch (epilogue) {
@@ -357,14 +355,14 @@ bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer
     return sync_debug(s, "gemm_split_kernel");
 }
 
-bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *planes, int ld) {
-    if (N <= 0 || K <= 0 || ldw < K || ld < K || (int64_t)N * ld > INT32_MAX) {
-        set_error("split_weights: bad shape N=%d K=%d ldw=%d ld=%d", N, K, ldw, ld);
+bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces) {
+    if (N <= 0 || K <= 0 || K % GS_BK || ldw < K || split_bytes(N, K) / 6 > (size_t)INT32_MAX) {
+        set_error("split_weights: bad shape N=%d K=%d ldw=%d (K a multiple of 16)", N, K, ldw);
         return false;
     }
-    const int64_t n = (int64_t)N * K;
+    const int64_t n = (int64_t)(N + GS_BN - 1) / GS_BN * GS_BN * K;
     hipLaunchKernelGGL(split_weight_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, W, N, K, ldw,
-                       static_cast<bf16 *>(planes), ld, (int64_t)N * ld);
+                       static_cast<bf16 *>(pieces));
     return sync_debug(s, "split_weight_kernel");
 }
 
@@ -631,8 +629,7 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     auto lin = [&](const float *A, int lda, const float *W, const void *Ws, const float *bias, float *C, int ldc, int N,
                    int K, int epi, const char *name) {
         if (Ws && precision == PREC_FP32 && K % SPLIT_K_MULTIPLE == 0)
-            return gemm_split(s, {A, lda, Ws, split_pitch(K), (int64_t)N * split_pitch(K), bias, C, ldc, tokens, N, K},
-                              epi, t, name);
+            return gemm_split(s, {A, lda, Ws, bias, C, ldc, tokens, N, K}, epi, t, name);
         return gemm(s, {A, lda, W, K, bias, C, ldc, tokens, N, K}, epi, t, name);
     };
     // pre-norm -> fused QKV (+gate logits with their bias)

@@ -106,25 +106,24 @@ bool gemm_bf16(hipStream_t s, const GemmArgsBF16 &g, int epilogue, KernelTimer *
 bool gemm_bf16_batched(hipStream_t s, const std::vector<GemmArgsBF16> &g, int epilogue, KernelTimer *t = nullptr,
                        const char *name = "gemm_bf16_batched");
 // fp32-accurate linear on bf16 matrix cores (gemm_split.hpp): A fp32, W as
-// three bf16 planes [3][N][ldw] from split_weights, C fp32.  K a multiple of
-// 16; lda a multiple of 4 and ldw of 8; A and W 16-byte aligned.
+// its three bf16 pieces in the tile-major layout split_weights writes, C fp32.
+// K a multiple of 16; lda a multiple of 4; A and W 16-byte aligned.
 struct GemmArgsSplit {
     const float *A; int lda;
-    const void *W; int ldw; int64_t plane;
+    const void *W;
     const float *bias;
     float *C; int ldc;
     int64_t M; int N, K;
 };
 bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer *t = nullptr,
                 const char *name = "gemm_split");
-// K granularity of gemm_split; row pitch of split planes for K columns, and
-// the bytes of the three planes.
+// K granularity of gemm_split, and the bytes of W's pieces (N rounded up to
+// a multiple of 128).
 constexpr int SPLIT_K_MULTIPLE = 16;
-inline int split_pitch(int K) { return (K + 15) / 16 * 16; }
-inline size_t split_bytes(int N, int K) { return (size_t)3 * N * split_pitch(K) * 2; }
-// fp32 W [N][ldw] -> three bf16 planes [3][N][ld], plane stride N * ld
-// (h = bf16(w), m = bf16(w - h), l = w - h - m; k permuted within groups of 16).
-bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *planes, int ld);
+inline size_t split_bytes(int N, int K) { return (size_t)(N + 127) / 128 * 128 * K * 6; }
+// fp32 W [N][ldw] -> its h, m, l bf16 pieces (h = bf16(w), m = bf16(w - h),
+// l = w - h - m), tile-major for gemm_split (split_bytes(N, K) bytes).
+bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces);
 
 // fp32 [rows][cols] -> bf16 [rows][ld] (ld >= cols, padding zeroed by the caller)
 bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst, int ld);

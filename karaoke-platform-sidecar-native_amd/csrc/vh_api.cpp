@@ -150,19 +150,21 @@ extern "C" int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void
     return gemm_bf16(ctx->stream, g, epilogue, &ctx->timer, "gemm_bf16") ? 1 : 0;
 }
 
-extern "C" int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws, int ldw,
+extern "C" int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws,
                              const float *bias, float *C, int ldc, int epilogue) {
     if (!ctx) return 0;
-    GemmArgsSplit g{A, lda, Ws, ldw, (int64_t)N * ldw, bias, C, ldc, M, N, K};
+    GemmArgsSplit g{A, lda, Ws, bias, C, ldc, M, N, K};
     return gemm_split(ctx->stream, g, epilogue, &ctx->timer, "gemm_split") ? 1 : 0;
 }
 
-extern "C" int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Ws, int ld) {
-    if (!ctx || !W || !Ws || ld % 8) {
-        set_error("vh_split_weights: bad arguments (ld a multiple of 8)");
+extern "C" size_t vh_split_bytes(int N, int K) { return N > 0 && K > 0 ? split_bytes(N, K) : 0; }
+
+extern "C" int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Ws) {
+    if (!ctx || !W || !Ws) {
+        set_error("vh_split_weights: null argument");
         return 0;
     }
-    return split_weights(ctx->stream, W, N, K, ldw_in, Ws, ld) ? 1 : 0;
+    return split_weights(ctx->stream, W, N, K, ldw_in, Ws) ? 1 : 0;
 }
 
 extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld) {
@@ -415,7 +417,7 @@ bool prepare_split(vh_model *m) {
         if (K % SPLIT_K_MULTIPLE) return true;  // the fp32 MFMA GEMM serves this matrix
         *dst = cur;
         cur += bytes(N, K);
-        return split_weights(s, src, N, K, K, *dst, split_pitch(K));
+        return split_weights(s, src, N, K, K, *dst);
     };
     for (LayerWeights &w : m->layers) {
         if (!split(w.wqkvg, d.qkvg_dim(), D, &w.wqkvg_s) || !split(w.wout, D, d.inner(), &w.wout_s) ||

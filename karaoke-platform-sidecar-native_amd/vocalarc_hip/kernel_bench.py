@@ -146,11 +146,11 @@ def main() -> int:
         for name, K, N, epi, ocols in shapes:
             a = torch.randn(M, K, device=dev, generator=g)
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
-            ws = torch.empty(3, N, K, dtype=torch.bfloat16, device=dev)
-            ctx.split_weights(w, ws, N, K, K)
+            ws = torch.empty(ctx.split_bytes(N, K) // 2, dtype=torch.bfloat16, device=dev)
+            ctx.split_weights(w, ws, N, K)
             b = torch.randn(N, device=dev, generator=g)
             c = torch.zeros(M, ocols, device=dev)
-            ms = _event_time(lambda: ctx.gemm_split(a, ws, c, M, N, K, K, bias=b, epilogue=epi), max(3, reps // 4))
+            ms = _event_time(lambda: ctx.gemm_split(a, ws, c, M, N, K, bias=b, epilogue=epi), max(3, reps // 4))
             gflop = 2.0 * M * K * N / 1e9
             _emit(name, ms, gflop=gflop, shape=f"M={M} K={K} N={N}",
                   extra={"bf16_matrix_core_frac": round(6 * gflop / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})

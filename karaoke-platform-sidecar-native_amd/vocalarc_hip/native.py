@@ -20,7 +20,7 @@ LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
 HARNESS_SYMBOLS = [
     "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
     "vh_rmsnorm", "vh_rmsnorm_bf16", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
-    "vh_gemm_split", "vh_split_weights", "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
+    "vh_gemm_split", "vh_split_bytes", "vh_split_weights", "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
     "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
 ]
 ABI_SYMBOLS = [
@@ -64,8 +64,9 @@ def lib():
         "vh_residual_add": (_I, [_P, _I64, _P, _P]),
         "vh_gemm": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
         "vh_gemm_bf16": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I, _I]),
-        "vh_gemm_split": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
-        "vh_split_weights": (_I, [_P, _I, _I, _P, _I, _P, _I]),
+        "vh_gemm_split": (_I, [_P, _I64, _I, _I, _P, _I, _P, _P, _P, _I, _I]),
+        "vh_split_bytes": (ctypes.c_size_t, [_I, _I]),
+        "vh_split_weights": (_I, [_P, _I, _I, _P, _I, _P]),
         "vh_to_bf16": (_I, [_P, _I64, _I, _P, _P, _I]),
         "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
         "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
@@ -180,14 +181,19 @@ class Context:
                                ptr(bias) if bias is not None else None, ptr(C),
                                ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue, flags), "vh_gemm_bf16")
 
-    def split_weights(self, W, Ws, N: int, K: int, ld: int, ldw_in: int | None = None):
-        """fp32 W [N][ldw_in] -> three bf16 planes Ws [3][N][ld] (see vh_split_weights)."""
-        _ok(lib().vh_split_weights(self.h, N, K, ptr(W), ldw_in or K, ptr(Ws), ld), "vh_split_weights")
+    @staticmethod
+    def split_bytes(N: int, K: int) -> int:
+        """Bytes of the bf16 pieces of an N x K weight (see split_weights)."""
+        return int(lib().vh_split_bytes(N, K))
 
-    def gemm_split(self, A, Ws, C, M: int, N: int, K: int, ldw: int, bias=None, epilogue: int = EPI_STORE,
+    def split_weights(self, W, Ws, N: int, K: int, ldw_in: int | None = None):
+        """fp32 W [N][ldw_in] -> its tile-major bf16 pieces Ws (split_bytes(N, K) bytes)."""
+        _ok(lib().vh_split_weights(self.h, N, K, ptr(W), ldw_in or K, ptr(Ws)), "vh_split_weights")
+
+    def gemm_split(self, A, Ws, C, M: int, N: int, K: int, bias=None, epilogue: int = EPI_STORE,
                    lda: int | None = None, ldc: int | None = None):
         """fp32-accurate linear on bf16 matrix cores; Ws from split_weights."""
-        _ok(lib().vh_gemm_split(self.h, M, N, K, ptr(A), lda or K, ptr(Ws), ldw,
+        _ok(lib().vh_gemm_split(self.h, M, N, K, ptr(A), lda or K, ptr(Ws),
                                 ptr(bias) if bias is not None else None, ptr(C),
                                 ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm_split")
 

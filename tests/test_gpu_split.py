@@ -4,7 +4,8 @@ Every fp32 x is the exact sum of three bf16 pieces h = bf16(x),
 m = bf16(x - h), l = x - h - m.  The split GEMM accumulates the six piece
 products that can reach 2^-24 of |a||w| in fp32.  Pinned here:
   * the pieces: bit-identical to torch's nearest-even bf16 rounding applied
-    in that chain, summing back to W exactly, in the documented slots;
+    in that chain, summing back to W exactly, at the documented tile-major
+    positions (every position written once, rows past N zero);
   * the GEMM: its error against a float64 product of the fp32 operands is no
     larger than the fp32 MFMA GEMM's (max and rms), and below a hard bound of
     2^-18 * sum_k |a_k w_k| that a dropped or misplaced piece product (>= 2^-8
@@ -37,9 +38,16 @@ def ctx():
 
 
 def _slot(k: np.ndarray) -> np.ndarray:
-    """Position of k in a plane row: within each group of 16, k 0-3, 8-11, 4-7, 12-15."""
+    """Position of k in its group of 16: k 0-3, 8-11 (slot 0), 4-7, 12-15 (slot 1)."""
     r = k & 15
     return (k & ~15) + 8 * ((r >> 2) & 1) + (r & 3) + 4 * (r >> 3)
+
+
+def _piece_index(n: np.ndarray, k: np.ndarray, p: int, K: int) -> np.ndarray:
+    """bf16 index of piece p of W[n][k] in the tile-major layout of vh_split_weights."""
+    pos = _slot(k) & 15
+    s, e = pos >> 3, pos & 7
+    return (((n // 128) * (K // 16) + k // 16) * 3 + p) * 2048 + (n % 128) * 16 + 8 * (s ^ ((n // 8) & 1)) + e
 
 
 def _bf16(x: np.ndarray) -> np.ndarray:
@@ -48,10 +56,9 @@ def _bf16(x: np.ndarray) -> np.ndarray:
 
 def _split(ctx, w: np.ndarray):
     n, k = w.shape
-    ld = (k + 15) // 16 * 16
-    planes = torch.zeros(3, n, ld, dtype=torch.bfloat16, device="cuda:0")
-    ctx.split_weights(to_dev(w), planes, n, k, ld)
-    return planes, ld
+    pieces = torch.zeros(ctx.split_bytes(n, k) // 2, dtype=torch.bfloat16, device="cuda:0")
+    ctx.split_weights(to_dev(w), pieces, n, k)
+    return pieces
 
 
 def test_slot_permutation_is_a_bijection():
@@ -62,17 +69,23 @@ def test_slot_permutation_is_a_bijection():
 
 
 def test_split_weights_exact(ctx, rng):
-    n, k, ld = 37, 48, 56
+    n, k = 137, 48  # two row tiles, the second ragged
+    assert ctx.split_bytes(n, k) == 256 * k * 6
     w = rng.standard_normal((n, k)).astype(np.float32) * np.float32(0.05)
     # full 24-bit significands, powers of two, signs, zeros, tiny and large values
     w[0, :8] = [1.0, -0.5, 0.0, -0.0, 3.0e38, -1.0e-30, 1.0 + 2.0 ** -23, -(1.0 - 2.0 ** -24)]
     w[1, :] = (np.arange(k, dtype=np.uint32) * 0x1F3 | 0x3F800000).view(np.float32)
-    planes = torch.full((3, n, ld), 7.0, dtype=torch.bfloat16, device="cuda:0")
-    ctx.split_weights(to_dev(w), planes, n, k, ld)
+    pieces = torch.full((ctx.split_bytes(n, k) // 2,), 7.0, dtype=torch.bfloat16, device="cuda:0")
+    ctx.split_weights(to_dev(w), pieces, n, k)
     torch.cuda.synchronize()
-    p = planes.float().cpu().numpy()
-    assert np.all(p[:, :, k:] == 7.0), "padding columns must be left untouched"
-    h, m, l = (p[i][:, _slot(np.arange(k))] for i in range(3))
+    flat = pieces.float().cpu().numpy()
+    nn, kk = np.meshgrid(np.arange(256), np.arange(k), indexing="ij")
+    idx = [_piece_index(nn, kk, p, k) for p in range(3)]
+    # every element written exactly once, rows past N zero
+    assert sorted(np.concatenate([i.ravel() for i in idx]).tolist()) == list(range(flat.size))
+    for p in range(3):
+        assert np.all(flat[idx[p][n:]] == 0.0)
+    h, m, l = (flat[idx[p][:n]] for p in range(3))
     # the rounding chain, bit for bit
     h_ref = _bf16(w)
     m_ref = _bf16(w - h_ref)
@@ -110,13 +123,13 @@ def test_gemm_split_accuracy(ctx, rng, M, N, K, epi, has_bias):
     w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
     b = rng.standard_normal(N).astype(np.float32) * np.float32(0.1) if has_bias else None
     c0 = rng.standard_normal((M, N)).astype(np.float32)
-    planes, ld = _split(ctx, w)
+    planes = _split(ctx, w)
     db = to_dev(b) if b is not None else None
     outs = {}
     for kind in ("split", "fp32"):
         dc = to_dev(c0)
         if kind == "split":
-            ctx.gemm_split(to_dev(x), planes, dc, M, N, K, ld, bias=db, epilogue=epi)
+            ctx.gemm_split(to_dev(x), planes, dc, M, N, K, bias=db, epilogue=epi)
         else:
             ctx.gemm(to_dev(x), to_dev(w), dc, M, N, K, bias=db, epilogue=epi)
         outs[kind] = from_dev(dc).astype(np.float64)
@@ -152,9 +165,9 @@ def test_gemm_split_geglu(ctx, rng):
     for c in range(F):
         perm[(c // 32) * 64 + (c % 32)] = c
         perm[(c // 32) * 64 + 32 + (c % 32)] = F + c
-    planes, ld = _split(ctx, np.ascontiguousarray(w[perm]))
+    planes = _split(ctx, np.ascontiguousarray(w[perm]))
     dc = empty_dev((M, F))
-    ctx.gemm_split(to_dev(x), planes, dc, M, 2 * F, K, ld, bias=to_dev(np.ascontiguousarray(b[perm])),
+    ctx.gemm_split(to_dev(x), planes, dc, M, 2 * F, K, bias=to_dev(np.ascontiguousarray(b[perm])),
                    epilogue=native.EPI_GEGLU)
     err = np.abs(from_dev(dc) - ref)
     assert err.max() <= 2e-5, err.max()
@@ -162,12 +175,14 @@ def test_gemm_split_geglu(ctx, rng):
 
 def test_gemm_split_rejects_bad_shapes(ctx):
     x = torch.zeros(8, 24, device="cuda:0")
-    planes = torch.zeros(3, 8, 32, dtype=torch.bfloat16, device="cuda:0")
+    pieces = torch.zeros(ctx.split_bytes(8, 32) // 2, dtype=torch.bfloat16, device="cuda:0")
     c = torch.zeros(8, 8, device="cuda:0")
     with pytest.raises(native.NativeError, match="unsupported shape"):
-        ctx.gemm_split(x, planes, c, 8, 8, 24, 32)  # K must be a multiple of 16
+        ctx.gemm_split(x, pieces, c, 8, 8, 24)  # K must be a multiple of 16
     with pytest.raises(native.NativeError, match="unsupported shape"):
-        ctx.gemm_split(x, planes, c, 8, 8, 16, 12, lda=24)  # ldw must be a multiple of 8 and >= K
+        ctx.gemm_split(x, pieces, c, 8, 8, 16, lda=14)  # lda must be a multiple of 4 and >= K
+    with pytest.raises(native.NativeError, match="bad shape"):
+        ctx.split_weights(torch.zeros(8, 24, device="cuda:0"), pieces, 8, 24)  # K % 16
 
 
 @pytest.mark.parametrize("dims_name", ["config", "reference"])
