@@ -35,6 +35,7 @@ ROLES = [
     (r"gemm_bf16_(dma_)?batched_kernel(<|ILi)0", "band split / mask layer 2 (bf16 variant)"),
     (r"attention_bf16_kernel(<|ILi)4", "time-axis attention, L = 801 (bf16 variant)"),
     (r"attention_bf16_kernel(<|ILi)2", "band-axis attention, L = 62 (bf16 variant)"),
+    (r"attention_split_kernel", "time-axis attention, L = 801 (fp32 via split bf16)"),
     (r"attention_kernel(<|ILi)4", "time-axis attention, L = 801"),
     (r"attention_short_kernel", "band-axis attention, L = 62"),
     (r"rmsnorm_kernel", "pre-norms and final norm"),
