@@ -9,8 +9,11 @@
 //     km.qh, kh.qm, kh.qh), small products first.
 //   O^T += V^T * P^T: the lane's fp32 probabilities of keys
 //     {16st + 4lh + 0..3, 16st + 8 + 4lh + 0..3} (registers 8st..8st+7, the
-//     bf16 kernel's key order) are split in registers; V^T pieces are read in
-//     the same key order; six products per 16 keys and 32 dims.
+//     bf16 kernel's key order) are split in registers; six products per 16
+//     keys and 32 dims.  Each V^T row stores its keys permuted inside groups
+//     of 16 (keys 0-3, 8-11, 4-7, 12-15), so those eight keys are one
+//     16-byte read per piece, and each thread stages two adjacent keys so the
+//     transposed writes are 32-bit pairs.
 // The probabilities, statistics, normalisation and gate are fp32 as in the
 // fp32 kernel; the dropped piece products are below 2^-23 of each term.
 #pragma once
@@ -65,14 +68,14 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
     }
 
     // Staging: chunk c of the K tile is key c/8, dims 8*(c%8); chunk c of the
-    // V tile is key c%32, dims 8*(c/32) (the bf16 kernel's maps).
+    // V tile is keys 2*(c%16) and 2*(c%16)+1, dims 4*(c/16) .. +3.
     floatx4 kreg[PER_T][2], vreg[PER_T][2];
     auto load = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
             const int c = tid + NT * i;
             const int kk = c >> 3, kd = 8 * (c & 7);
-            const int vk = c & 31, vd = 8 * (c >> 5);
+            const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
             const int pk = kb * ATT_KB + kk, pv = kb * ATT_KB + vk;
             if (pk < a.L) {
                 const float *kp = qkv + (size_t)attn_row(a, s, pk) * a.ld + kcol + kd;
@@ -81,12 +84,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
             } else {
                 kreg[i][0] = kreg[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
             }
-            if (pv < a.L) {
-                const float *vp = qkv + (size_t)attn_row(a, s, pv) * a.ld + vcol + vd;
-                vreg[i][0] = ld4(vp);
-                vreg[i][1] = ld4(vp + 4);
-            } else {
-                vreg[i][0] = vreg[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                if (pv + e < a.L) vreg[i][e] = ld4(qkv + (size_t)attn_row(a, s, pv + e) * a.ld + vcol + vd);
+                else vreg[i][e] = floatx4{0.f, 0.f, 0.f, 0.f};
             }
         }
     };
@@ -98,12 +99,17 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
             split8(kreg[i][0], kreg[i][1], p[0], p[1], p[2]);
 #pragma unroll
             for (int k = 0; k < 3; k++) *reinterpret_cast<bf16x8 *>(&Ks[buf][k][c >> 3][8 * (c & 7)]) = p[k];
+            // p[k] = pieces of (key vk: dims vd..vd+3, key vk+1: dims vd..vd+3)
             split8(vreg[i][0], vreg[i][1], p[0], p[1], p[2]);
-            const int vk = c & 31, vd = 8 * (c >> 5);
+            const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
+            const int pos = (vk & 16) | split_k_slot(vk & 15);  // even: the pair stays adjacent
 #pragma unroll
             for (int k = 0; k < 3; k++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) Vt[buf][k][vd + e][vk] = p[k][e];
+                for (int e = 0; e < 4; e++) {
+                    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                    *reinterpret_cast<bf16x2_t *>(&Vt[buf][k][vd + e][pos]) = bf16x2_t{p[k][e], p[k][4 + e]};
+                }
         }
     };
 
@@ -153,12 +159,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
                 for (int t = 0; t < 2; t++) {
                     bf16x8 v[3];
 #pragma unroll
-                    for (int k = 0; k < 3; k++) {
-                        const bf16 *vr = &Vt[buf][k][32 * t + li][16 * st + 4 * lh];
-                        const bf16x4 v0 = *reinterpret_cast<const bf16x4 *>(vr);
-                        const bf16x4 v1 = *reinterpret_cast<const bf16x4 *>(vr + 8);
-                        v[k] = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                    }
+                    for (int k = 0; k < 3; k++)
+                        v[k] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][k][32 * t + li][16 * st + 8 * lh]);
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[2], ph, o[t], 0, 0, 0);
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pl, o[t], 0, 0, 0);
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], pm, o[t], 0, 0, 0);
