@@ -86,8 +86,9 @@ int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int ld
    exact sum of three bf16 pieces (h = bf16(x), m = bf16(x - h),
    l = x - h - m) and the six piece products that reach 2^-24 of a product
    are accumulated in fp32.  Ws: the weight's pieces from vh_split_weights.
-   K a multiple of 16, lda a multiple of 4, A and Ws 16-byte aligned.  The
-   token-wise linear of native/vocalarc_separation.c:631-636, as vh_gemm. */
+   K a multiple of 16, lda a multiple of 4 and at most 2^21, A and Ws
+   16-byte aligned.  The token-wise linear of
+   native/vocalarc_separation.c:631-636, as vh_gemm. */
 int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws,
                   const float *bias, float *C, int ldc, int epilogue);
 /* Bytes of the pieces of an N x K weight (N rounded up to 128 rows). */

@@ -271,6 +271,15 @@ VH_DEVICE void lds_dma16(const void *gaddr, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gaddr), "s"(lds_base) : "memory");
 }
 
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// byte offset (the instruction's saddr form): one VGPR per load stream
+// instead of a 64-bit address pair, and no per-lane address arithmetic when
+// the base advances.
+VH_DEVICE void lds_dma16s(uint32_t voffset, const void *sbase, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voffset), "s"(sbase), "s"(lds_base)
+                 : "memory");
+}
+
 template <int N>
 VH_DEVICE void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");

@@ -32,6 +32,10 @@
 // ring: A as fp32 rows of 64 B (4 slots, slot c of row r at c ^ (r/4)%4),
 // each W plane as rows of 32 B (2 slots, slot s of row r at s ^ (r/8)%2), so
 // the operand reads are conflict-free.  56 KB of LDS, two workgroups per CU.
+// The loads take a wave-uniform base and a 32-bit lane offset (the saddr
+// form), which keeps the kernel within 120 VGPRs and its address arithmetic
+// scalar; the per-wave branch on live accumulator columns is taken once per
+// tile, outside the K loop.
 #pragma once
 
 #include "gemm_bf16.hpp"
@@ -111,7 +115,9 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
     const int n0 = (in_group / group_rows) * GS_BN;
 
     const int tid = (int)threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    // wave-uniform: the per-wave choices below are scalar branches and the
+    // load bases live in SGPRs
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 31, lh = lane >> 5;
     const uint32_t ring_base = (uint32_t)(uintptr_t)ring;
@@ -119,35 +125,30 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
     auto swz_w = [](int r) { return (r >> 3) & 1; };
 
     // Each load instruction fills 1 KB of the stage.  A: 16 blocks of 16 rows
-    // (lane -> row l/4, slot l%4); wave w loads blocks w and w+8.  W: the 12
-    // 1 KB blocks of the chunk's tile-major image, lane l the l-th 16 bytes;
-    // wave w loads block w, and waves 0-3 also block w+8.
-    const float *a_src[2];
-    uint32_t a_off[2];
+    // (lane -> row l/4, slot l%4); wave w loads blocks w and w+8, each lane
+    // from the tile's first row (scalar base) plus its own byte offset (below
+    // 2^32: 256 rows of lda <= 2^21 floats).  W: the 12 1 KB blocks of the chunk's
+    // tile-major image, lane l the l-th 16 bytes; wave w loads block w, and
+    // waves 0-3 also block w+8.
+    const float *a_base = d.A + (size_t)m0 * d.lda;
+    uint32_t a_voff[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        const int q = wave + 8 * j;
-        const int r = 16 * q + (lane >> 2);
-        a_src[j] = d.A + (size_t)min(m0 + r, d.M - 1) * d.lda + 4 * ((lane & 3) ^ swz_a(r));
-        a_off[j] = q * 1024;
+        const int r = 16 * (wave + 8 * j) + (lane >> 2);
+        a_voff[j] = (uint32_t)(min(m0 + r, d.M - 1) - m0) * (uint32_t)d.lda * 4u + 16u * ((lane & 3) ^ swz_a(r));
     }
-    const bf16 *w_src[2];
-    uint32_t w_off[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int b = min(wave + 8 * j, 11);
-        w_src[j] = d.W + (size_t)(n0 / GS_BN) * (d.K / GS_BK) * GS_WBLOCK + b * 512 + 8 * lane;
-        w_off[j] = A_BYTES + b * 1024;
-    }
+    const bf16 *w_base = d.W + (size_t)(n0 / GS_BN) * (d.K / GS_BK) * GS_WBLOCK;
+    const uint32_t w_voff = 16 * lane;
+    const int wb1 = min(wave + 8, 11);
     const bool two_w = wave < 4;
     auto issue = [&](int kt) {
         const uint32_t sb = ring_base + (kt & 1) * STAGE_BYTES;
-        const int k0 = kt * GS_BK;
-        lds_dma16(a_src[0] + k0, __builtin_amdgcn_readfirstlane(sb + a_off[0]));
-        lds_dma16(a_src[1] + k0, __builtin_amdgcn_readfirstlane(sb + a_off[1]));
-        const int wk = kt * GS_WBLOCK;
-        lds_dma16(w_src[0] + wk, __builtin_amdgcn_readfirstlane(sb + w_off[0]));
-        if (two_w) lds_dma16(w_src[1] + wk, __builtin_amdgcn_readfirstlane(sb + w_off[1]));
+        const float *ab = a_base + kt * GS_BK;
+        lds_dma16s(a_voff[0], ab, sb + wave * 1024);
+        lds_dma16s(a_voff[1], ab, sb + (wave + 8) * 1024);
+        const bf16 *wb = w_base + (size_t)kt * GS_WBLOCK;
+        lds_dma16s(w_voff, wb + wave * 512, sb + A_BYTES + wave * 1024);
+        if (two_w) lds_dma16s(w_voff, wb + wb1 * 512, sb + A_BYTES + wb1 * 1024);
     };
 
     floatx16 acc[2][2];
@@ -158,52 +159,56 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    // Accumulator columns past N (the ragged last column tile) are skipped
-    // as a whole: one wave-uniform branch per chunk, not one per MFMA.
-    const bool live1 = n0 + wn * 64 + 32 < d.N;
-    const bool live0 = n0 + wn * 64 < d.N;
     const int nk = d.K / GS_BK;
     issue(0);
     wait_vmcnt<0>();
     __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        // chunk kt+1 goes to the slot chunk kt-1 used: every wave finished
-        // reading it before the barrier that ended the previous iteration
-        if (kt + 1 < nk) issue(kt + 1);
-        const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
-        bf16x8 ah[2], am[2], al[2], wh[2], wmd[2], wl[2];
+    // The K loop for a wave with NJ live accumulator columns (2; 1 or 0 in the
+    // ragged last column tile, whose columns past N are skipped): chosen once
+    // per tile, so the loop body is one basic block the compiler can schedule
+    // as a whole.  Every wave takes part in the loads and barriers.
+    auto k_loop = [&](auto nj_c) {
+        constexpr int NJ = decltype(nj_c)::value;
+        for (int kt = 0; kt < nk; kt++) {
+            // chunk kt+1 goes to the slot chunk kt-1 used: every wave finished
+            // reading it before the barrier that ended the previous iteration
+            if (kt + 1 < nk) issue(kt + 1);
+            if constexpr (NJ > 0) {
+                const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
+                bf16x8 ah[2], am[2], al[2], wh[NJ], wmd[NJ], wl[NJ];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int r = wm * 64 + 32 * i + li;
-            const floatx4 lo = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * (lh ^ swz_a(r)));
-            const floatx4 hi = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * ((2 + lh) ^ swz_a(r)));
-            split8(lo, hi, ah[i], am[i], al[i]);
+                for (int i = 0; i < 2; i++) {
+                    const int r = wm * 64 + 32 * i + li;
+                    const floatx4 lo = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * (lh ^ swz_a(r)));
+                    const floatx4 hi = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * ((2 + lh) ^ swz_a(r)));
+                    split8(lo, hi, ah[i], am[i], al[i]);
+                }
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    const int r = wn * 64 + 32 * j + li;
+                    const unsigned char *wp = sbuf + A_BYTES + r * 32 + 16 * (lh ^ swz_w(r));
+                    wh[j] = *reinterpret_cast<const bf16x8 *>(wp);
+                    wmd[j] = *reinterpret_cast<const bf16x8 *>(wp + P_BYTES);
+                    wl[j] = *reinterpret_cast<const bf16x8 *>(wp + 2 * P_BYTES);
+                }
+                // small products first: (l,h) (h,l) (m,m) (m,h) (h,m) (h,h)
+                const bf16x8 *pa[6] = {al, ah, am, am, ah, ah};
+                const bf16x8 *pw[6] = {wh, wl, wmd, wh, wmd, wh};
+#pragma unroll
+                for (int t = 0; t < 6; t++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+#pragma unroll
+                        for (int i = 0; i < 2; i++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[t][i], pw[t][j], acc[i][j], 0, 0, 0);
+            }
+            wait_vmcnt<0>();  // chunk kt+1 has landed
+            __syncthreads();
         }
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int r = wn * 64 + 32 * j + li;
-            const unsigned char *wp = sbuf + A_BYTES + r * 32 + 16 * (lh ^ swz_w(r));
-            wh[j] = *reinterpret_cast<const bf16x8 *>(wp);
-            wmd[j] = *reinterpret_cast<const bf16x8 *>(wp + P_BYTES);
-            wl[j] = *reinterpret_cast<const bf16x8 *>(wp + 2 * P_BYTES);
-        }
-        // small products first: (l,h) (h,l) (m,m) (m,h) (h,m) (h,h)
-        const bf16x8 *pa[6] = {al, ah, am, am, ah, ah};
-        const bf16x8 *pw[6] = {wh, wl, wmd, wh, wmd, wh};
-        auto products = [&](auto nj) {
-#pragma unroll
-            for (int t = 0; t < 6; t++)
-#pragma unroll
-                for (int j = 0; j < decltype(nj)::value; j++)
-#pragma unroll
-                    for (int i = 0; i < 2; i++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[t][i], pw[t][j], acc[i][j], 0, 0, 0);
-        };
-        if (live1) products(std::integral_constant<int, 2>());
-        else if (live0) products(std::integral_constant<int, 1>());
-        wait_vmcnt<0>();  // chunk kt+1 has landed
-        __syncthreads();
-    }
+    };
+    if (n0 + wn * 64 + 32 < d.N) k_loop(std::integral_constant<int, 2>());
+    else if (n0 + wn * 64 < d.N) k_loop(std::integral_constant<int, 1>());
+    else k_loop(std::integral_constant<int, 0>());
     GemmDescBF16 e{};
     e.bias = d.bias; e.C = d.C; e.M = d.M; e.N = d.N; e.K = d.K; e.ldc = d.ldc;
     gemm_bf16_epilogue<EPI, float, 2, 2>(e, acc, m0 + wm * 64, n0 + wn * 64, li, lh);

@@ -322,7 +322,7 @@ static_assert(GS_BK == SPLIT_K_MULTIPLE, "split GEMM K chunk");
 
 static bool gemm_split_ok(const GemmArgsSplit &g, int epilogue) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2) return false;
-    if (g.K % GS_BK || g.lda % 4 || g.lda < g.K) return false;
+    if (g.K % GS_BK || g.lda % 4 || g.lda < g.K || g.lda > (1 << 21)) return false;  // lane load offsets are 32-bit
     if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return false;
     return true;
