@@ -26,16 +26,18 @@
 // in memory (no producer changes); each wave splits the A values it reads
 // from LDS in registers.
 //
-// Pipeline.  256x128 block, 8 waves in a 4x2 grid of 64x64 (2x2 32x32
-// accumulators), K in chunks of 16.  Operands go straight from global memory
-// to LDS (global_load_lds_dwordx4, as gemm_bf16_dma_kernel) into a 2-chunk
-// ring: A as fp32 rows of 64 B (4 slots, slot c of row r at c ^ (r/4)%4),
-// each W plane as rows of 32 B (2 slots, slot s of row r at s ^ (r/8)%2), so
-// the operand reads are conflict-free.  56 KB of LDS, two workgroups per CU.
+// Pipeline.  256x128 block, 8 waves of 32x128 (four 32x32 accumulators in a
+// row), K in chunks of 16: each wave splits the eight A values per lane of
+// its 32 rows (every A element is split once per block) and reads all four
+// W column tiles.  Operands go straight from global memory to LDS
+// (global_load_lds_dwordx4, as gemm_bf16_dma_kernel) into a 2-chunk ring: A
+// as fp32 rows of 64 B (4 slots, slot c of row r at c ^ (r/4)%4), each W
+// plane as rows of 32 B (2 slots, slot s of row r at s ^ (r/8)%2), so the
+// operand reads are conflict-free.  56 KB of LDS, two workgroups per CU.
 // The loads take a wave-uniform base and a 32-bit lane offset (the saddr
 // form), which keeps the kernel within 120 VGPRs and its address arithmetic
-// scalar; the per-wave branch on live accumulator columns is taken once per
-// tile, outside the K loop.
+// scalar; the branch on live accumulator columns is taken once per tile,
+// outside the K loop.
 #pragma once
 
 #include "gemm_bf16.hpp"
@@ -118,7 +120,6 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
     // wave-uniform: the per-wave choices below are scalar branches and the
     // load bases live in SGPRs
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 31, lh = lane >> 5;
     const uint32_t ring_base = (uint32_t)(uintptr_t)ring;
     auto swz_a = [](int r) { return (r >> 2) & 3; };
@@ -151,67 +152,67 @@ __device__ __forceinline__ void gemm_split_body(const GemmDescSplit &d, int tile
         if (two_w) lds_dma16s(w_voff, wb + wb1 * 512, sb + A_BYTES + wb1 * 1024);
     };
 
-    floatx16 acc[2][2];
+    floatx16 acc[1][4];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int j = 0; j < 4; j++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 16; r++) acc[0][j][r] = 0.0f;
 
     const int nk = d.K / GS_BK;
     issue(0);
     wait_vmcnt<0>();
     __syncthreads();
-    // The K loop for a wave with NJ live accumulator columns (2; 1 or 0 in the
-    // ragged last column tile, whose columns past N are skipped): chosen once
-    // per tile, so the loop body is one basic block the compiler can schedule
-    // as a whole.  Every wave takes part in the loads and barriers.
+    // The K loop for NJ live 32-column accumulators (4; 2 or 1 in a ragged
+    // last column tile, whose columns past N are skipped, or computed from
+    // the zero rows of the pieces when N - n0 is 65..96): chosen once per
+    // tile, so the loop body is one basic block the compiler can schedule as
+    // a whole.
     auto k_loop = [&](auto nj_c) {
         constexpr int NJ = decltype(nj_c)::value;
         for (int kt = 0; kt < nk; kt++) {
             // chunk kt+1 goes to the slot chunk kt-1 used: every wave finished
             // reading it before the barrier that ended the previous iteration
             if (kt + 1 < nk) issue(kt + 1);
-            if constexpr (NJ > 0) {
-                const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
-                bf16x8 ah[2], am[2], al[2], wh[NJ], wmd[NJ], wl[NJ];
+            const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
+            const int r = wave * 32 + li;
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * (lh ^ swz_a(r)));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * ((2 + lh) ^ swz_a(r)));
+            bf16x8 ah, am, al;
+            split8(lo, hi, ah, am, al);
+            // small products first: (l,h) (h,l) (m,m) (m,h) (h,m) (h,h)
+            const bf16x8 pa[6] = {al, ah, am, am, ah, ah};
+            // W column tiles two at a time: their 6 pieces, then 12 products
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const int r = wm * 64 + 32 * i + li;
-                    const floatx4 lo = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * (lh ^ swz_a(r)));
-                    const floatx4 hi = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * ((2 + lh) ^ swz_a(r)));
-                    split8(lo, hi, ah[i], am[i], al[i]);
-                }
+            for (int jp = 0; jp < (NJ + 1) / 2; jp++) {
+                constexpr int NJJ = NJ == 1 ? 1 : 2;
+                bf16x8 wh[NJJ], wmd[NJJ], wl[NJJ];
 #pragma unroll
-                for (int j = 0; j < NJ; j++) {
-                    const int r = wn * 64 + 32 * j + li;
-                    const unsigned char *wp = sbuf + A_BYTES + r * 32 + 16 * (lh ^ swz_w(r));
-                    wh[j] = *reinterpret_cast<const bf16x8 *>(wp);
-                    wmd[j] = *reinterpret_cast<const bf16x8 *>(wp + P_BYTES);
-                    wl[j] = *reinterpret_cast<const bf16x8 *>(wp + 2 * P_BYTES);
+                for (int jj = 0; jj < NJJ; jj++) {
+                    const int rw = 32 * (2 * jp + jj) + li;
+                    const unsigned char *wp = sbuf + A_BYTES + rw * 32 + 16 * (lh ^ swz_w(rw));
+                    wh[jj] = *reinterpret_cast<const bf16x8 *>(wp);
+                    wmd[jj] = *reinterpret_cast<const bf16x8 *>(wp + P_BYTES);
+                    wl[jj] = *reinterpret_cast<const bf16x8 *>(wp + 2 * P_BYTES);
                 }
-                // small products first: (l,h) (h,l) (m,m) (m,h) (h,m) (h,h)
-                const bf16x8 *pa[6] = {al, ah, am, am, ah, ah};
                 const bf16x8 *pw[6] = {wh, wl, wmd, wh, wmd, wh};
 #pragma unroll
                 for (int t = 0; t < 6; t++)
 #pragma unroll
-                    for (int j = 0; j < NJ; j++)
-#pragma unroll
-                        for (int i = 0; i < 2; i++)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[t][i], pw[t][j], acc[i][j], 0, 0, 0);
+                    for (int jj = 0; jj < NJJ; jj++)
+                        acc[0][2 * jp + jj] =
+                            __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[t], pw[t][jj], acc[0][2 * jp + jj], 0, 0, 0);
             }
             wait_vmcnt<0>();  // chunk kt+1 has landed
             __syncthreads();
         }
     };
-    if (n0 + wn * 64 + 32 < d.N) k_loop(std::integral_constant<int, 2>());
-    else if (n0 + wn * 64 < d.N) k_loop(std::integral_constant<int, 1>());
-    else k_loop(std::integral_constant<int, 0>());
+    const int live = d.N - n0;
+    if (live > 64) k_loop(std::integral_constant<int, 4>());
+    else if (live > 32) k_loop(std::integral_constant<int, 2>());
+    else k_loop(std::integral_constant<int, 1>());
     GemmDescBF16 e{};
     e.bias = d.bias; e.C = d.C; e.M = d.M; e.N = d.N; e.K = d.K; e.ldc = d.ldc;
-    gemm_bf16_epilogue<EPI, float, 2, 2>(e, acc, m0 + wm * 64, n0 + wn * 64, li, lh);
+    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh);
 }
 
 template <int EPI>
