@@ -42,86 +42,52 @@ static __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__rest
 
 // ------------------------------------------------------------ row softmax
 // Materialised softmax of score rows (max, exp, sum, divide), the
-// decomposition of native/native_gpu_cuda.cu:357-381, one wavefront per row.
-// Rows of odd length are not 16-byte aligned, so a wave reads the aligned
-// float4 chunks that cover its row and masks the neighbouring rows'
-// elements; chunks that straddle a row boundary are written element by
-// element (the neighbour belongs to another wave).
-template <int MAXC>
-VH_DEVICE void softmax_load_row(const float *__restrict__ in, int64_t row, int len, int64_t total, int lane,
-                                floatx4 (&v)[MAXC], float &m) {
-    const int64_t first = row * len, last = first + len;  // [first, last)
-    const int64_t c0 = first >> 2;                        // first float4 chunk
-    const int nchunks = (int)(((last + 3) >> 2) - c0);
-    m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < MAXC; i++) {
-        const int c = lane + 64 * i;
-        v[i] = floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        if (c < nchunks) {
-            const int64_t e0 = (c0 + c) * 4;
-            floatx4 x;
-            if (e0 + 4 <= total) {
-                x = ld4_stream(in + e0);
-            } else {  // the tensor's last chunk may be partial: no read past its end
-#pragma unroll
-                for (int k = 0; k < 4; k++) x[k] = e0 + k < total ? in[e0 + k] : 0.0f;
-            }
-            if (e0 >= first && e0 + 4 <= last) {
-                v[i] = x;
-            } else {
-#pragma unroll
-                for (int k = 0; k < 4; k++) v[i][k] = (e0 + k >= first && e0 + k < last) ? x[k] : -INFINITY;
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) m = fmaxf(m, v[i][k]);
-    }
-}
-
-template <int MAXC>
-VH_DEVICE void softmax_store_row(float *__restrict__ out, int64_t row, int len, int lane, floatx4 (&v)[MAXC],
-                                 float m) {
-    const int64_t first = row * len, last = first + len;
-    const int64_t c0 = first >> 2;
-    const int nchunks = (int)(((last + 3) >> 2) - c0);
-    m = wave_max(m);
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < MAXC; i++)
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            v[i][k] = fast_exp_dev(v[i][k] - m);  // exp(-inf) = 0 for masked elements
-            s += v[i][k];
-        }
-    const float inv = 1.0f / wave_sum(s);
-#pragma unroll
-    for (int i = 0; i < MAXC; i++) {
-        const int c = lane + 64 * i;
-        if (c < nchunks) {
-            const int64_t e0 = (c0 + c) * 4;
-            const floatx4 y = v[i] * inv;
-            if (e0 >= first && e0 + 4 <= last) {
-                st4_stream(out + e0, y);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    if (e0 + k >= first && e0 + k < last) out[e0 + k] = y[k];
-            }
-        }
-    }
-}
-
-template <int MAXC>
+// decomposition of native/native_gpu_cuda.cu:357-381.  A workgroup takes 4
+// consecutive rows: their 4*len floats start 16-byte aligned whatever len is
+// (the first row index is a multiple of 4), so the block moves them between
+// HBM and LDS as whole aligned float4s (non-temporal) and never splits a
+// chunk with a neighbouring block; wave w then reduces row w from LDS (lane
+// l holds elements l, l+64, ...) and writes the result back for the block's
+// aligned store.  Rows up to 64*MAXV long.
+template <int MAXV>
 static __global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restrict__ in,
                                                                   float *__restrict__ out, int64_t rows, int len) {
-    const int64_t row = (int64_t)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
-    const int lane = (int)threadIdx.x & 63;
-    if (row >= rows) return;
-    floatx4 v[MAXC];
-    float m;
-    softmax_load_row<MAXC>(in, row, len, rows * len, lane, v, m);
-    softmax_store_row<MAXC>(out, row, len, lane, v, m);
+    extern __shared__ float srow[];  // [4][len]
+    const int tid = (int)threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t row0 = (int64_t)blockIdx.x * 4;
+    const int nrows = (int)min<int64_t>(4, rows - row0);
+    const int64_t e0 = row0 * len;
+    const int ne = nrows * len, n4 = ne >> 2;
+    for (int c = tid; c < n4; c += 256) *reinterpret_cast<floatx4 *>(&srow[4 * c]) = ld4_stream(in + e0 + 4 * c);
+    for (int e = 4 * n4 + tid; e < ne; e += 256) srow[e] = in[e0 + e];  // the last block's partial chunk
+    __syncthreads();
+    if (w < nrows) {
+        float *r = srow + w * len;
+        float v[MAXV];
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) {
+            const int e = lane + 64 * i;
+            v[i] = e < len ? r[e] : -INFINITY;
+            m = fmaxf(m, v[i]);
+        }
+        m = wave_max(m);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) {
+            v[i] = fast_exp_dev(v[i] - m);  // exp(-inf) = 0 past the row's end
+            sum += v[i];
+        }
+        const float inv = 1.0f / wave_sum(sum);
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) {
+            const int e = lane + 64 * i;
+            if (e < len) r[e] = v[i] * inv;
+        }
+    }
+    __syncthreads();
+    for (int c = tid; c < n4; c += 256) st4_stream(out + e0 + 4 * c, *reinterpret_cast<const floatx4 *>(&srow[4 * c]));
+    for (int e = 4 * n4 + tid; e < ne; e += 256) out[e0 + e] = srow[e];
 }
 
 // --------------------------------------------------------- rotary [BH][L][64]

@@ -227,8 +227,11 @@ static int64_t tiles_bf16(const GemmArgsBF16 &g) {
 }
 
 // The DMA ring takes whole 32-element K chunks of bf16 A (16-byte aligned
-// rows, which gemm_bf16_ok already requires of bf16 A).
-static bool dma_ok(const GemmArgsBF16 &g) { return g.a_bf16 && g.K % GBD_BK == 0 && !g.staged; }
+// rows, which gemm_bf16_ok already requires of bf16 A) and row pitches whose
+// 256-row offsets fit its 32-bit lane offsets.
+static bool dma_ok(const GemmArgsBF16 &g) {
+    return g.a_bf16 && g.K % GBD_BK == 0 && !g.staged && g.lda <= (1 << 21) && g.ldb <= (1 << 21);
+}
 
 template <int EPI, typename TA, typename TC>
 static void launch_bf16_typed(hipStream_t s, const GemmDescBF16 *single, const GemmBatchBF16 *batch, unsigned tiles,
@@ -407,12 +410,13 @@ bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int 
     }
     Scope sc(t, s, "softmax");
     const unsigned grid = blocks_for(rows, 4);
-    const int chunks = (len + 3) / 4 + 1;  // a row covers at most this many float4 chunks
-    if (chunks <= 64) hipLaunchKernelGGL(softmax_rows_kernel<1>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else if (chunks <= 128) hipLaunchKernelGGL(softmax_rows_kernel<2>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else if (chunks <= 256) hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else if (chunks <= 512) hipLaunchKernelGGL(softmax_rows_kernel<8>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
-    else hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(grid), dim3(256), 0, s, in, out, rows, len);
+    const size_t lds = 4 * (size_t)len * sizeof(float);
+    if (len <= 256) hipLaunchKernelGGL(softmax_rows_kernel<4>, dim3(grid), dim3(256), lds, s, in, out, rows, len);
+    else if (len <= 512) hipLaunchKernelGGL(softmax_rows_kernel<8>, dim3(grid), dim3(256), lds, s, in, out, rows, len);
+    else if (len <= 832) hipLaunchKernelGGL(softmax_rows_kernel<13>, dim3(grid), dim3(256), lds, s, in, out, rows, len);
+    else if (len <= 1024) hipLaunchKernelGGL(softmax_rows_kernel<16>, dim3(grid), dim3(256), lds, s, in, out, rows, len);
+    else if (len <= 2048) hipLaunchKernelGGL(softmax_rows_kernel<32>, dim3(grid), dim3(256), lds, s, in, out, rows, len);
+    else hipLaunchKernelGGL(softmax_rows_kernel<64>, dim3(grid), dim3(256), lds, s, in, out, rows, len);
     return sync_debug(s, "softmax_rows_kernel");
 }
 

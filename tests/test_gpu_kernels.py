@@ -100,7 +100,7 @@ def test_rmsnorm(ctx, rng, rows, dim):
     assert_close(ref, from_dev(dy), rtol=4e-6, atol=1e-6, what=f"rmsnorm {rows}x{dim}")
 
 
-@pytest.mark.parametrize("rows,length", [(7, 801), (100, 62), (3, 1), (5, 2048), (2000, 801)])
+@pytest.mark.parametrize("rows,length", [(7, 801), (100, 62), (3, 1), (5, 2048), (2000, 801), (9, 1000), (6, 4092)])
 def test_softmax_rows(ctx, rng, rows, length):
     x = (3.0 * rng.standard_normal((rows, length))).astype(np.float32)
     ref = O.softmax_rows(x)
