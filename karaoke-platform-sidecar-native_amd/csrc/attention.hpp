@@ -52,8 +52,7 @@ VH_DEVICE int attn_row(const AttnArgs &a, int s, int p) {
 
 // Rotate the two interleaved pairs of a float4 that starts at dimension d0
 // (one 16-byte table load: cos and sin of both pairs).
-VH_DEVICE floatx4 rope4(floatx4 v, const float *tab, int pos, int d0) {
-    if (tab == nullptr) return v;
+VH_DEVICE floatx4 rope4_table(floatx4 v, const float *tab, int pos, int d0) {
     const floatx4 t = ld4(tab + pos * ATT_DH + d0);
     const float c0 = t[0], s0 = t[1], c1 = t[2], s1 = t[3];
     floatx4 r;
@@ -62,6 +61,9 @@ VH_DEVICE floatx4 rope4(floatx4 v, const float *tab, int pos, int d0) {
     r[2] = v[2] * c1 - v[3] * s1;
     r[3] = v[2] * s1 + v[3] * c1;
     return r;
+}
+VH_DEVICE floatx4 rope4(floatx4 v, const float *tab, int pos, int d0) {
+    return tab == nullptr ? v : rope4_table(v, tab, pos, d0);
 }
 
 // Workgroup: WAVES wavefronts x 32 queries of one (sequence, head).  Each

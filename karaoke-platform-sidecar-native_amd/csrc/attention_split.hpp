@@ -24,7 +24,7 @@
 
 namespace vh {
 
-template <int WAVES, typename TO>
+template <int WAVES, typename TO, bool ROPE>
 __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs a) {
     constexpr int NT = 64 * WAVES;
     constexpr int CHUNKS = ATT_KB * ATT_DH / 8;  // 8-element chunks per K (or V) tile: 256
@@ -42,10 +42,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
     const int s = sh / a.H;
 
     const int tid = (int)threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int li = lane & 31, lh = lane >> 5;
     const int q0 = (qg * WAVES + wave) * 32;
-    const bool wave_active = q0 < a.L;
 
     const int kcol = a.inner + h * ATT_DH;
     const int vcol = 2 * a.inner + h * ATT_DH;
@@ -61,56 +60,89 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const int d0 = 16 * g + 8 * lh;
-            const floatx4 lo = rope4(ld4(qp + d0), a.rope, q, d0) * qs;
-            const floatx4 hi = rope4(ld4(qp + d0 + 4), a.rope, q, d0 + 4) * qs;
-            split8(lo, hi, qh[g], qm[g], ql[g]);
+            floatx4 lo = ld4(qp + d0), hi = ld4(qp + d0 + 4);
+            if constexpr (ROPE) {
+                lo = rope4_table(lo, a.rope, q, d0);
+                hi = rope4_table(hi, a.rope, q, d0 + 4);
+            }
+            split8(lo * qs, hi * qs, qh[g], qm[g], ql[g]);
         }
     }
 
-    // Staging: chunk c of the K tile is key c/8, dims 8*(c%8); chunk c of the
-    // V tile is keys 2*(c%16) and 2*(c%16)+1, dims 4*(c/16) .. +3.
-    floatx4 kreg[PER_T][2], vreg[PER_T][2];
-    auto load = [&](int kb) {
+    // Staging.  A stage holds one K block and one V block in registers (K
+    // runs one block ahead of V, below).  Chunk c of the K tile is key c/8,
+    // dims 8*(c%8); chunk c of the V tile is keys 2*(c%16) and 2*(c%16)+1,
+    // dims 4*(c/16) .. +3.  Keys past L (and blocks past the last) load the
+    // row of key L-1 and stage zeros: no branch around the loads.
+    struct Stage {
+        floatx4 k[PER_T][2], v[PER_T][2];
+    };
+    auto load = [&](Stage &st, int kbk, int kbv) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
             const int c = tid + NT * i;
             const int kk = c >> 3, kd = 8 * (c & 7);
-            const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
-            const int pk = kb * ATT_KB + kk, pv = kb * ATT_KB + vk;
-            if (pk < a.L) {
-                const float *kp = qkv + (size_t)attn_row(a, s, pk) * a.ld + kcol + kd;
-                kreg[i][0] = rope4(ld4(kp), a.rope, pk, kd);
-                kreg[i][1] = rope4(ld4(kp + 4), a.rope, pk, kd + 4);
-            } else {
-                kreg[i][0] = kreg[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const int pk = kbk * ATT_KB + kk, pkc = min(pk, a.L - 1);
+            const float *kp = qkv + (size_t)attn_row(a, s, pkc) * a.ld + kcol + kd;
+            floatx4 k0 = ld4(kp), k1 = ld4(kp + 4);
+            if constexpr (ROPE) {
+                k0 = rope4_table(k0, a.rope, pkc, kd);
+                k1 = rope4_table(k1, a.rope, pkc, kd + 4);
             }
+            const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+            st.k[i][0] = pk < a.L ? k0 : zero;
+            st.k[i][1] = pk < a.L ? k1 : zero;
+            const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                if (pv + e < a.L) vreg[i][e] = ld4(qkv + (size_t)attn_row(a, s, pv + e) * a.ld + vcol + vd);
-                else vreg[i][e] = floatx4{0.f, 0.f, 0.f, 0.f};
+                const int pv = kbv * ATT_KB + vk + e;
+                const floatx4 v = ld4(qkv + (size_t)attn_row(a, s, min(pv, a.L - 1)) * a.ld + vcol + vd);
+                st.v[i][e] = pv < a.L ? v : zero;
             }
         }
     };
-    auto store = [&](int buf) {
+    // split a stage's K into Ks[kbuf] and its V (transposed) into Vt[vbuf]
+    auto store = [&](const Stage &st, int kbuf, int vbuf, bool with_v) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
             const int c = tid + NT * i;
             bf16x8 p[3];
-            split8(kreg[i][0], kreg[i][1], p[0], p[1], p[2]);
+            split8(st.k[i][0], st.k[i][1], p[0], p[1], p[2]);
 #pragma unroll
-            for (int k = 0; k < 3; k++) *reinterpret_cast<bf16x8 *>(&Ks[buf][k][c >> 3][8 * (c & 7)]) = p[k];
-            // p[k] = pieces of (key vk: dims vd..vd+3, key vk+1: dims vd..vd+3)
-            split8(vreg[i][0], vreg[i][1], p[0], p[1], p[2]);
-            const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
-            const int pos = (vk & 16) | split_k_slot(vk & 15);  // even: the pair stays adjacent
+            for (int k = 0; k < 3; k++) *reinterpret_cast<bf16x8 *>(&Ks[kbuf][k][c >> 3][8 * (c & 7)]) = p[k];
+            if (with_v) {
+                // p[k] = pieces of (key vk: dims vd..vd+3, key vk+1: dims vd..vd+3)
+                split8(st.v[i][0], st.v[i][1], p[0], p[1], p[2]);
+                const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
+                const int pos = (vk & 16) | split_k_slot(vk & 15);  // even: the pair stays adjacent
 #pragma unroll
-            for (int k = 0; k < 3; k++)
+                for (int k = 0; k < 3; k++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-                    *reinterpret_cast<bf16x2_t *>(&Vt[buf][k][vd + e][pos]) = bf16x2_t{p[k][e], p[k][4 + e]};
-                }
+                    for (int e = 0; e < 4; e++) {
+                        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                        *reinterpret_cast<bf16x2_t *>(&Vt[vbuf][k][vd + e][pos]) = bf16x2_t{p[k][e], p[k][4 + e]};
+                    }
+            }
         }
+    };
+    // S^T block of 32 keys x 32 queries from Ks[kbuf]
+    auto qk = [&](int kbuf) {
+        floatx16 sc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&Ks[kbuf][0][li][16 * g + 8 * lh]);
+            const bf16x8 km = *reinterpret_cast<const bf16x8 *>(&Ks[kbuf][1][li][16 * g + 8 * lh]);
+            const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&Ks[kbuf][2][li][16 * g + 8 * lh]);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, qm[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, qh[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qm[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[g], sc, 0, 0, 0);
+        }
+        return sc;
     };
 
     floatx16 o[2];
@@ -120,61 +152,108 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
         for (int r = 0; r < 16; r++) o[t][r] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const int nkb = (a.L + ATT_KB - 1) / ATT_KB;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kb = 0; kb < nkb; kb++) {
-        const int buf = kb & 1;
-        if (kb + 1 < nkb) load(kb + 1);
-        if (wave_active) {
-            floatx16 sc;
+    // First half of the online softmax of block kb (its scores just
+    // computed): mask keys past L, raise the running maximum (and rescale o
+    // and l) as online_softmax_block does.
+    auto soft_max = [&](floatx16 &sc, int kb) {
+        const int valid = a.L - kb * ATT_KB;
+        if (valid < ATT_KB) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+            for (int r = 0; r < 16; r++)
+                if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
+        }
+        float mb = -INFINITY;
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&Ks[buf][0][li][16 * g + 8 * lh]);
-                const bf16x8 km = *reinterpret_cast<const bf16x8 *>(&Ks[buf][1][li][16 * g + 8 * lh]);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&Ks[buf][2][li][16 * g + 8 * lh]);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[g], sc, 0, 0, 0);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[g], sc, 0, 0, 0);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, qm[g], sc, 0, 0, 0);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, qh[g], sc, 0, 0, 0);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qm[g], sc, 0, 0, 0);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[g], sc, 0, 0, 0);
-            }
-            const int valid = a.L - kb * ATT_KB;
-            if (valid < ATT_KB) {
+        for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        const bool grow = mb > m_run + 8.0f;
+        if (__ballot(grow)) {
+            const float m_new = grow ? mb : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+            o[0] *= alpha;
+            o[1] *= alpha;
+            m_run = m_new;
+        }
+    };
+    // Second half (probabilities, row sum) and O^T += V^T P^T from Vt[vbuf].
+    auto soft_pv = [&](floatx16 &sc, int vbuf) {
+        float ls = 0.0f;
 #pragma unroll
-                for (int r = 0; r < 16; r++)
-                    if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
-            }
-            online_softmax_block(sc, m_run, l_run, o);
+        for (int r = 0; r < 16; r++) {
+            sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_run);
+            ls += sc[r];
+        }
+        l_run += ls;
 #pragma unroll
-            for (int st = 0; st < 2; st++) {
-                bf16x8 ph, pm, pl;
-                split8(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
-                       floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, ph, pm, pl);
+        for (int st = 0; st < 2; st++) {
+            bf16x8 ph, pm, pl;
+            split8(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
+                   floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, ph, pm, pl);
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    bf16x8 v[3];
+            for (int t = 0; t < 2; t++) {
+                bf16x8 v[3];
 #pragma unroll
-                    for (int k = 0; k < 3; k++)
-                        v[k] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][k][32 * t + li][16 * st + 8 * lh]);
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[2], ph, o[t], 0, 0, 0);
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pl, o[t], 0, 0, 0);
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], pm, o[t], 0, 0, 0);
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], ph, o[t], 0, 0, 0);
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pm, o[t], 0, 0, 0);
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], ph, o[t], 0, 0, 0);
-                }
+                for (int k = 0; k < 3; k++)
+                    v[k] = *reinterpret_cast<const bf16x8 *>(&Vt[vbuf][k][32 * t + li][16 * st + 8 * lh]);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[2], ph, o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pl, o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], pm, o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], ph, o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pm, o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], ph, o[t], 0, 0, 0);
             }
         }
-        if (kb + 1 < nkb) store(buf ^ 1);
-        __syncthreads();
+    };
+
+    // Pipeline over key blocks kb = 0 .. nkb-1.  Entering iteration kb:
+    // Ks[(kb+1)%2] holds K(kb+1), Vt[kb%2] holds V(kb), the registers of
+    // stage `cur` hold K(kb+2) and V(kb+1), and S holds block kb's scores
+    // with its maximum applied.  The iteration loads K(kb+3), V(kb+2) into
+    // stage `nxt`, computes block kb+1's scores (their MFMAs run beside
+    // block kb's exponentials), accumulates block kb's P V, stages `cur`
+    // into Ks[kb%2] and Vt[(kb+1)%2] (read last in iteration kb-1), and
+    // after the barrier applies block kb+1's maximum.  Blocks past the last
+    // are computed from staged zeros and never used.
+    const int nkb = (a.L + ATT_KB - 1) / ATT_KB;
+    Stage sa, sb;
+    load(sa, 0, 0);
+    store(sa, 0, 0, true);
+    load(sb, 1, 1);
+    store(sb, 1, 0, false);
+    load(sa, 2, 1);
+    __syncthreads();
+    auto run = [&](auto active_c) {
+        constexpr bool ACTIVE = decltype(active_c)::value;
+        floatx16 s0, s1;
+        if constexpr (ACTIVE) {
+            s0 = qk(0);
+            soft_max(s0, 0);
+        }
+        __syncthreads();  // every wave has read K(0): iteration 0 restages Ks[0]
+        auto iteration = [&](int kb, Stage &cur, Stage &nxt, floatx16 &sc, floatx16 &sn) {
+            load(nxt, kb + 3, kb + 2);
+            if constexpr (ACTIVE) {
+                sn = qk((kb + 1) & 1);
+                soft_pv(sc, kb & 1);
+            }
+            store(cur, kb & 1, (kb + 1) & 1, true);
+            __syncthreads();
+            if constexpr (ACTIVE) {
+                if (kb + 1 < nkb) soft_max(sn, kb + 1);
+            }
+        };
+        for (int kb = 0; kb < nkb; kb += 2) {
+            iteration(kb, sa, sb, s0, s1);
+            if (kb + 1 < nkb) iteration(kb + 1, sb, sa, s1, s0);
+        }
+    };
+    if (q0 < a.L) run(std::true_type());
+    else {
+        run(std::false_type());
+        return;
     }
 
-    if (!wave_active) return;
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     const int q = q0 + li;
     if (q >= a.L) return;

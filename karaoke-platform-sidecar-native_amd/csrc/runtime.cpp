@@ -474,8 +474,13 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
     const dim3 block(64 * WAVES);
     if constexpr (WAVES == 4) {
         if (split) {
-            if (out_bf16) hipLaunchKernelGGL((attention_split_kernel<WAVES, bf16>), dim3(grid), block, 0, s, a);
-            else hipLaunchKernelGGL((attention_split_kernel<WAVES, float>), dim3(grid), block, 0, s, a);
+            if (a.rope) {
+                if (out_bf16) hipLaunchKernelGGL((attention_split_kernel<WAVES, bf16, true>), dim3(grid), block, 0, s, a);
+                else hipLaunchKernelGGL((attention_split_kernel<WAVES, float, true>), dim3(grid), block, 0, s, a);
+            } else {
+                if (out_bf16) hipLaunchKernelGGL((attention_split_kernel<WAVES, bf16, false>), dim3(grid), block, 0, s, a);
+                else hipLaunchKernelGGL((attention_split_kernel<WAVES, float, false>), dim3(grid), block, 0, s, a);
+            }
             return;
         }
     }
