@@ -50,17 +50,21 @@ VH_DEVICE int attn_row(const AttnArgs &a, int s, int p) {
     return (s / a.group) * a.group_stride + (s % a.group) * a.seq_stride + p * a.pos_stride;
 }
 
-// Rotate the two interleaved pairs of a float4 that starts at dimension d0
-// (one 16-byte table load: cos and sin of both pairs).
-VH_DEVICE floatx4 rope4_table(floatx4 v, const float *tab, int pos, int d0) {
-    const floatx4 t = ld4(tab + pos * ATT_DH + d0);
+// Rotate the two interleaved pairs of a float4 by t = (cos, sin) of each
+// pair; rope4_table reads t for the float4 at dimension d0 of position pos
+// from the table (one 16-byte load).
+VH_DEVICE floatx4 rope_pairs(floatx4 v, floatx4 t) {
     const float c0 = t[0], s0 = t[1], c1 = t[2], s1 = t[3];
     floatx4 r;
-    r[0] = v[0] * c0 - v[1] * s0;
-    r[1] = v[0] * s0 + v[1] * c0;
-    r[2] = v[2] * c1 - v[3] * s1;
-    r[3] = v[2] * s1 + v[3] * c1;
+    // explicit fused forms: the same rounding in every kernel that rotates
+    r[0] = __builtin_fmaf(v[0], c0, -(v[1] * s0));
+    r[1] = __builtin_fmaf(v[0], s0, v[1] * c0);
+    r[2] = __builtin_fmaf(v[2], c1, -(v[3] * s1));
+    r[3] = __builtin_fmaf(v[2], s1, v[3] * c1);
     return r;
+}
+VH_DEVICE floatx4 rope4_table(floatx4 v, const float *tab, int pos, int d0) {
+    return rope_pairs(v, ld4(tab + pos * ATT_DH + d0));
 }
 VH_DEVICE floatx4 rope4(floatx4 v, const float *tab, int pos, int d0) {
     return tab == nullptr ? v : rope4_table(v, tab, pos, d0);

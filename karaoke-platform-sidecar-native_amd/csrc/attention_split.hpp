@@ -69,72 +69,87 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
         }
     }
 
-    // Staging.  A stage holds one K block and one V block in registers (K
-    // runs one block ahead of V, below).  Chunk c of the K tile is key c/8,
-    // dims 8*(c%8); chunk c of the V tile is keys 2*(c%16) and 2*(c%16)+1,
-    // dims 4*(c/16) .. +3.  Keys past L (and blocks past the last) load the
-    // row of key L-1 and stage zeros: no branch around the loads.
+    // Staging.  The stage holds one K block and one V block in registers as
+    // loaded (K runs one block ahead of V, below); rotation and the split
+    // happen when it is written to LDS, an iteration after its loads were
+    // issued, so no wait on them falls inside the iteration's MFMA work.
+    // Chunk c of the K tile is key c/8, dims 8*(c%8); chunk c of the V tile
+    // is keys 2*(c%16) and 2*(c%16)+1, dims 4*(c/16) .. +3.  Keys past L (and
+    // blocks past the last) load the row of key L-1: no branch around the
+    // loads, and nothing to zero -- their scores are masked to -inf, so their
+    // probabilities are exactly 0 and their (finite) V rows add nothing.
     struct Stage {
-        floatx4 k[PER_T][2], v[PER_T][2];
+        floatx4 k[PER_T][2], kr[PER_T][2], v[PER_T][2];
     };
     auto load = [&](Stage &st, int kbk, int kbv) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
             const int c = tid + NT * i;
             const int kk = c >> 3, kd = 8 * (c & 7);
-            const int pk = kbk * ATT_KB + kk, pkc = min(pk, a.L - 1);
+            const int pkc = min(kbk * ATT_KB + kk, a.L - 1);
             const float *kp = qkv + (size_t)attn_row(a, s, pkc) * a.ld + kcol + kd;
-            floatx4 k0 = ld4(kp), k1 = ld4(kp + 4);
+            st.k[i][0] = ld4(kp);
+            st.k[i][1] = ld4(kp + 4);
             if constexpr (ROPE) {
-                k0 = rope4_table(k0, a.rope, pkc, kd);
-                k1 = rope4_table(k1, a.rope, pkc, kd + 4);
+                st.kr[i][0] = ld4(a.rope + pkc * ATT_DH + kd);
+                st.kr[i][1] = ld4(a.rope + pkc * ATT_DH + kd + 4);
             }
-            const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
-            st.k[i][0] = pk < a.L ? k0 : zero;
-            st.k[i][1] = pk < a.L ? k1 : zero;
             const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const int pv = kbv * ATT_KB + vk + e;
-                const floatx4 v = ld4(qkv + (size_t)attn_row(a, s, min(pv, a.L - 1)) * a.ld + vcol + vd);
-                st.v[i][e] = pv < a.L ? v : zero;
+                const int pvc = min(kbv * ATT_KB + vk + e, a.L - 1);
+                st.v[i][e] = ld4(qkv + (size_t)attn_row(a, s, pvc) * a.ld + vcol + vd);
             }
         }
     };
-    // split a stage's K into Ks[kbuf] and its V (transposed) into Vt[vbuf]
-    auto store = [&](const Stage &st, int kbuf, int vbuf, bool with_v) {
+    // rotate and split: K block kbk into Ks[kbk%2], and (with_v) V block kbv
+    // transposed into Vt[kbv%2]
+    auto store = [&](const Stage &st, int kbk, int kbv, bool with_v) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
             const int c = tid + NT * i;
+            floatx4 k0 = st.k[i][0], k1 = st.k[i][1];
+            if constexpr (ROPE) {
+                k0 = rope_pairs(k0, st.kr[i][0]);
+                k1 = rope_pairs(k1, st.kr[i][1]);
+            }
             bf16x8 p[3];
-            split8(st.k[i][0], st.k[i][1], p[0], p[1], p[2]);
+            split8(k0, k1, p[0], p[1], p[2]);
 #pragma unroll
-            for (int k = 0; k < 3; k++) *reinterpret_cast<bf16x8 *>(&Ks[kbuf][k][c >> 3][8 * (c & 7)]) = p[k];
+            for (int k = 0; k < 3; k++) *reinterpret_cast<bf16x8 *>(&Ks[kbk & 1][k][c >> 3][8 * (c & 7)]) = p[k];
             if (with_v) {
-                // p[k] = pieces of (key vk: dims vd..vd+3, key vk+1: dims vd..vd+3)
-                split8(st.v[i][0], st.v[i][1], p[0], p[1], p[2]);
+                // the two keys' values interleaved, so dword e of each piece is
+                // the (key vk, key vk+1) pair of dim vd+e: one 32-bit write each
+                const floatx4 &v0 = st.v[i][0], &v1 = st.v[i][1];
+                split8(floatx4{v0[0], v1[0], v0[1], v1[1]}, floatx4{v0[2], v1[2], v0[3], v1[3]}, p[0], p[1], p[2]);
                 const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
                 const int pos = (vk & 16) | split_k_slot(vk & 15);  // even: the pair stays adjacent
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-                for (int k = 0; k < 3; k++)
+                for (int k = 0; k < 3; k++) {
+                    const u32x4 w = __builtin_bit_cast(u32x4, p[k]);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-                        *reinterpret_cast<bf16x2_t *>(&Vt[vbuf][k][vd + e][pos]) = bf16x2_t{p[k][e], p[k][4 + e]};
-                    }
+                    for (int e = 0; e < 4; e++) *reinterpret_cast<uint32_t *>(&Vt[kbv & 1][k][vd + e][pos]) = w[e];
+                }
             }
         }
     };
-    // S^T block of 32 keys x 32 queries from Ks[kbuf]
+    // S^T block of 32 keys x 32 queries from Ks[kbuf]; each 16-dim group's
+    // K pieces are read while the previous group's products run
     auto qk = [&](int kbuf) {
         floatx16 sc;
 #pragma unroll
         for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+        bf16x8 kp[2][3];
+        auto read = [&](int g, bf16x8 (&k)[3]) {
+#pragma unroll
+            for (int p = 0; p < 3; p++) k[p] = *reinterpret_cast<const bf16x8 *>(&Ks[kbuf][p][li][16 * g + 8 * lh]);
+        };
+        read(0, kp[0]);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&Ks[kbuf][0][li][16 * g + 8 * lh]);
-            const bf16x8 km = *reinterpret_cast<const bf16x8 *>(&Ks[kbuf][1][li][16 * g + 8 * lh]);
-            const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&Ks[kbuf][2][li][16 * g + 8 * lh]);
+            if (g < 3) read(g + 1, kp[(g + 1) & 1]);
+            const bf16x8 &kh = kp[g & 1][0], &km = kp[g & 1][1], &kl = kp[g & 1][2];
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[g], sc, 0, 0, 0);
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[g], sc, 0, 0, 0);
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(km, qm[g], sc, 0, 0, 0);
@@ -185,43 +200,54 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
             ls += sc[r];
         }
         l_run += ls;
+        // the lane's probabilities of keys 16st + {4lh..4lh+3, 8+4lh..8+4lh+3}
+        // (registers 8st..8st+7) as pieces; V^T pieces for (st, t) read one
+        // step ahead of their products
+        bf16x8 pp[2][3];
 #pragma unroll
-        for (int st = 0; st < 2; st++) {
-            bf16x8 ph, pm, pl;
+        for (int st = 0; st < 2; st++)
             split8(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
-                   floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, ph, pm, pl);
+                   floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, pp[st][0], pp[st][1],
+                   pp[st][2]);
+        bf16x8 vp[2][3];
+        auto read = [&](int step, bf16x8 (&v)[3]) {
+            const int st = step >> 1, t = step & 1;
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                bf16x8 v[3];
+            for (int k = 0; k < 3; k++)
+                v[k] = *reinterpret_cast<const bf16x8 *>(&Vt[vbuf][k][32 * t + li][16 * st + 8 * lh]);
+        };
+        read(0, vp[0]);
 #pragma unroll
-                for (int k = 0; k < 3; k++)
-                    v[k] = *reinterpret_cast<const bf16x8 *>(&Vt[vbuf][k][32 * t + li][16 * st + 8 * lh]);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[2], ph, o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pl, o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], pm, o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], ph, o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pm, o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], ph, o[t], 0, 0, 0);
-            }
+        for (int step = 0; step < 4; step++) {
+            if (step < 3) read(step + 1, vp[(step + 1) & 1]);
+            const int st = step >> 1, t = step & 1;
+            const bf16x8(&v)[3] = vp[step & 1];
+            const bf16x8 &ph = pp[st][0], &pm = pp[st][1], &pl = pp[st][2];
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[2], ph, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pl, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], pm, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[1], ph, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], pm, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v[0], ph, o[t], 0, 0, 0);
         }
     };
 
     // Pipeline over key blocks kb = 0 .. nkb-1.  Entering iteration kb:
-    // Ks[(kb+1)%2] holds K(kb+1), Vt[kb%2] holds V(kb), the registers of
-    // stage `cur` hold K(kb+2) and V(kb+1), and S holds block kb's scores
-    // with its maximum applied.  The iteration loads K(kb+3), V(kb+2) into
-    // stage `nxt`, computes block kb+1's scores (their MFMAs run beside
-    // block kb's exponentials), accumulates block kb's P V, stages `cur`
-    // into Ks[kb%2] and Vt[(kb+1)%2] (read last in iteration kb-1), and
-    // after the barrier applies block kb+1's maximum.  Blocks past the last
-    // are computed from staged zeros and never used.
+    // Ks[(kb+1)%2] holds K(kb+1), Vt[kb%2] holds V(kb), the stage registers
+    // hold the loads of K(kb+2) and V(kb+1), and S holds block kb's scores
+    // with its maximum applied.  The iteration computes block kb+1's scores
+    // (their MFMAs run beside block kb's exponentials), accumulates block
+    // kb's P V, stages K(kb+2) into Ks[kb%2] and V(kb+1) into Vt[(kb+1)%2]
+    // (read last in iteration kb-1), issues the loads of K(kb+3) and
+    // V(kb+2), and after the barrier applies block kb+1's maximum.  Blocks
+    // past the last are computed from staged zeros and never used.
     const int nkb = (a.L + ATT_KB - 1) / ATT_KB;
-    Stage sa, sb;
-    load(sa, 0, 0);
-    store(sa, 0, 0, true);
-    load(sb, 1, 1);
-    store(sb, 1, 0, false);
-    load(sa, 2, 1);
+    Stage st;
+    load(st, 0, 0);
+    store(st, 0, 0, true);
+    load(st, 1, 1);
+    store(st, 1, 0, false);
+    load(st, 2, 1);
     __syncthreads();
     auto run = [&](auto active_c) {
         constexpr bool ACTIVE = decltype(active_c)::value;
@@ -231,21 +257,21 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
             soft_max(s0, 0);
         }
         __syncthreads();  // every wave has read K(0): iteration 0 restages Ks[0]
-        auto iteration = [&](int kb, Stage &cur, Stage &nxt, floatx16 &sc, floatx16 &sn) {
-            load(nxt, kb + 3, kb + 2);
+        auto iteration = [&](int kb, floatx16 &sc, floatx16 &sn) {
             if constexpr (ACTIVE) {
                 sn = qk((kb + 1) & 1);
                 soft_pv(sc, kb & 1);
             }
-            store(cur, kb & 1, (kb + 1) & 1, true);
+            store(st, kb + 2, kb + 1, true);
+            load(st, kb + 3, kb + 2);
             __syncthreads();
             if constexpr (ACTIVE) {
                 if (kb + 1 < nkb) soft_max(sn, kb + 1);
             }
         };
         for (int kb = 0; kb < nkb; kb += 2) {
-            iteration(kb, sa, sb, s0, s1);
-            if (kb + 1 < nkb) iteration(kb + 1, sb, sa, s1, s0);
+            iteration(kb, s0, s1);
+            if (kb + 1 < nkb) iteration(kb + 1, s1, s0);
         }
     };
     if (q0 < a.L) run(std::true_type());

@@ -266,15 +266,10 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_batched_kernel(Ge
 // LDS read after an LDS DMA as dependent on all of them (vmcnt(0)), which
 // would serialise the ring.  The asm sets m0 (the LDS base of the DMA) right
 // before each load; these kernels make no other use of m0 (checked on the
-// built library by the boundary tests).
-VH_DEVICE void lds_dma16(const void *gaddr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gaddr), "s"(lds_base) : "memory");
-}
-
-// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
-// byte offset (the instruction's saddr form): one VGPR per load stream
-// instead of a 64-bit address pair, and no per-lane address arithmetic when
-// the base advances.
+// built library by the boundary tests).  The load takes its address as a
+// wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane byte offset (the
+// instruction's saddr form): one VGPR per load stream instead of a 64-bit
+// address pair, and no per-lane address arithmetic when the base advances.
 VH_DEVICE void lds_dma16s(uint32_t voffset, const void *sbase, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voffset), "s"(sbase), "s"(lds_base)
                  : "memory");
@@ -306,35 +301,35 @@ __device__ __forceinline__ void gemm_bf16_dma_body(const GemmDescBF16 &d, int ti
     const int n0 = (in_group / group_rows) * BN;
 
     const int tid = (int)threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves of 64 x 64
     const int li = lane & 31, lh = lane >> 5;
-    const bf16 *A = static_cast<const bf16 *>(d.A);
     const uint32_t ring_base = (uint32_t)(uintptr_t)ring;
     auto swz = [](int r) { return (r >> 2) & 3; };
 
+    // load sources: the tile's first row (wave-uniform base) plus a 32-bit
+    // lane byte offset (below 2^32: at most 256 rows of lda, ldb <= 2^21)
     const int dr = lane >> 2, dp = lane & 3;
-    const bf16 *a_src[NA];
+    const bf16 *a_base = static_cast<const bf16 *>(d.A) + (size_t)m0 * d.lda;
+    const bf16 *b_base = d.B + (size_t)n0 * d.ldb;
+    uint32_t a_voff[NA], b_voff[NB];
 #pragma unroll
     for (int j = 0; j < NA; j++) {
         const int r = 16 * (NA * wave + j) + dr;
-        a_src[j] = A + (size_t)min(m0 + r, d.M - 1) * d.lda + 8 * (dp ^ swz(r));
+        a_voff[j] = (uint32_t)(min(m0 + r, d.M - 1) - m0) * (uint32_t)d.lda * 2u + 16u * (dp ^ swz(r));
     }
-    const bf16 *b_src[NB];
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const int r = 16 * (NB * wave + j) + dr;
-        b_src[j] = d.B + (size_t)min(n0 + r, d.N - 1) * d.ldb + 8 * (dp ^ swz(r));
+        b_voff[j] = (uint32_t)(min(n0 + r, d.N - 1) - n0) * (uint32_t)d.ldb * 2u + 16u * (dp ^ swz(r));
     }
     auto issue = [&](int kt) {
         const uint32_t sb = ring_base + (kt % STAGES) * STAGE_BYTES;
         const int k0 = kt * BK;
 #pragma unroll
-        for (int j = 0; j < NA; j++)
-            lds_dma16(a_src[j] + k0, __builtin_amdgcn_readfirstlane(sb + (NA * wave + j) * 1024));
+        for (int j = 0; j < NA; j++) lds_dma16s(a_voff[j], a_base + k0, sb + (NA * wave + j) * 1024);
 #pragma unroll
-        for (int j = 0; j < NB; j++)
-            lds_dma16(b_src[j] + k0, __builtin_amdgcn_readfirstlane(sb + A_BYTES + (NB * wave + j) * 1024));
+        for (int j = 0; j < NB; j++) lds_dma16s(b_voff[j], b_base + k0, sb + A_BYTES + (NB * wave + j) * 1024);
     };
 
     floatx16 acc[2][2];
