@@ -24,7 +24,10 @@
 
 namespace vh {
 
-template <int WAVES, typename TO, bool ROPE>
+// OFF32: every row of qkv lies below 4 GB and a position step of the sequence
+// is below 16 MB (the launcher checks), so the staging addresses are one
+// 24-bit multiply-add from a per-lane byte offset and the SGPR base.
+template <int WAVES, typename TO, bool ROPE, bool OFF32>
 __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs a) {
     constexpr int NT = 64 * WAVES;
     constexpr int CHUNKS = ATT_KB * ATT_DH / 8;  // 8-element chunks per K (or V) tile: 256
@@ -81,25 +84,33 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
     struct Stage {
         floatx4 k[PER_T][2], kr[PER_T][2], v[PER_T][2];
     };
+    const char *qkv_b = reinterpret_cast<const char *>(qkv);
+    const uint32_t row_s_bytes = (uint32_t)attn_row(a, s, 0) * (uint32_t)a.ld * 4u;  // used when OFF32
+    const uint32_t pos_bytes = (uint32_t)a.pos_stride * (uint32_t)a.ld * 4u;
+    auto row_ptr = [&](int p, int col) -> const float * {
+        if constexpr (OFF32)
+            return reinterpret_cast<const float *>(qkv_b + (__umul24((uint32_t)p, pos_bytes) + row_s_bytes + 4u * col));
+        else
+            return qkv + (size_t)attn_row(a, s, p) * a.ld + col;
+    };
     auto load = [&](Stage &st, int kbk, int kbv) {
 #pragma unroll
         for (int i = 0; i < PER_T; i++) {
             const int c = tid + NT * i;
             const int kk = c >> 3, kd = 8 * (c & 7);
             const int pkc = min(kbk * ATT_KB + kk, a.L - 1);
-            const float *kp = qkv + (size_t)attn_row(a, s, pkc) * a.ld + kcol + kd;
+            const float *kp = row_ptr(pkc, kcol + kd);
             st.k[i][0] = ld4(kp);
             st.k[i][1] = ld4(kp + 4);
             if constexpr (ROPE) {
-                st.kr[i][0] = ld4(a.rope + pkc * ATT_DH + kd);
-                st.kr[i][1] = ld4(a.rope + pkc * ATT_DH + kd + 4);
+                const float *tp = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.rope) +
+                                                                  (__umul24((uint32_t)pkc, 4u * ATT_DH) + 4u * kd));
+                st.kr[i][0] = ld4(tp);
+                st.kr[i][1] = ld4(tp + 4);
             }
             const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int pvc = min(kbv * ATT_KB + vk + e, a.L - 1);
-                st.v[i][e] = ld4(qkv + (size_t)attn_row(a, s, pvc) * a.ld + vcol + vd);
-            }
+            for (int e = 0; e < 2; e++) st.v[i][e] = ld4(row_ptr(min(kbv * ATT_KB + vk + e, a.L - 1), vcol + vd));
         }
     };
     // rotate and split: K block kbk into Ks[kbk%2], and (with_v) V block kbv

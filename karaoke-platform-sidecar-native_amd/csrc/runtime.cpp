@@ -474,12 +474,25 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
     const dim3 block(64 * WAVES);
     if constexpr (WAVES == 4) {
         if (split) {
+            // 32-bit staging offsets when the last row's end lies below 4 GB
+            // and one position step below 16 MB (positive strides)
+            const int64_t last_row = (int64_t)((a.S - 1) / a.group) * a.group_stride +
+                                     (int64_t)(std::min(a.S, a.group) - 1) * a.seq_stride +
+                                     (int64_t)(a.L - 1) * a.pos_stride;
+            const bool off32 = a.group_stride >= 0 && a.seq_stride >= 0 && a.pos_stride >= 0 &&
+                               (last_row + 1) * a.ld * 4 <= (int64_t)UINT32_MAX &&
+                               (int64_t)a.pos_stride * a.ld * 4 < (1 << 24);
+            auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, dim3(grid), block, 0, s, a); };
             if (a.rope) {
-                if (out_bf16) hipLaunchKernelGGL((attention_split_kernel<WAVES, bf16, true>), dim3(grid), block, 0, s, a);
-                else hipLaunchKernelGGL((attention_split_kernel<WAVES, float, true>), dim3(grid), block, 0, s, a);
+                if (out_bf16) off32 ? go(attention_split_kernel<WAVES, bf16, true, true>)
+                                    : go(attention_split_kernel<WAVES, bf16, true, false>);
+                else off32 ? go(attention_split_kernel<WAVES, float, true, true>)
+                           : go(attention_split_kernel<WAVES, float, true, false>);
             } else {
-                if (out_bf16) hipLaunchKernelGGL((attention_split_kernel<WAVES, bf16, false>), dim3(grid), block, 0, s, a);
-                else hipLaunchKernelGGL((attention_split_kernel<WAVES, float, false>), dim3(grid), block, 0, s, a);
+                if (out_bf16) off32 ? go(attention_split_kernel<WAVES, bf16, false, true>)
+                                    : go(attention_split_kernel<WAVES, bf16, false, false>);
+                else off32 ? go(attention_split_kernel<WAVES, float, false, true>)
+                           : go(attention_split_kernel<WAVES, float, false, false>);
             }
             return;
         }
