@@ -224,3 +224,25 @@ def test_attention_split(ctx, rng, S, L):
     # noisier statistic and gets a looser factor
     assert np.sqrt(np.mean(e_split ** 2)) <= 1.25 * np.sqrt(np.mean(e_fp32 ** 2)) + 1e-9
     assert e_split.max() <= 2.0 * e_fp32.max() + 1e-8
+
+
+def test_attention_split_beyond_4gb(ctx):
+    """qkv larger than 4 GB takes the kernel's 64-bit staging addresses: its
+    outputs equal, bit for bit, those of the 32-bit-offset kernel on the same
+    sequences copied into a small buffer (first and last sequences)."""
+    import torch
+    S, L, H = 875, 801, 8  # 700875 rows x 6 KB = 4.31 GB > 2^32 bytes
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(7)
+    qkv = torch.randn(S * L, 3 * H * 64, device="cuda:0", generator=g)
+    assert qkv.numel() * 4 > 2 ** 32
+    out = torch.empty(S * L, H * 64, device="cuda:0")
+    ctx.attention(qkv, out, S, L, H, rotary=True, split=True)
+    for first in (0, S - 2):
+        small = qkv[first * L:(first + 2) * L].clone()
+        ref = torch.empty(2 * L, H * 64, device="cuda:0")
+        ctx.attention(small, ref, 2, L, H, rotary=True, split=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out[first * L:(first + 2) * L], ref), f"sequences {first}, {first + 1}"
+    del qkv, out
+    torch.cuda.empty_cache()
