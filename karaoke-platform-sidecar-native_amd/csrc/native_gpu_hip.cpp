@@ -461,6 +461,8 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
               gpu->tables.ensure(sizeof(MaskTable), "hipMalloc(mask table)");
     if (!ok) return gpu->fail("mask buffers");
     std::vector<GemmArgs> g1, g2;
+    std::vector<GemmArgsSplit> s1, s2;  // the same products on the split GEMM
+    bool sp = true;
     MaskTable tab;
     memset(&tab, 0, sizeof(tab));
     int64_t off = 0;
@@ -475,6 +477,11 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
         float *hid = gpu->hidden.f() + (size_t)b * M * Hm;
         g1.push_back({gpu->normed.f() + (size_t)b * D, B * D, w1, D, b1, hid, Hm, M, Hm, D});
         g2.push_back({hid, Hm, w2, Hm, b2, gpu->proj.f() + off, 2 * dim, M, 2 * dim, Hm});
+        const void *w1s = sp ? gpu->split(w1, D, Hm) : nullptr;
+        const void *w2s = sp ? gpu->split(w2, Hm, 2 * dim) : nullptr;
+        sp = sp && w1s && w2s;
+        s1.push_back({gpu->normed.f() + (size_t)b * D, B * D, w1s, b1, hid, Hm, M, Hm, D});
+        s2.push_back({hid, Hm, w2s, b2, gpu->proj.f() + off, 2 * dim, M, 2 * dim, Hm});
         tab.first_freq[b] = bands[b].first_frequency;
         tab.dim[b] = dim;
         tab.proj_offset[b] = off;
@@ -482,7 +489,8 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
         maxdim = std::max(maxdim, dim);
     }
     ok = rmsnorm(s, gpu->x.f(), D, gamma, gpu->normed.f(), D, gpu->tokens, D) &&
-         gemm_batched(s, g1, EPI_TANH) && gemm_batched(s, g2, EPI_STORE) &&
+         (sp ? gemm_split_batched(s, s1, EPI_TANH) && gemm_split_batched(s, s2, EPI_STORE)
+             : gemm_batched(s, g1, EPI_TANH) && gemm_batched(s, g2, EPI_STORE)) &&
          check(hipMemcpyAsync(gpu->tables.ptr, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(mask table)");
     if (ok) {
         hipLaunchKernelGGL(mask_glu_scatter_kernel, dim3((unsigned)(((int64_t)M * maxdim + 255) / 256), B), dim3(256), 0,

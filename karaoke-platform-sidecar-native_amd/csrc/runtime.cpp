@@ -331,6 +331,14 @@ static bool gemm_split_ok(const GemmArgsSplit &g, int epilogue) {
     return true;
 }
 
+static GemmDescSplit to_desc_split(const GemmArgsSplit &g) {
+    GemmDescSplit d;
+    d.A = g.A; d.W = static_cast<const bf16 *>(g.W); d.bias = g.bias; d.C = g.C;
+    d.M = (int)g.M; d.N = g.N; d.K = g.K;
+    d.lda = g.lda; d.ldc = g.ldc;
+    return d;
+}
+
 template <int EPI>
 static void launch_split(hipStream_t s, const GemmDescSplit &d, unsigned tiles) {
     hipLaunchKernelGGL(gemm_split_kernel<EPI>, dim3(tiles), dim3(GS_THREADS), 0, s, d);
@@ -341,10 +349,7 @@ bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer
         set_error("gemm_split: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K, g.lda);
         return false;
     }
-    GemmDescSplit d;
-    d.A = g.A; d.W = static_cast<const bf16 *>(g.W); d.bias = g.bias; d.C = g.C;
-    d.M = (int)g.M; d.N = g.N; d.K = g.K;
-    d.lda = g.lda; d.ldc = g.ldc;
+    const GemmDescSplit d = to_desc_split(g);
     const unsigned tiles = (unsigned)(((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
     Scope sc(t, s, name);
     switch (epilogue) {
@@ -356,6 +361,43 @@ bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer
         default: set_error("unknown GEMM epilogue %d", epilogue); return false;
     }
     return sync_debug(s, "gemm_split_kernel");
+}
+
+template <int EPI>
+static void launch_split_batched(hipStream_t s, const GemmBatchSplit &b, unsigned tiles, unsigned n) {
+    hipLaunchKernelGGL(gemm_split_batched_kernel<EPI>, dim3(tiles, 1, n), dim3(GS_THREADS), 0, s, b);
+}
+
+bool gemm_split_batched(hipStream_t s, const std::vector<GemmArgsSplit> &gs, int epilogue, KernelTimer *t,
+                        const char *name) {
+    Scope sc(t, s, name);
+    for (size_t first = 0; first < gs.size(); first += GS_MAX_BATCH) {
+        const size_t count = std::min(gs.size() - first, (size_t)GS_MAX_BATCH);
+        GemmBatchSplit b;
+        memset(&b, 0, sizeof(b));
+        int64_t max_tiles = 0;
+        for (size_t i = 0; i < count; i++) {
+            const GemmArgsSplit &g = gs[first + i];
+            if (!gemm_split_ok(g, epilogue)) {
+                set_error("gemm_split_batched: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K,
+                          g.lda);
+                return false;
+            }
+            b.d[i] = to_desc_split(g);
+            max_tiles = std::max(max_tiles, ((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
+        }
+        const unsigned tiles = (unsigned)max_tiles, n = (unsigned)count;
+        switch (epilogue) {
+            case EPI_STORE: launch_split_batched<EPI_STORE>(s, b, tiles, n); break;
+            case EPI_GELU: launch_split_batched<EPI_GELU>(s, b, tiles, n); break;
+            case EPI_TANH: launch_split_batched<EPI_TANH>(s, b, tiles, n); break;
+            case EPI_RESIDUAL: launch_split_batched<EPI_RESIDUAL>(s, b, tiles, n); break;
+            case EPI_GEGLU: launch_split_batched<EPI_GEGLU>(s, b, tiles, n); break;
+            default: set_error("unknown GEMM epilogue %d", epilogue); return false;
+        }
+        if (!sync_debug(s, "gemm_split_batched_kernel")) return false;
+    }
+    return true;
 }
 
 bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces) {

@@ -117,6 +117,9 @@ struct GemmArgsSplit {
 };
 bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer *t = nullptr,
                 const char *name = "gemm_split");
+// A ragged batch of split GEMMs (one launch per 64 problems).
+bool gemm_split_batched(hipStream_t s, const std::vector<GemmArgsSplit> &gs, int epilogue, KernelTimer *t = nullptr,
+                        const char *name = "gemm_split");
 // K granularity of gemm_split, and the bytes of W's pieces (N rounded up to
 // a multiple of 128).
 constexpr int SPLIT_K_MULTIPLE = 16;

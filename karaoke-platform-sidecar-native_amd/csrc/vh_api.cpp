@@ -47,8 +47,9 @@ struct vh_model {
     // bf16 copies of every matrix (built on the first switch to bf16)
     int precision = PREC_FP32;
     DeviceBuffer weights_h;
-    // split planes of the transformer matrices (built at load)
+    // split planes of the transformer and mask-estimator matrices (built at load)
     DeviceBuffer weights_s;
+    std::vector<void *> mask_w1_s, mask_w2_s;
     std::vector<void *> band_w_h, mask_w1_h, mask_w2_h;
     // DSP constants
     DeviceBuffer window, twiddle;
@@ -400,16 +401,20 @@ bool prepare_bf16(vh_model *m) {
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(bf16 weights)");
 }
 
-// Split planes (three bf16 pieces) of the transformer matrices whose K is a
-// multiple of 16: the fp32 path's linears on bf16 matrix cores.
+// Split planes (three bf16 pieces) of the transformer and mask-estimator
+// matrices whose K is a multiple of 16: the fp32 path's linears on bf16
+// matrix cores.
 bool prepare_split(vh_model *m) {
     if (m->weights_s.ptr) return true;
     const Dims &d = m->d;
     hipStream_t s = m->ctx->stream;
-    const int D = d.dim;
+    const int D = d.dim, Hm = d.mask_hidden;
     auto bytes = [](int N, int K) { return K % SPLIT_K_MULTIPLE ? 0 : (split_bytes(N, K) + 255) & ~(size_t)255; };
     const size_t per_layer = bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) + bytes(D, d.ff_dim);
-    const size_t total = per_layer * m->layers.size();
+    size_t total = per_layer * m->layers.size();
+    for (int b = 0; b < d.bands; b++) total += bytes(Hm, D) + bytes(2 * d.in_dim(b), Hm);
+    m->mask_w1_s.assign(d.bands, nullptr);
+    m->mask_w2_s.assign(d.bands, nullptr);
     if (total == 0) return true;
     if (!m->weights_s.ensure(total, "hipMalloc(split weights)")) return false;
     char *cur = static_cast<char *>(m->weights_s.ptr);
@@ -424,6 +429,9 @@ bool prepare_split(vh_model *m) {
             !split(w.w1, d.ff1_out(), D, &w.w1_s) || !split(w.w2, D, d.ff_dim, &w.w2_s))
             return false;
     }
+    for (int b = 0; b < d.bands; b++)
+        if (!split(m->mask_w1[b], Hm, D, &m->mask_w1_s[b]) || !split(m->mask_w2[b], 2 * d.in_dim(b), Hm, &m->mask_w2_s[b]))
+            return false;
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(split weights)");
 }
 
@@ -517,6 +525,10 @@ bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, i
         return false;
     std::vector<GemmArgs> g1, g2;
     std::vector<GemmArgsBF16> h1, h2;
+    std::vector<GemmArgsSplit> s1, s2;
+    // fp32 path: both layers on the split GEMM when every band's pieces exist
+    bool sp = m->precision == PREC_FP32 && !normed_bf16;
+    for (int b = 0; b < B && sp; b++) sp = m->mask_w1_s.size() == (size_t)B && m->mask_w1_s[b] && m->mask_w2_s[b];
     MaskTable tab;
     memset(&tab, 0, sizeof(tab));
     int64_t off = 0;
@@ -533,6 +545,11 @@ bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, i
             c.a_bf16 = true;
             h1.push_back(a);
             h2.push_back(c);
+        } else if (sp) {
+            s1.push_back({reinterpret_cast<const float *>(feat), B * D, m->mask_w1_s[b], m->mask_b1[b],
+                          reinterpret_cast<float *>(hid), Hm, M, Hm, D});
+            s2.push_back({reinterpret_cast<const float *>(hid), Hm, m->mask_w2_s[b], m->mask_b2[b], proj, out, M, out,
+                          Hm});
         } else {
             g1.push_back({reinterpret_cast<const float *>(feat), B * D, m->mask_w1[b], D, m->mask_b1[b],
                           reinterpret_cast<float *>(hid), Hm, M, Hm, D});
@@ -547,6 +564,9 @@ bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, i
     KernelTimer *t = &m->ctx->timer;
     if (h) {
         if (!gemm_bf16_batched(s, h1, EPI_TANH, t, "gemm_mask1") || !gemm_bf16_batched(s, h2, EPI_STORE, t, "gemm_mask2"))
+            return false;
+    } else if (sp) {
+        if (!gemm_split_batched(s, s1, EPI_TANH, t, "gemm_mask1") || !gemm_split_batched(s, s2, EPI_STORE, t, "gemm_mask2"))
             return false;
     } else if (!gemm_batched(s, g1, EPI_TANH, t, "gemm_mask1") || !gemm_batched(s, g2, EPI_STORE, t, "gemm_mask2")) {
         return false;

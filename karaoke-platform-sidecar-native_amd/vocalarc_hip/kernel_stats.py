@@ -22,12 +22,14 @@ ROLES = [
     (r"gemm_split_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via split bf16)"),
+    (r"gemm_split_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32 via split bf16)"),
+    (r"gemm_split_batched_kernel(<|ILi)0", "mask estimator layer 2, batched over bands (fp32 via split bf16)"),
     (r"split_weight_kernel", "weight split into bf16 pieces (model load)"),
     (r"gemm_f32_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32)"),
     (r"gemm_f32_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32)"),
     (r"gemm_f32_kernel(<|ILi)0", "fused QKV + gate projection (fp32)"),
     (r"gemm_f32_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32)"),
-    (r"gemm_f32_batched_kernel(<|ILi)0", "band split / mask estimator layer 2, batched over bands (fp32)"),
+    (r"gemm_f32_batched_kernel(<|ILi)0", "band split (and mask layer 2 off the split path), batched over bands (fp32)"),
     (r"gemm_bf16_(dma_)?kernel(<|ILi)4", "FFN up-projection + GELU-GLU (bf16 variant)"),
     (r"gemm_bf16_(dma_)?kernel(<|ILi)3", "out / FFN down-projection + residual (bf16 variant)"),
     (r"gemm_bf16_(dma_)?kernel(<|ILi)0", "fused QKV + gate projection (bf16 variant)"),
