@@ -308,9 +308,13 @@ __global__ __launch_bounds__(256, 4) void attention_short_kernel(AttnArgs a) {
         if (a.gate_col >= 0) gpre = qkv[qrow + a.gate_col + h];
     };
 
-    int task = (int)blockIdx.x;
-    if (task < tasks) prefetch(task);
-    for (; task < tasks; task += (int)gridDim.x) {
+    // a contiguous run of tasks per workgroup: the heads of one sequence in
+    // turn, so the block reads its rows' q/k/v slices back to back
+    const int per = (tasks + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int t_end = min(tasks, ((int)blockIdx.x + 1) * per);
+    int task = (int)blockIdx.x * per;
+    if (task < t_end) prefetch(task);
+    for (; task < t_end; task++) {
         const int h = task % a.H, s = task / a.H;
         // this task's keys into LDS (K rotated), its queries into registers
 #pragma unroll
@@ -327,7 +331,7 @@ __global__ __launch_bounds__(256, 4) void attention_short_kernel(AttnArgs a) {
         }
         const float gate_logit = gpre;
         __syncthreads();
-        if (task + (int)gridDim.x < tasks) prefetch(task + (int)gridDim.x);
+        if (task + 1 < t_end) prefetch(task + 1);
 
         floatx4 sc[4];
 #pragma unroll
