@@ -191,7 +191,12 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs
         float mb = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        {
+            // the other half-wave's maximum (lanes l and l^32 hold one query):
+            // one v_permlane32_swap instead of an LDS permute round trip
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
+            mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
         const bool grow = mb > m_run + 8.0f;
         if (__ballot(grow)) {
             const float m_new = grow ? mb : m_run;
