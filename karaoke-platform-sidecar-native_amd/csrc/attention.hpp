@@ -316,11 +316,13 @@ __global__ __launch_bounds__(256, 4) void attention_short_kernel(AttnArgs a) {
     if (task < t_end) prefetch(task);
     for (; task < t_end; task++) {
         const int h = task % a.H, s = task / a.H;
-        // this task's keys into LDS (K rotated), its queries into registers
+        // this task's keys into LDS (K rotated), its queries into registers;
+        // keys past L are zeros, rotated with the table's last row (the table
+        // has L rows)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int key = (tid >> 4) + 16 * i;
-            st4(&Ks[key][d_st], rope4(kpre[i], a.rope, key, d_st));
+            st4(&Ks[key][d_st], rope4(kpre[i], a.rope, min(key, a.L - 1), d_st));
             st4(&Vs[key][d_st], vpre[i]);
         }
         floatx4 qr[4];
