@@ -100,6 +100,34 @@ size_t vh_split_bytes(int N, int K);
    where within every group of 16 k the (slot s, element e) order is
    k 0-3, 8-11 (s = 0), 4-7, 12-15 (s = 1); rows past N are zero. */
 int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Ws);
+/* vh_gemm in fp32 accuracy on fp16 matrix cores: A and W are scaled by
+   powers of two (A's from a_bound, which every |A| element must respect;
+   a_bound <= 0 computes max|A| on the device first; W's from its maximum)
+   and every scaled value is split into two fp16 pieces (h = fp16(y),
+   m = fp16(y - h)); the products hh, hm, mh are accumulated in fp32 and the
+   result scaled back.  Wp: the weight's pieces from vh_split_weights_h2.
+   K a multiple of 16, lda a multiple of 4 and at most 2^21, A 16-byte
+   aligned.  The token-wise linear of native/vocalarc_separation.c:631-636,
+   as vh_gemm; the default fp32 path's linears. */
+int vh_gemm_h2(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, float a_bound, const void *Wp,
+               const float *bias, float *C, int ldc, int epilogue);
+/* Bytes of the fp16 pieces of an N x K weight: a 256-byte header, then two
+   planes (N rounded up to 128 rows). */
+size_t vh_h2_bytes(int N, int K);
+/* fp32 W[N][ldw_in] (K a multiple of 16) -> max|W| in the header (float 0)
+   and the fp16 pieces of W * 2^e (e: the largest with max|W| * 2^e < 2^14),
+   tile-major as vh_split_weights with two planes: piece p (h, m) of W[n][k]
+   at fp16 index 128 + ((n/128 * K/16 + k/16) * 2 + p) * 2048 + (n%128) * 16
+   + 8 * (s ^ (n/8)%2) + e.  Wp 256-byte aligned, vh_h2_bytes(N, K) bytes. */
+int vh_split_weights_h2(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Wp);
+/* Bounds the model gives vh_gemm_h2 for A operands downstream of an RMSNorm
+   with device gain gamma[D] (|y_i| <= ||y||_2 <= sqrt(D) max|gamma|):
+   out[0] = sqrt(D) max|gamma| (1 + 2^-10); with W [N][D] (and bias b, may be
+   null) out[1] = t, or t^2 when square (a GELU-GLU of two outputs), where
+   t = (out[0] max_n ||W_n||_2 + max_n |b_n|)(1 + 2^-10) bounds every output
+   of W y + b; 0 without W.  out: 2 device floats. */
+int vh_operand_bounds(vh_context *ctx, const float *gamma, int D, const float *W, int N, const float *b, int square,
+                      float *out);
 /* fp32 src[rows][cols] -> bf16 dst[rows][ld] (round to nearest even). */
 int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld);
 /* Fused attention core over qkv[S*L][3*H*64] (rotary applied here):
@@ -124,9 +152,10 @@ void vh_model_free(vh_model *model);
 /* Arithmetic of the model's matrix products (every linear of the transformer
    stack, band split and mask estimator):
    VH_PRECISION_FP32 (default, the parity path): fp32 accuracy.  The
-     transformer linears run on bf16 matrix cores by exact operand splitting
-     (vh_gemm_split; split planes made at load), every other product on the
-     fp32 MFMA instruction.
+     transformer and mask-estimator linears run on fp16 matrix cores by
+     two-piece operand splitting (vh_gemm_h2; pieces and operand bounds made
+     at load), the time-axis attention on bf16 matrix cores by three-piece
+     splitting, every other product on the fp32 MFMA instruction.
    VH_PRECISION_FP32_MFMA: every product on the fp32 MFMA instruction.
    VH_PRECISION_BF16: activations rounded to bf16 as they enter the matrix
      cores, bf16 weight copies made on the first switch, fp32 accumulation,

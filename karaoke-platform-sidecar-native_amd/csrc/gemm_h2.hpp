@@ -1,0 +1,336 @@
+// fp32 token-wise linear on fp16 matrix cores by two-piece operand splitting:
+// C[M][N] (op)= A[M][K] * W[N][K]^T with fp32 inputs, fp32 accumulation and
+// the fused epilogues of the fp32 GEMM (gemm.hpp).  The default fp32 path's
+// transformer and mask-estimator linears.
+//
+// Splitting.  Each operand is first scaled by a power of two 2^e (exact), so
+// that everything it can hold lies below 2^14; then every scaled value y is
+// split into two fp16 values (round to nearest even)
+//   h = fp16(y),  m = fp16(y - h)
+// y - h is exact in fp32 (Sterbenz) and |m| <= 2^-11 |y|, so h + m carries 22
+// significant bits; where m is an fp16 subnormal (|y| < 2^-3, i.e. below
+// 2^-17 of the operand's bound) the pair is exact to 2^-25 absolute.  The
+// kernel accumulates the three products hh, hm, mh -- each exact in fp32
+// (11 x 11 bits) -- and drops mm (<= 2^-22 |a||w|) and the pieces' rounding
+// (<= 2^-22 each): per product term about 2^-21 relative, which the fp32
+// accumulation over K (16 terms per MFMA, K/16 x 3 roundings) already
+// exceeds.  Measured against fp64 on the transformer shapes, the result is
+// 1.5-2 dB more accurate than the three-piece bf16 split (gemm_split.hpp,
+// six products) and as accurate as a sequential fp32 FMA chain, at half its
+// matrix-core work.
+//
+// Scales.  W's exponent comes from its absolute maximum, found on the device
+// when the pieces are made and kept in their 256-byte header.  A's comes
+// from a bound the caller supplies -- a value or a device float -- that every
+// |A| element respects; the model derives exact bounds from the producers'
+// weights (operand_bounds_kernel): an RMSNorm output obeys
+// |y_i| <= ||y||_2 <= sqrt(D) max|gamma|, a linear of it obeys
+// |W y + b|_n <= sqrt(D) max|gamma| ||W_n||_2 + |b_n|, an attention output
+// (a convex combination of value rows times a gate in (0, 1)) obeys the
+// value bound, a GELU-GLU output the square of its pre-activation bound
+// (|gelu(g)| <= |g|), a tanh output 1.  The bound only has to hold: a loose
+// one costs precision only for elements more than 2^17 below it.
+//
+// Operands and pipeline as gemm_split.hpp (256x128 block, 8 waves of 32x128,
+// K chunks of 16 in a 2-chunk global->LDS DMA ring, A fp32 in LDS split by
+// each wave in registers): W's pieces are two fp16 planes per tile-major
+// block (8 KB per 128 rows x 16 k, the same row/slot permutation), one 1 KB
+// load per wave per chunk; 48 KB of LDS; per wave and chunk 12 MFMAs
+// (v_mfma_f32_32x32x16_f16) and 4 VALU per A value for the scale and split.
+#pragma once
+
+#include "gemm_split.hpp"
+
+namespace vh {
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
+struct GemmDescH2 {
+    const float *A;  // fp32 [M][lda]
+    const void *W;   // pieces (split_weight_h2_kernel): 256-byte header, then the planes
+    const float *bias;
+    float *C;
+    int M, N, K;
+    int lda, ldc;
+};
+// Bound on |A|: *ptr when ptr is set (a device float), else value.
+struct H2Bound {
+    const float *ptr;
+    float value;
+};
+
+constexpr int H2_HEADER = 256;                // bytes before the planes: float max|W|
+constexpr int H2_WBLOCK = 2 * GS_BN * GS_BK;  // fp16 per (row tile, K chunk) block of W pieces
+
+// The exponent e with bound * 2^e < 2^14 (the largest such, clamped to
+// [-100, 100]); 0 for a zero, infinite or NaN bound.
+VH_HOST_DEVICE inline int h2_exponent(float bound) {
+    if (!(bound > 0.0f) || !(bound <= 3.4e38f)) return 0;
+    int E;
+    (void)frexpf(bound, &E);  // bound < 2^E
+    const int e = 14 - E;
+    return e < -100 ? -100 : (e > 100 ? 100 : e);
+}
+
+// Two fp32 -> two fp16 (nearest even) in one dword: one v_cvt_pk_f16_f32.
+VH_DEVICE uint32_t pack_f16x2(float a, float b) {
+    typedef float floatx2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, halfx2));
+}
+VH_DEVICE float f16_lo(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p & 0xffffu)); }
+VH_DEVICE float f16_hi(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p >> 16)); }
+
+// Eight fp32 values times s -> their h and m fp16 pieces, packed as the MFMA
+// operand wants them (a lane's eight k-values): 4 VALU per value.
+VH_DEVICE void split8_h2(floatx4 lo, floatx4 hi, float s, halfx8 &h, halfx8 &m) {
+    const float x[8] = {lo[0] * s, lo[1] * s, lo[2] * s, lo[3] * s, hi[0] * s, hi[1] * s, hi[2] * s, hi[3] * s};
+    uint32_t ph[4], pm[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        ph[e] = pack_f16x2(x[2 * e], x[2 * e + 1]);
+        pm[e] = pack_f16x2(x[2 * e] - f16_lo(ph[e]), x[2 * e + 1] - f16_hi(ph[e]));
+    }
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    h = __builtin_bit_cast(halfx8, (u32x4){ph[0], ph[1], ph[2], ph[3]});
+    m = __builtin_bit_cast(halfx8, (u32x4){pm[0], pm[1], pm[2], pm[3]});
+}
+
+template <int EPI>
+__device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound, int tile) {
+    constexpr int A_BYTES = GS_BM * GS_BK * 4;  // 16 KB: fp32 rows of 64 B
+    constexpr int P_BYTES = GS_BN * GS_BK * 2;  // 4 KB per W plane: fp16 rows of 32 B
+    constexpr int STAGE_BYTES = A_BYTES + 2 * P_BYTES;
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[2 * STAGE_BYTES];
+
+    const int tiles_n = (d.N + GS_BN - 1) / GS_BN;
+    const int tiles_m = (d.M + GS_BM - 1) / GS_BM;
+    if (tile >= tiles_m * tiles_n) return;
+    // column-fastest order within groups of row tiles (see gemm.hpp)
+    const int gsz = (size_t)d.N * d.K * 4 <= (3u << 20) ? 1 : 8;
+    const int group = tile / (gsz * tiles_n);
+    const int in_group = tile % (gsz * tiles_n);
+    const int group_rows = min(gsz, tiles_m - group * gsz);
+    const int m0 = (group * gsz + in_group % group_rows) * GS_BM;
+    const int n0 = (in_group / group_rows) * GS_BN;
+
+    const int ea = h2_exponent(a_bound);
+    const int ew = h2_exponent(*static_cast<const float *>(d.W));
+    const float a_scale = ldexpf(1.0f, ea), a_unscale = ldexpf(1.0f, -ea), w_unscale = ldexpf(1.0f, -ew);
+
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, lh = lane >> 5;
+    const uint32_t ring_base = (uint32_t)(uintptr_t)ring;
+    auto swz_a = [](int r) { return (r >> 2) & 3; };
+    auto swz_w = [](int r) { return (r >> 3) & 1; };
+
+    // A: 16 loads of 1 KB (16 rows each), wave w loads blocks w and w+8 from
+    // the tile's first row (scalar base) plus its lane offset (below 2^32:
+    // 256 rows of lda <= 2^21 floats).  W: the 8 1 KB blocks of the chunk's
+    // tile-major image, wave w the w-th.
+    const float *a_base = d.A + (size_t)m0 * d.lda;
+    uint32_t a_voff[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int r = 16 * (wave + 8 * j) + (lane >> 2);
+        a_voff[j] = (uint32_t)(min(m0 + r, d.M - 1) - m0) * (uint32_t)d.lda * 4u + 16u * ((lane & 3) ^ swz_a(r));
+    }
+    const _Float16 *w_base = reinterpret_cast<const _Float16 *>(static_cast<const char *>(d.W) + H2_HEADER) +
+                             (size_t)(n0 / GS_BN) * (d.K / GS_BK) * H2_WBLOCK;
+    const uint32_t w_voff = 16 * lane;
+    auto issue = [&](int kt) {
+        const uint32_t sb = ring_base + (kt & 1) * STAGE_BYTES;
+        const float *ab = a_base + kt * GS_BK;
+        lds_dma16s(a_voff[0], ab, sb + wave * 1024);
+        lds_dma16s(a_voff[1], ab, sb + (wave + 8) * 1024);
+        lds_dma16s(w_voff, w_base + (size_t)kt * H2_WBLOCK + wave * 512, sb + A_BYTES + wave * 1024);
+    };
+
+    floatx16 acc[1][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[0][j][r] = 0.0f;
+
+    const int nk = d.K / GS_BK;
+    issue(0);
+    wait_vmcnt<0>();
+    __syncthreads();
+    // NJ live 32-column accumulators, chosen once per tile (as gemm_split_body)
+    auto k_loop = [&](auto nj_c) {
+        constexpr int NJ = decltype(nj_c)::value;
+        for (int kt = 0; kt < nk; kt++) {
+            // chunk kt+1 goes to the slot chunk kt-1 used: every wave finished
+            // reading it before the barrier that ended the previous iteration
+            if (kt + 1 < nk) issue(kt + 1);
+            const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
+            const int r = wave * 32 + li;
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * (lh ^ swz_a(r)));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * ((2 + lh) ^ swz_a(r)));
+            halfx8 ah, am;
+            split8_h2(lo, hi, a_scale, ah, am);
+            // W column tiles two at a time: their pieces, then (m,h) (h,m) (h,h)
+#pragma unroll
+            for (int jp = 0; jp < (NJ + 1) / 2; jp++) {
+                constexpr int NJJ = NJ == 1 ? 1 : 2;
+                halfx8 wh[NJJ], wm[NJJ];
+#pragma unroll
+                for (int jj = 0; jj < NJJ; jj++) {
+                    const int rw = 32 * (2 * jp + jj) + li;
+                    const unsigned char *wp = sbuf + A_BYTES + rw * 32 + 16 * (lh ^ swz_w(rw));
+                    wh[jj] = *reinterpret_cast<const halfx8 *>(wp);
+                    wm[jj] = *reinterpret_cast<const halfx8 *>(wp + P_BYTES);
+                }
+#pragma unroll
+                for (int jj = 0; jj < NJJ; jj++)
+                    acc[0][2 * jp + jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, wh[jj], acc[0][2 * jp + jj], 0, 0, 0);
+#pragma unroll
+                for (int jj = 0; jj < NJJ; jj++)
+                    acc[0][2 * jp + jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wm[jj], acc[0][2 * jp + jj], 0, 0, 0);
+#pragma unroll
+                for (int jj = 0; jj < NJJ; jj++)
+                    acc[0][2 * jp + jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wh[jj], acc[0][2 * jp + jj], 0, 0, 0);
+            }
+            wait_vmcnt<0>();  // chunk kt+1 has landed
+            __syncthreads();
+        }
+    };
+    const int live = d.N - n0;
+    if (live > 64) k_loop(std::integral_constant<int, 4>());
+    else if (live > 32) k_loop(std::integral_constant<int, 2>());
+    else k_loop(std::integral_constant<int, 1>());
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[0][j] = (acc[0][j] * a_unscale) * w_unscale;  // exact: powers of two
+    GemmDescBF16 e{};
+    e.bias = d.bias; e.C = d.C; e.M = d.M; e.N = d.N; e.K = d.K; e.ldc = d.ldc;
+    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(GS_THREADS, 2) void gemm_h2_kernel(GemmDescH2 d, H2Bound b) {
+    gemm_h2_body<EPI>(d, b.ptr ? *b.ptr : b.value, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+}
+
+// Ragged batch (the mask estimator's per-band linears): problem blockIdx.z,
+// one bound for all problems.
+struct GemmBatchH2 {
+    GemmDescH2 d[GS_MAX_BATCH];
+    H2Bound b;
+};
+
+template <int EPI>
+__global__ __launch_bounds__(GS_THREADS, 2) void gemm_h2_batched_kernel(GemmBatchH2 b) {
+    gemm_h2_body<EPI>(b.d[blockIdx.z], b.b.ptr ? *b.b.ptr : b.b.value, (int)blockIdx.x);
+}
+
+// max |W| over W [N][ldw] (first K columns) into out[0]; one workgroup of
+// 1024 threads, no atomics.
+static __global__ __launch_bounds__(1024) void absmax_kernel(const float *__restrict__ W, int N, int K, int ldw,
+                                                            float *__restrict__ out) {
+    __shared__ float red[16];
+    float mx = 0.0f;
+    const int64_t n = (int64_t)N * K;
+    for (int64_t i = threadIdx.x; i < n; i += 1024) mx = fmaxf(mx, fabsf(W[(i / K) * ldw + i % K]));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; w++) mx = fmaxf(mx, red[w]);
+        out[0] = mx;
+    }
+}
+
+// Per-workgroup max |x| over x[n] (grid-stride, 256 threads) into
+// partial[blockIdx.x]; absmax_kernel over the partials finishes the reduction.
+static __global__ __launch_bounds__(256) void absmax_partial_kernel(const float *__restrict__ x, int64_t n,
+                                                                   float *__restrict__ partial) {
+    __shared__ float red[4];
+    float mx = 0.0f;
+    const int64_t n4 = ((uintptr_t)x & 15) ? 0 : n / 4;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+        const floatx4 v = ld4(x + 4 * i);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    }
+    for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        mx = fmaxf(mx, fabsf(x[i]));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// fp32 W [N][ldw_in] (K a multiple of 16) scaled by 2^h2_exponent(max|W|)
+// (max|W| read from the header) -> its h, m fp16 pieces, tile-major: element
+// (n, k) of piece p at H2_HEADER bytes plus, in fp16 units,
+//   ((n/128 * K/16 + k/16) * 2 + p) * 2048 + (n%128) * 16 + 8 * (s ^ (n/8)%2) + e
+// with slot s and element e from split_k_slot(k) % 16 = 8 s + e (the layout
+// of split_weight_kernel with two planes).  Rows past N are zero.
+static __global__ __launch_bounds__(256) void split_weight_h2_kernel(const float *__restrict__ W, int N, int K,
+                                                                    int ldw_in, void *__restrict__ pieces) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int rows = (N + GS_BN - 1) / GS_BN * GS_BN;
+    if (idx >= (int64_t)rows * K) return;
+    const float s = ldexpf(1.0f, h2_exponent(*static_cast<const float *>(pieces)));
+    const int n = (int)(idx / K), k = (int)(idx % K);
+    _Float16 h = (_Float16)0.0f, m = (_Float16)0.0f;
+    if (n < N) {
+        const float y = W[(size_t)n * ldw_in + k] * s;
+        h = (_Float16)y;
+        m = (_Float16)(y - (float)h);
+    }
+    const int r = n % GS_BN, pos = split_k_slot(k) & 15;
+    const int phys = (pos >> 3) ^ ((r >> 3) & 1);
+    const size_t o = ((size_t)(n / GS_BN) * (K / GS_BK) + k / GS_BK) * H2_WBLOCK + (size_t)r * GS_BK + 8 * phys + (pos & 7);
+    _Float16 *planes = reinterpret_cast<_Float16 *>(static_cast<char *>(pieces) + H2_HEADER);
+    planes[o] = h;
+    planes[o + GS_BN * GS_BK] = m;
+}
+
+// Bounds on the operands downstream of an RMSNorm with gain gamma[D]:
+//   out[0] = sqrt(D) max|gamma|                  (|y_i| <= ||y||_2 <= out[0])
+//   out[1] = t or t^2 (square), t = out[0] max_n ||W_n||_2 + max_n |b_n|
+//            (a bound on every output of the linear W y + b, W [N][D]; its
+//            square bounds a GELU-GLU of two such outputs); 0 without W.
+// One workgroup of 1024 threads: one wave per row of W at a time.
+static __global__ __launch_bounds__(1024) void operand_bounds_kernel(const float *__restrict__ gamma, int D,
+                                                                    const float *__restrict__ W, int N,
+                                                                    const float *__restrict__ b, int square,
+                                                                    float *__restrict__ out) {
+    __shared__ float red[2][16];
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float g = 0.0f, nrm = 0.0f, bm = 0.0f;
+    for (int i = tid; i < D; i += 1024) g = fmaxf(g, fabsf(gamma[i]));
+    if (W) {
+        for (int n = wave; n < N; n += 16) {
+            float ss = 0.0f;
+            for (int k = lane; k < D; k += 64) ss = fmaf(W[(size_t)n * D + k], W[(size_t)n * D + k], ss);
+            nrm = fmaxf(nrm, sqrtf(wave_sum(ss)));
+        }
+        if (b)
+            for (int n = tid; n < N; n += 1024) bm = fmaxf(bm, fabsf(b[n]));
+    }
+    g = wave_max(g);
+    bm = wave_max(bm);
+    if (lane == 0) {
+        red[0][wave] = fmaxf(g, 0.0f);
+        red[1][wave] = bm;
+    }
+    __shared__ float red_n[16];
+    if (lane == 0) red_n[wave] = nrm;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++) {
+            red[0][0] = fmaxf(red[0][0], red[0][w]);
+            red[1][0] = fmaxf(red[1][0], red[1][w]);
+            red_n[0] = fmaxf(red_n[0], red_n[w]);
+        }
+        // 1 + 2^-10 covers the rounding of the sums above
+        const float in = sqrtf((float)D) * red[0][0] * (1.0f + 0x1p-10f);
+        out[0] = in;
+        float t = W ? (in * red_n[0] + red[1][0]) * (1.0f + 0x1p-10f) : 0.0f;
+        out[1] = square ? t * t : t;
+    }
+}
+
+}  // namespace vh

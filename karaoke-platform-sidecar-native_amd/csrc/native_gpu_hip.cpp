@@ -77,7 +77,7 @@ struct CacheEntry {
     uint64_t fp;
     float *dev;
     float *dev_bias;   // fused QKV+gate bias
-    void *dev_split = nullptr;  // split planes of dev (made on first use)
+    void *dev_split = nullptr;  // fp16 two-piece planes of dev (made on first use)
 };
 
 }  // namespace
@@ -99,6 +99,14 @@ struct native_gpu {
     bool transposed = false;   // physical [ll][ls]
     // mask + matmul scratch
     DeviceBuffer normed, hidden, proj, mask, io_in, io_out, tables;
+    // A-operand bounds of the fp16 two-piece GEMMs: [0..3] the current layer
+    // (layer_bounds), [4..5] the mask features, [6] a matmul input, then
+    // absmax scratch
+    DeviceBuffer bounds;
+    float *bound(int i) { return bounds.f() + i; }
+    bool ensure_bounds() {
+        return bounds.ensure((64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bounds)");
+    }
 
     // Report, disable for the rest of the process, and tell the host to
     // compute this step itself.
@@ -137,8 +145,8 @@ struct native_gpu {
         return dev;
     }
 
-    // Split planes (gemm_split) of a cached device matrix [out][in]; null
-    // when `in` is not a multiple of 16 (the fp32 MFMA GEMM serves it).
+    // fp16 two-piece planes (gemm_h2) of a cached device matrix [out][in];
+    // null when `in` is not a multiple of 16 (the fp32 MFMA GEMM serves it).
     // VOCALARC_GPU_SPLIT=0 keeps every product on the fp32 MFMA instruction.
     const void *split(const float *dev, int in, int out) {
         static const bool off = [] {
@@ -150,8 +158,8 @@ struct native_gpu {
             if (e.dev != dev) continue;
             if (e.dev_split) return e.dev_split;
             void *p = nullptr;
-            if (!check(hipMalloc(&p, split_bytes(out, in)), "hipMalloc(split weight)")) return nullptr;
-            if (!split_weights(stream, dev, out, in, in, p)) {
+            if (!check(hipMalloc(&p, h2_bytes(out, in)), "hipMalloc(split weight)")) return nullptr;
+            if (!split_weights_h2(stream, dev, out, in, in, p)) {
                 (void)hipFree(p);
                 return nullptr;
             }
@@ -220,10 +228,14 @@ struct native_gpu {
         L.w2 = const_cast<float *>(matrix(w->ff2_weight, d.ff_dim, D));
         L.b2 = const_cast<float *>(vector(w->ff2_bias, D));
         if (!(L.gamma && L.ff_gamma && L.wout && L.w1 && L.b1 && L.w2 && L.b2)) return false;
-        L.wqkvg_s = const_cast<void *>(split(L.wqkvg, D, d.qkvg_dim()));
-        L.wout_s = const_cast<void *>(split(L.wout, d.inner(), D));
-        L.w1_s = const_cast<void *>(split(L.w1, D, d.ff1_out()));
-        L.w2_s = const_cast<void *>(split(L.w2, d.ff_dim, D));
+        L.wqkvg_p = const_cast<void *>(split(L.wqkvg, D, d.qkvg_dim()));
+        L.wout_p = const_cast<void *>(split(L.wout, d.inner(), D));
+        L.w1_p = const_cast<void *>(split(L.w1, D, d.ff1_out()));
+        L.w2_p = const_cast<void *>(split(L.w2, d.ff_dim, D));
+        // the bounds follow this call's gains and matrices (a few microseconds
+        // of device work, ordered before the layer's GEMMs on the stream)
+        if (!ensure_bounds() || !layer_bounds(stream, d, L, bound(0))) return false;
+        L.bounds = bound(0);
         return true;
     }
 
@@ -344,8 +356,11 @@ extern "C" int native_gpu_matmul(native_gpu *gpu, int64_t rows, int in, int out,
     const size_t ib = (size_t)rows * in * sizeof(float), ob = (size_t)rows * out * sizeof(float);
     hipStream_t s = gpu->stream;
     auto product = [&]() {
-        if (Ws)
-            return gemm_split(s, {gpu->io_in.f(), in, Ws, B, gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
+        if (Ws)  // the input's own maximum bounds it
+            return gpu->ensure_bounds() &&
+                   absmax(s, gpu->io_in.f(), rows * in, gpu->bound(64), gpu->bound(6)) &&
+                   gemm_h2(s, {gpu->io_in.f(), in, Ws, B, gpu->io_out.f(), out, rows, out, in},
+                           OperandBound{gpu->bound(6), 0.0f}, EPI_STORE);
         return gemm(s, {gpu->io_in.f(), in, W, in, B, gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
     };
     bool ok = gpu->io_in.ensure(ib, "hipMalloc(matmul input)") && gpu->io_out.ensure(ob, "hipMalloc(matmul output)") &&
@@ -461,7 +476,7 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
               gpu->tables.ensure(sizeof(MaskTable), "hipMalloc(mask table)");
     if (!ok) return gpu->fail("mask buffers");
     std::vector<GemmArgs> g1, g2;
-    std::vector<GemmArgsSplit> s1, s2;  // the same products on the split GEMM
+    std::vector<GemmArgsH2> s1, s2;  // the same products on the fp16 two-piece GEMM
     bool sp = true;
     MaskTable tab;
     memset(&tab, 0, sizeof(tab));
@@ -488,8 +503,12 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
         off += (int64_t)M * 2 * dim;
         maxdim = std::max(maxdim, dim);
     }
+    // layer 1's A: the final RMSNorm's output (bound from its gain); layer
+    // 2's A: tanh, within [-1, 1]
     ok = rmsnorm(s, gpu->x.f(), D, gamma, gpu->normed.f(), D, gpu->tokens, D) &&
-         (sp ? gemm_split_batched(s, s1, EPI_TANH) && gemm_split_batched(s, s2, EPI_STORE)
+         (sp ? gpu->ensure_bounds() && operand_bounds(s, gamma, D, nullptr, 0, nullptr, false, gpu->bound(4)) &&
+                   gemm_h2_batched(s, s1, OperandBound{gpu->bound(4), 0.0f}, EPI_TANH) &&
+                   gemm_h2_batched(s, s2, OperandBound{nullptr, 1.0f}, EPI_STORE)
              : gemm_batched(s, g1, EPI_TANH) && gemm_batched(s, g2, EPI_STORE)) &&
          check(hipMemcpyAsync(gpu->tables.ptr, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(mask table)");
     if (ok) {

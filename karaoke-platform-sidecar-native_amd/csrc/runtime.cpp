@@ -16,6 +16,7 @@
 #include "gemm.hpp"
 #include "gemm_bf16.hpp"
 #include "gemm_split.hpp"
+#include "gemm_h2.hpp"
 
 namespace vh {
 
@@ -411,6 +412,128 @@ bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *p
     return sync_debug(s, "split_weight_kernel");
 }
 
+// ------------------------------------------------------- fp16 two-piece GEMM
+static bool gemm_h2_ok(const GemmArgsH2 &g, int epilogue) {
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2 || !g.W) return false;
+    if (g.K % GS_BK || g.lda % 4 || g.lda < g.K || g.lda > (1 << 21)) return false;  // lane load offsets are 32-bit
+    if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
+    if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return false;
+    return true;
+}
+
+static GemmDescH2 to_desc_h2(const GemmArgsH2 &g) {
+    GemmDescH2 d;
+    d.A = g.A; d.W = g.W; d.bias = g.bias; d.C = g.C;
+    d.M = (int)g.M; d.N = g.N; d.K = g.K;
+    d.lda = g.lda; d.ldc = g.ldc;
+    return d;
+}
+
+template <int EPI>
+static void launch_h2(hipStream_t s, const GemmDescH2 &d, const H2Bound &b, unsigned tiles) {
+    hipLaunchKernelGGL(gemm_h2_kernel<EPI>, dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
+}
+
+bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int epilogue, KernelTimer *t,
+             const char *name) {
+    if (!gemm_h2_ok(g, epilogue)) {
+        set_error("gemm_h2: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K, g.lda);
+        return false;
+    }
+    const GemmDescH2 d = to_desc_h2(g);
+    const H2Bound b{bound.dev, bound.value};
+    const unsigned tiles = (unsigned)(((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
+    Scope sc(t, s, name);
+    switch (epilogue) {
+        case EPI_STORE: launch_h2<EPI_STORE>(s, d, b, tiles); break;
+        case EPI_GELU: launch_h2<EPI_GELU>(s, d, b, tiles); break;
+        case EPI_TANH: launch_h2<EPI_TANH>(s, d, b, tiles); break;
+        case EPI_RESIDUAL: launch_h2<EPI_RESIDUAL>(s, d, b, tiles); break;
+        case EPI_GEGLU: launch_h2<EPI_GEGLU>(s, d, b, tiles); break;
+        default: set_error("unknown GEMM epilogue %d", epilogue); return false;
+    }
+    return sync_debug(s, "gemm_h2_kernel");
+}
+
+template <int EPI>
+static void launch_h2_batched(hipStream_t s, const GemmBatchH2 &b, unsigned tiles, unsigned n) {
+    hipLaunchKernelGGL(gemm_h2_batched_kernel<EPI>, dim3(tiles, 1, n), dim3(GS_THREADS), 0, s, b);
+}
+
+bool gemm_h2_batched(hipStream_t s, const std::vector<GemmArgsH2> &gs, const OperandBound &bound, int epilogue,
+                     KernelTimer *t, const char *name) {
+    Scope sc(t, s, name);
+    for (size_t first = 0; first < gs.size(); first += GS_MAX_BATCH) {
+        const size_t count = std::min(gs.size() - first, (size_t)GS_MAX_BATCH);
+        GemmBatchH2 b;
+        memset(&b, 0, sizeof(b));
+        b.b = H2Bound{bound.dev, bound.value};
+        int64_t max_tiles = 0;
+        for (size_t i = 0; i < count; i++) {
+            const GemmArgsH2 &g = gs[first + i];
+            if (!gemm_h2_ok(g, epilogue)) {
+                set_error("gemm_h2_batched: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K,
+                          g.lda);
+                return false;
+            }
+            b.d[i] = to_desc_h2(g);
+            max_tiles = std::max(max_tiles, ((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
+        }
+        const unsigned tiles = (unsigned)max_tiles, n = (unsigned)count;
+        switch (epilogue) {
+            case EPI_STORE: launch_h2_batched<EPI_STORE>(s, b, tiles, n); break;
+            case EPI_GELU: launch_h2_batched<EPI_GELU>(s, b, tiles, n); break;
+            case EPI_TANH: launch_h2_batched<EPI_TANH>(s, b, tiles, n); break;
+            case EPI_RESIDUAL: launch_h2_batched<EPI_RESIDUAL>(s, b, tiles, n); break;
+            case EPI_GEGLU: launch_h2_batched<EPI_GEGLU>(s, b, tiles, n); break;
+            default: set_error("unknown GEMM epilogue %d", epilogue); return false;
+        }
+        if (!sync_debug(s, "gemm_h2_batched_kernel")) return false;
+    }
+    return true;
+}
+
+bool split_weights_h2(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces) {
+    if (N <= 0 || K <= 0 || K % GS_BK || ldw < K || (h2_bytes(N, K) - H2_HEADER) / 4 > (size_t)INT32_MAX ||
+        ((uintptr_t)pieces & 255)) {
+        set_error("split_weights_h2: bad shape N=%d K=%d ldw=%d (K a multiple of 16, pieces 256-byte aligned)", N, K,
+                  ldw);
+        return false;
+    }
+    hipLaunchKernelGGL(absmax_kernel, dim3(1), dim3(1024), 0, s, W, N, K, ldw, static_cast<float *>(pieces));
+    if (!sync_debug(s, "absmax_kernel")) return false;
+    const int64_t n = (int64_t)(N + GS_BN - 1) / GS_BN * GS_BN * K;
+    hipLaunchKernelGGL(split_weight_h2_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, W, N, K, ldw, pieces);
+    return sync_debug(s, "split_weight_h2_kernel");
+}
+
+bool absmax(hipStream_t s, const float *x, int64_t n, float *scratch, float *out) {
+    if (!x || n <= 0 || !scratch || !out) {
+        set_error("absmax: bad arguments");
+        return false;
+    }
+    const unsigned blocks = (unsigned)std::min<int64_t>(ABSMAX_PARTIALS, (n + 1023) / 1024);
+    hipLaunchKernelGGL(absmax_partial_kernel, dim3(blocks), dim3(256), 0, s, x, n, scratch);
+    if (!sync_debug(s, "absmax_partial_kernel")) return false;
+    hipLaunchKernelGGL(absmax_kernel, dim3(1), dim3(1024), 0, s, scratch, 1, (int)blocks, (int)blocks, out);
+    return sync_debug(s, "absmax_kernel");
+}
+
+bool layer_bounds(hipStream_t s, const Dims &d, const LayerWeights &w, float *bounds) {
+    return operand_bounds(s, w.gamma, d.dim, w.wqkvg, d.qkvg_dim(), w.bqkvg, false, bounds) &&
+           operand_bounds(s, w.ff_gamma, d.dim, w.w1, d.ff1_out(), w.b1, d.ffn_glu != 0, bounds + 2);
+}
+
+bool operand_bounds(hipStream_t s, const float *gamma, int D, const float *W, int N, const float *b, bool square,
+                    float *out) {
+    if (!gamma || D <= 0 || (W && N <= 0) || !out) {
+        set_error("operand_bounds: bad arguments D=%d N=%d", D, N);
+        return false;
+    }
+    hipLaunchKernelGGL(operand_bounds_kernel, dim3(1), dim3(1024), 0, s, gamma, D, W, N, b, square ? 1 : 0, out);
+    return sync_debug(s, "operand_bounds_kernel");
+}
+
 bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst, int ld) {
     const int64_t n = (int64_t)rows * cols;
     hipLaunchKernelGGL(to_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, src, static_cast<bf16 *>(dst),
@@ -689,26 +812,28 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
         if (!lin(normed, D, w.w1_h, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, true, "gemm_ff1")) return false;
         return lin(hid, d.ff_dim, w.w2_h, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, false, "gemm_ff2");
     }
-    // fp32 linears: split planes on bf16 matrix cores, or the fp32 MFMA GEMM
-    auto lin = [&](const float *A, int lda, const float *W, const void *Ws, const float *bias, float *C, int ldc, int N,
-                   int K, int epi, const char *name) {
-        if (Ws && precision == PREC_FP32 && K % SPLIT_K_MULTIPLE == 0)
-            return gemm_split(s, {A, lda, Ws, bias, C, ldc, tokens, N, K}, epi, t, name);
+    // fp32 linears: fp16 two-piece planes on the matrix cores (A bounded by
+    // bounds[slot]), or the fp32 MFMA GEMM
+    auto lin = [&](const float *A, int lda, const float *W, const void *Wp, int slot, const float *bias, float *C,
+                   int ldc, int N, int K, int epi, const char *name) {
+        if (Wp && w.bounds && precision == PREC_FP32 && K % SPLIT_K_MULTIPLE == 0)
+            return gemm_h2(s, {A, lda, Wp, bias, C, ldc, tokens, N, K}, OperandBound{w.bounds + slot, 0.0f}, epi, t,
+                           name);
         return gemm(s, {A, lda, W, K, bias, C, ldc, tokens, N, K}, epi, t, name);
     };
     // pre-norm -> fused QKV (+gate logits with their bias)
     if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
-    if (!lin(normed, D, w.wqkvg, w.wqkvg_s, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
+    if (!lin(normed, D, w.wqkvg, w.wqkvg_p, 0, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
     // rotary + attention + gates (long sequences: products as split bf16 on
     // the default fp32 path)
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32))
         return false;
     // out projection added to the residual stream
-    if (!lin(attn, inner, w.wout, w.wout_s, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;
+    if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;
     // FFN
     if (!rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
-    if (!lin(normed, D, w.w1, w.w1_s, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, "gemm_ff1")) return false;
-    return lin(hid, d.ff_dim, w.w2, w.w2_s, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, "gemm_ff2");
+    if (!lin(normed, D, w.w1, w.w1_p, 2, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, "gemm_ff1")) return false;
+    return lin(hid, d.ff_dim, w.w2, w.w2_p, 3, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, "gemm_ff2");
 }
 
 // ---------------------------------------------------------------- upload

@@ -128,6 +128,44 @@ inline size_t split_bytes(int N, int K) { return (size_t)(N + 127) / 128 * 128 *
 // l = w - h - m), tile-major for gemm_split (split_bytes(N, K) bytes).
 bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces);
 
+// fp32-accurate linear on fp16 matrix cores (gemm_h2.hpp): A fp32 with every
+// |A| element at most the bound, W as its two fp16 pieces (split_weights_h2),
+// C fp32.  K a multiple of 16; lda a multiple of 4 and at most 2^21; A 16-byte
+// aligned.  The bound is a device float (dev) or a value.
+struct GemmArgsH2 {
+    const float *A; int lda;
+    const void *W;
+    const float *bias;
+    float *C; int ldc;
+    int64_t M; int N, K;
+};
+struct OperandBound {
+    const float *dev = nullptr;
+    float value = 0.0f;
+};
+bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int epilogue, KernelTimer *t = nullptr,
+             const char *name = "gemm_h2");
+// A ragged batch of fp16 two-piece GEMMs with one A bound (one launch per 64 problems).
+bool gemm_h2_batched(hipStream_t s, const std::vector<GemmArgsH2> &gs, const OperandBound &bound, int epilogue,
+                     KernelTimer *t = nullptr, const char *name = "gemm_h2");
+// Bytes of W's fp16 pieces: a 256-byte header (max|W|) and two planes (N
+// rounded up to a multiple of 128).
+inline size_t h2_bytes(int N, int K) { return 256 + (size_t)(N + 127) / 128 * 128 * K * 4; }
+// fp32 W [N][ldw] -> max|W| and the h, m fp16 pieces of W * 2^e
+// (h2_bytes(N, K) bytes, 256-byte aligned).
+bool split_weights_h2(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces);
+// Device bounds for the fp16 two-piece GEMM's A operands downstream of an
+// RMSNorm with gain gamma[D] (operand_bounds_kernel in gemm_h2.hpp):
+// out[0] bounds the normalised activations, out[1] (when W [N][D] is given)
+// every output of W y + b, or its square when `square` (a GELU-GLU of two).
+bool operand_bounds(hipStream_t s, const float *gamma, int D, const float *W, int N, const float *b, bool square,
+                    float *out);
+
+// max |x[i]| over n floats into the device float out (scratch: ABSMAX_PARTIALS
+// device floats).
+constexpr int ABSMAX_PARTIALS = 1024;
+bool absmax(hipStream_t s, const float *x, int64_t n, float *scratch, float *out);
+
 // fp32 [rows][cols] -> bf16 [rows][ld] (ld >= cols, padding zeroed by the caller)
 bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst, int ld);
 inline int bf16_pitch(int k) { return (k + 7) & ~7; }
@@ -184,14 +222,20 @@ struct LayerWeights {
     float *w2 = nullptr, *b2 = nullptr;        // [D][ff_dim]
     // bf16 copies for the reduced-precision variant (null: fp32 only)
     void *wqkvg_h = nullptr, *wout_h = nullptr, *w1_h = nullptr, *w2_h = nullptr;
-    // split planes (split_weights) for the fp32 path on bf16 matrix cores
-    // (null: the fp32 MFMA GEMM runs instead)
-    void *wqkvg_s = nullptr, *wout_s = nullptr, *w1_s = nullptr, *w2_s = nullptr;
+    // fp16 two-piece planes (split_weights_h2) for the fp32 path on fp16
+    // matrix cores, and the device bounds of their A operands {QKV, out,
+    // FFN up, FFN down} (layer_bounds); null: the fp32 MFMA GEMM runs instead
+    void *wqkvg_p = nullptr, *wout_p = nullptr, *w1_p = nullptr, *w2_p = nullptr;
+    float *bounds = nullptr;
 };
+// The four A-operand bounds of a layer's linears into the device floats
+// bounds[0..3] (operand_bounds on its two RMSNorm gains and the matrices they
+// feed; the attention output is bounded by the fused projection's bound).
+bool layer_bounds(hipStream_t s, const Dims &d, const LayerWeights &w, float *bounds);
 
 // Arithmetic of the matrix products.  PREC_FP32 (the parity path): fp32
-// accuracy, the transformer linears on bf16 matrix cores by exact operand
-// splitting where split planes exist, the fp32 MFMA GEMM elsewhere.
+// accuracy, the transformer linears on fp16 matrix cores by two-piece operand
+// splitting where the planes exist, the fp32 MFMA GEMM elsewhere.
 // PREC_FP32_MFMA: every product on the fp32 MFMA instruction.  PREC_BF16:
 // bf16 operands with fp32 accumulation (separately reported variant).
 enum Precision : int { PREC_FP32 = 0, PREC_BF16 = 1, PREC_FP32_MFMA = 2 };

@@ -33,6 +33,7 @@ struct vh_context {
     RopeCache rope;
     BlockScratch scratch;
     DeviceBuffer staging;
+    DeviceBuffer bounds;  // vh_gemm_h2's computed A bound and its absmax scratch
 };
 
 struct vh_model {
@@ -47,8 +48,11 @@ struct vh_model {
     // bf16 copies of every matrix (built on the first switch to bf16)
     int precision = PREC_FP32;
     DeviceBuffer weights_h;
-    // split planes of the transformer and mask-estimator matrices (built at load)
-    DeviceBuffer weights_s;
+    // fp16 two-piece planes of the transformer and mask-estimator matrices and
+    // the bounds of their A operands (built at load): per layer 4 floats
+    // (layer_bounds), then the mask estimator's feature bound, then absmax
+    // scratch
+    DeviceBuffer weights_s, bounds;
     std::vector<void *> mask_w1_s, mask_w2_s;
     std::vector<void *> band_w_h, mask_w1_h, mask_w2_h;
     // DSP constants
@@ -166,6 +170,41 @@ extern "C" int vh_split_weights(vh_context *ctx, int N, int K, const float *W, i
         return 0;
     }
     return split_weights(ctx->stream, W, N, K, ldw_in, Ws) ? 1 : 0;
+}
+
+extern "C" int vh_gemm_h2(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, float a_bound,
+                          const void *Wp, const float *bias, float *C, int ldc, int epilogue) {
+    if (!ctx) return 0;
+    GemmArgsH2 g{A, lda, Wp, bias, C, ldc, M, N, K};
+    OperandBound b{nullptr, a_bound};
+    if (!(a_bound > 0.0f)) {
+        // the caller gave no bound: A's own maximum
+        if (M <= 0 || K <= 0 || lda < K || !A) {
+            set_error("vh_gemm_h2: bad shape M=%lld K=%d lda=%d", (long long)M, K, lda);
+            return 0;
+        }
+        if (!ctx->bounds.ensure((64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bound)") ||
+            !absmax(ctx->stream, A, (M - 1) * lda + K, ctx->bounds.f() + 64, ctx->bounds.f()))
+            return 0;
+        b.dev = ctx->bounds.f();
+    }
+    return gemm_h2(ctx->stream, g, b, epilogue, &ctx->timer, "gemm_h2") ? 1 : 0;
+}
+
+extern "C" size_t vh_h2_bytes(int N, int K) { return N > 0 && K > 0 ? h2_bytes(N, K) : 0; }
+
+extern "C" int vh_split_weights_h2(vh_context *ctx, int N, int K, const float *W, int ldw_in, void *Wp) {
+    if (!ctx || !W || !Wp) {
+        set_error("vh_split_weights_h2: null argument");
+        return 0;
+    }
+    return split_weights_h2(ctx->stream, W, N, K, ldw_in, Wp) ? 1 : 0;
+}
+
+extern "C" int vh_operand_bounds(vh_context *ctx, const float *gamma, int D, const float *W, int N, const float *b,
+                                 int square, float *out) {
+    if (!ctx) return 0;
+    return operand_bounds(ctx->stream, gamma, D, W, N, b, square != 0, out) ? 1 : 0;
 }
 
 extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *dst, int ld) {
@@ -401,20 +440,26 @@ bool prepare_bf16(vh_model *m) {
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(bf16 weights)");
 }
 
-// Split planes (three bf16 pieces) of the transformer and mask-estimator
-// matrices whose K is a multiple of 16: the fp32 path's linears on bf16
-// matrix cores.
+// fp16 two-piece planes of the transformer and mask-estimator matrices whose
+// K is a multiple of 16 (the fp32 path's linears on the matrix cores), and
+// the bounds of their A operands.
+static float *mask_feature_bound(vh_model *m) { return m->bounds.f() + 4 * m->layers.size(); }
+static float *absmax_scratch(vh_model *m) { return m->bounds.f() + 4 * m->layers.size() + 64; }
+
 bool prepare_split(vh_model *m) {
     if (m->weights_s.ptr) return true;
     const Dims &d = m->d;
     hipStream_t s = m->ctx->stream;
     const int D = d.dim, Hm = d.mask_hidden;
-    auto bytes = [](int N, int K) { return K % SPLIT_K_MULTIPLE ? 0 : (split_bytes(N, K) + 255) & ~(size_t)255; };
+    auto bytes = [](int N, int K) { return K % SPLIT_K_MULTIPLE ? 0 : (h2_bytes(N, K) + 255) & ~(size_t)255; };
     const size_t per_layer = bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) + bytes(D, d.ff_dim);
     size_t total = per_layer * m->layers.size();
     for (int b = 0; b < d.bands; b++) total += bytes(Hm, D) + bytes(2 * d.in_dim(b), Hm);
     m->mask_w1_s.assign(d.bands, nullptr);
     m->mask_w2_s.assign(d.bands, nullptr);
+    if (!m->bounds.ensure((4 * m->layers.size() + 64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bounds)"))
+        return false;
+    if (!operand_bounds(s, m->final_gamma, D, nullptr, 0, nullptr, false, mask_feature_bound(m))) return false;
     if (total == 0) return true;
     if (!m->weights_s.ensure(total, "hipMalloc(split weights)")) return false;
     char *cur = static_cast<char *>(m->weights_s.ptr);
@@ -422,12 +467,15 @@ bool prepare_split(vh_model *m) {
         if (K % SPLIT_K_MULTIPLE) return true;  // the fp32 MFMA GEMM serves this matrix
         *dst = cur;
         cur += bytes(N, K);
-        return split_weights(s, src, N, K, K, *dst);
+        return split_weights_h2(s, src, N, K, K, *dst);
     };
-    for (LayerWeights &w : m->layers) {
-        if (!split(w.wqkvg, d.qkvg_dim(), D, &w.wqkvg_s) || !split(w.wout, D, d.inner(), &w.wout_s) ||
-            !split(w.w1, d.ff1_out(), D, &w.w1_s) || !split(w.w2, D, d.ff_dim, &w.w2_s))
+    for (size_t i = 0; i < m->layers.size(); i++) {
+        LayerWeights &w = m->layers[i];
+        if (!split(w.wqkvg, d.qkvg_dim(), D, &w.wqkvg_p) || !split(w.wout, D, d.inner(), &w.wout_p) ||
+            !split(w.w1, d.ff1_out(), D, &w.w1_p) || !split(w.w2, D, d.ff_dim, &w.w2_p))
             return false;
+        w.bounds = m->bounds.f() + 4 * i;
+        if (!layer_bounds(s, d, w, w.bounds)) return false;
     }
     for (int b = 0; b < d.bands; b++)
         if (!split(m->mask_w1[b], Hm, D, &m->mask_w1_s[b]) || !split(m->mask_w2[b], 2 * d.in_dim(b), Hm, &m->mask_w2_s[b]))
@@ -509,7 +557,7 @@ bool stage_band_split(vh_model *m, const float *source, const SpecLayout &lay, i
 // final-normed features (frame-major rows m*B + b; fp32, or bf16 when
 // normed_bf16) -> mask bins (layout lay)
 bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, int T, float *mask,
-                const SpecLayout &lay) {
+                const SpecLayout &lay, bool final_normed) {
     const Dims &d = m->d;
     hipStream_t s = m->ctx->stream;
     const int M = chunks * T, B = d.bands, D = d.dim, Hm = d.mask_hidden;
@@ -525,8 +573,8 @@ bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, i
         return false;
     std::vector<GemmArgs> g1, g2;
     std::vector<GemmArgsBF16> h1, h2;
-    std::vector<GemmArgsSplit> s1, s2;
-    // fp32 path: both layers on the split GEMM when every band's pieces exist
+    std::vector<GemmArgsH2> s1, s2;
+    // fp32 path: both layers on the fp16 two-piece GEMM when every band's pieces exist
     bool sp = m->precision == PREC_FP32 && !normed_bf16;
     for (int b = 0; b < B && sp; b++) sp = m->mask_w1_s.size() == (size_t)B && m->mask_w1_s[b] && m->mask_w2_s[b];
     MaskTable tab;
@@ -566,7 +614,16 @@ bool stage_mask(vh_model *m, const void *normed, bool normed_bf16, int chunks, i
         if (!gemm_bf16_batched(s, h1, EPI_TANH, t, "gemm_mask1") || !gemm_bf16_batched(s, h2, EPI_STORE, t, "gemm_mask2"))
             return false;
     } else if (sp) {
-        if (!gemm_split_batched(s, s1, EPI_TANH, t, "gemm_mask1") || !gemm_split_batched(s, s2, EPI_STORE, t, "gemm_mask2"))
+        // layer 1's A: the final RMSNorm's bound, or for features from a caller
+        // their maximum; layer 2's A: tanh, within [-1, 1]
+        OperandBound b1{mask_feature_bound(m), 0.0f};
+        if (!final_normed) {
+            float *fb = mask_feature_bound(m) + 1;
+            if (!absmax(s, static_cast<const float *>(normed), (int64_t)M * B * D, absmax_scratch(m), fb)) return false;
+            b1.dev = fb;
+        }
+        if (!gemm_h2_batched(s, s1, b1, EPI_TANH, t, "gemm_mask1") ||
+            !gemm_h2_batched(s, s2, OperandBound{nullptr, 1.0f}, EPI_STORE, t, "gemm_mask2"))
             return false;
     } else if (!gemm_batched(s, g1, EPI_TANH, t, "gemm_mask1") || !gemm_batched(s, g2, EPI_STORE, t, "gemm_mask2")) {
         return false;
@@ -644,7 +701,7 @@ bool run_windows(vh_model *m, const float *audio, int64_t audio_len, const int64
           : !rmsnorm(m->ctx->stream, m->x.f(), d.dim, m->final_gamma, m->normed.f(), d.dim, tokens, d.dim,
                      &m->ctx->timer))
         return false;
-    if (!stage_mask(m, m->normed.ptr, h, chunks, T, m->mask.f(), lay)) return false;
+    if (!stage_mask(m, m->normed.ptr, h, chunks, T, m->mask.f(), lay, true)) return false;
     return stage_istft(m, m->source.f(), m->mask.f(), lay, chunks, T, sig_len, out, pitch);
 }
 
@@ -734,7 +791,7 @@ extern "C" int vh_mask_estimate(vh_context *ctx, vh_model *m, const float *featu
     if (!ctx || !m || frames <= 0) return 0;
     SpecLayout lay;
     if (!spec_layout_of(layout, m->d, frames, &lay)) return 0;
-    return stage_mask(m, features, false, 1, frames, mask, lay) ? 1 : 0;
+    return stage_mask(m, features, false, 1, frames, mask, lay, false) ? 1 : 0;
 }
 
 extern "C" int vh_forward(vh_context *ctx, vh_model *m, const float *audio, int length, float *vocals,

@@ -20,7 +20,7 @@ LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
 HARNESS_SYMBOLS = [
     "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
     "vh_rmsnorm", "vh_rmsnorm_bf16", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
-    "vh_gemm_split", "vh_split_bytes", "vh_split_weights", "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
+    "vh_gemm_split", "vh_split_bytes", "vh_split_weights", "vh_gemm_h2", "vh_h2_bytes", "vh_split_weights_h2", "vh_operand_bounds", "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
     "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
 ]
 ABI_SYMBOLS = [
@@ -67,6 +67,10 @@ def lib():
         "vh_gemm_split": (_I, [_P, _I64, _I, _I, _P, _I, _P, _P, _P, _I, _I]),
         "vh_split_bytes": (ctypes.c_size_t, [_I, _I]),
         "vh_split_weights": (_I, [_P, _I, _I, _P, _I, _P]),
+        "vh_gemm_h2": (_I, [_P, _I64, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _I, _I]),
+        "vh_h2_bytes": (ctypes.c_size_t, [_I, _I]),
+        "vh_split_weights_h2": (_I, [_P, _I, _I, _P, _I, _P]),
+        "vh_operand_bounds": (_I, [_P, _P, _I, _P, _I, _P, _I, _P]),
         "vh_to_bf16": (_I, [_P, _I64, _I, _P, _P, _I]),
         "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
         "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
@@ -196,6 +200,28 @@ class Context:
         _ok(lib().vh_gemm_split(self.h, M, N, K, ptr(A), lda or K, ptr(Ws),
                                 ptr(bias) if bias is not None else None, ptr(C),
                                 ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm_split")
+
+    @staticmethod
+    def h2_bytes(N: int, K: int) -> int:
+        """Bytes of the fp16 pieces of an N x K weight (see split_weights_h2)."""
+        return int(lib().vh_h2_bytes(N, K))
+
+    def split_weights_h2(self, W, Wp, N: int, K: int, ldw_in: int | None = None):
+        """fp32 W [N][ldw_in] -> max|W| and the tile-major fp16 pieces Wp (h2_bytes(N, K) bytes)."""
+        _ok(lib().vh_split_weights_h2(self.h, N, K, ptr(W), ldw_in or K, ptr(Wp)), "vh_split_weights_h2")
+
+    def gemm_h2(self, A, Wp, C, M: int, N: int, K: int, bias=None, epilogue: int = EPI_STORE,
+                lda: int | None = None, ldc: int | None = None, a_bound: float = 0.0):
+        """fp32-accurate linear on fp16 matrix cores; Wp from split_weights_h2; a_bound bounds |A| (0: max|A|)."""
+        _ok(lib().vh_gemm_h2(self.h, M, N, K, ptr(A), lda or K, float(a_bound), ptr(Wp),
+                             ptr(bias) if bias is not None else None, ptr(C),
+                             ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm_h2")
+
+    def operand_bounds(self, gamma, D: int, out, W=None, N: int = 0, bias=None, square: bool = False):
+        """Device bounds out[0..1] of the A operands after an RMSNorm with gain gamma (see vh_operand_bounds)."""
+        _ok(lib().vh_operand_bounds(self.h, ptr(gamma), D, ptr(W) if W is not None else None, N,
+                                    ptr(bias) if bias is not None else None, 1 if square else 0, ptr(out)),
+            "vh_operand_bounds")
 
     def to_bf16(self, src, dst, rows: int, cols: int, ld: int):
         _ok(lib().vh_to_bf16(self.h, rows, cols, ptr(src), ptr(dst), ld), "vh_to_bf16")

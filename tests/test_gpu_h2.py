@@ -1,0 +1,234 @@
+"""fp32 linears on fp16 matrix cores by two-piece operand splitting.
+
+Each operand is scaled by a power of two 2^e that puts its bound below 2^14,
+and every scaled value y is split into h = fp16(y), m = fp16(y - h) (nearest
+even); the GEMM accumulates hh + hm + mh in fp32 and scales back.  Pinned here:
+  * the exponent and the pieces: max|W| in the header, h and m bit-identical
+    to numpy's nearest-even float16 rounding applied in that chain, at the
+    documented tile-major positions (every position written once, rows past
+    N zero), h + m within 2^-22 |y| (or 2^-25 absolute) of y;
+  * the GEMM: its error against a float64 product of the fp32 operands is no
+    larger than the fp32 MFMA GEMM's (max and rms) and below 2^-18 sum|a w|,
+    which a dropped hm/mh product (2^-11 relative) or a misplaced piece would
+    break; an explicit bound equal to max|A| gives the same bits as the
+    computed one; a bound 2^16 times too loose still meets the error bound;
+  * the operand bounds: equal to their closed forms (sqrt(D) max|gamma|,
+    sqrt(D) max|gamma| max||W_n|| + max|b|, squared for GELU-GLU) and never
+    exceeded by an RMSNorm output, its linear or its GELU-GLU;
+  * the model: the fp32 parity bar with these linears (test_gpu_split's
+    forward test runs the default path, which uses them).
+"""
+
+import numpy as np
+import pytest
+
+from helpers import empty_dev, from_dev, gpu_available, to_dev
+
+pytestmark = pytest.mark.gpu
+
+if gpu_available():
+    import torch
+    import oracle as O
+    from vocalarc_hip import native
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    c = native.Context()
+    yield c
+    c.close()
+
+
+def _slot(k: np.ndarray) -> np.ndarray:
+    r = k & 15
+    return (k & ~15) + 8 * ((r >> 2) & 1) + (r & 3) + 4 * (r >> 3)
+
+
+def _piece_index(n: np.ndarray, k: np.ndarray, p: int, K: int) -> np.ndarray:
+    """fp16 index of piece p of W[n][k] in the layout of vh_split_weights_h2 (after the 128-half header)."""
+    pos = _slot(k) & 15
+    s, e = pos >> 3, pos & 7
+    return 128 + (((n // 128) * (K // 16) + k // 16) * 2 + p) * 2048 + (n % 128) * 16 + 8 * (s ^ ((n // 8) & 1)) + e
+
+
+def _exponent(bound: float) -> int:
+    """The e with bound * 2^e < 2^14, largest such (frexp: bound = f 2^E, f in [0.5, 1))."""
+    if not bound > 0 or not np.isfinite(bound):
+        return 0
+    return int(np.clip(14 - np.frexp(np.float32(bound))[1], -100, 100))
+
+
+def _pieces(ctx, w: np.ndarray):
+    n, k = w.shape
+    p = torch.zeros(ctx.h2_bytes(n, k) // 2, dtype=torch.float16, device="cuda:0")
+    ctx.split_weights_h2(to_dev(w), p, n, k)
+    return p
+
+
+def test_exponent_closed_form():
+    assert _exponent(1.0) == 13            # 1 * 2^13 < 2^14, 2^14 is not
+    assert _exponent(0.999) == 14
+    assert _exponent(16383.0) == 0
+    assert _exponent(16384.0) == -1
+    assert _exponent(0.0) == 0 and _exponent(float("nan")) == 0
+
+
+def test_split_weights_h2_exact(ctx, rng):
+    n, k = 137, 48  # two row tiles, the second ragged
+    assert ctx.h2_bytes(n, k) == 256 + 256 * k * 4
+    w = rng.standard_normal((n, k)).astype(np.float32) * np.float32(0.05)
+    # signs, zeros, powers of two, full significands, values far below the maximum
+    w[0, :8] = [0.25, -0.125, 0.0, -0.0, 1.0e-30, -3.0e-9, 0.2 * (1 + 2.0 ** -23), -(0.1 - 2.0 ** -30)]
+    w[1, :] = (np.arange(k, dtype=np.uint32) * 0x1F3 | 0x3E000000).view(np.float32)
+    pieces = torch.full((ctx.h2_bytes(n, k) // 2,), 7.0, dtype=torch.float16, device="cuda:0")
+    ctx.split_weights_h2(to_dev(w), pieces, n, k)
+    torch.cuda.synchronize()
+    raw = pieces.cpu().numpy()
+    wmax = float(np.abs(w).max())
+    assert raw[:2].view(np.float32)[0] == np.float32(wmax)
+    flat = raw[128:].astype(np.float32)
+    nn, kk = np.meshgrid(np.arange(256), np.arange(k), indexing="ij")
+    idx = [_piece_index(nn, kk, p, k) - 128 for p in range(2)]
+    assert sorted(np.concatenate([i.ravel() for i in idx]).tolist()) == list(range(flat.size))
+    for p in range(2):
+        assert np.all(flat[idx[p][n:]] == 0.0)
+    h, m = (flat[idx[p][:n]] for p in range(2))
+    y = w * np.float32(2.0 ** _exponent(wmax))
+    assert np.abs(y).max() < 2 ** 14
+    h_ref = y.astype(np.float16).astype(np.float32)
+    m_ref = (y - h_ref).astype(np.float16).astype(np.float32)
+    # bit for bit, except that the device may give a zero either sign
+    for got, want in ((h, h_ref), (m, m_ref)):
+        nz = want != 0
+        assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32))
+        assert np.all(got[~nz] == 0.0)
+    err = np.abs(h.astype(np.float64) + m - y)
+    assert np.all(err <= 2.0 ** -22 * np.abs(y) + 2.0 ** -25)
+
+
+CASES = [
+    # M, N, K, epilogue, bias
+    (300, 200, 96, 0, True),
+    (1000, 1568, 384, 0, True),   # ragged last column tile (1568 = 12.25 x 128)
+    (4097, 768, 512, 0, False),
+    (77, 384, 1536, 3, True),
+    (257, 1024, 256, 1, True),
+    (130, 1536, 384, 2, True),
+    (1, 8, 16, 0, True),          # one K chunk, one row
+    (513, 129, 32, 3, False),
+]
+
+
+def _ref64(x, w, b):
+    y = x.astype(np.float64) @ w.astype(np.float64).T
+    if b is not None:
+        y += b.astype(np.float64)
+    return y
+
+
+@pytest.mark.parametrize("M,N,K,epi,has_bias", CASES)
+def test_gemm_h2_accuracy(ctx, rng, M, N, K, epi, has_bias):
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) * np.float32(0.1) if has_bias else None
+    c0 = rng.standard_normal((M, N)).astype(np.float32)
+    planes = _pieces(ctx, w)
+    db = to_dev(b) if b is not None else None
+    dx = to_dev(x)
+    amax = float(np.abs(x).max())
+    outs = {}
+    for kind in ("h2", "h2_bound", "h2_loose", "fp32"):
+        dc = to_dev(c0)
+        if kind == "fp32":
+            ctx.gemm(dx, to_dev(w), dc, M, N, K, bias=db, epilogue=epi)
+        else:
+            bound = {"h2": 0.0, "h2_bound": amax, "h2_loose": amax * 2.0 ** 16}[kind]
+            ctx.gemm_h2(dx, planes, dc, M, N, K, bias=db, epilogue=epi, a_bound=bound)
+        outs[kind] = from_dev(dc).astype(np.float64)
+    # the device maximum gives the same exponent as the explicit bound
+    assert np.array_equal(outs["h2"], outs["h2_bound"])
+    pre = _ref64(x, w, b)
+    if epi == native.EPI_STORE or epi == native.EPI_RESIDUAL:
+        ref = pre + (c0 if epi == native.EPI_RESIDUAL else 0.0)
+        err = {kind: np.abs(o - ref) for kind, o in outs.items()}
+        scale = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T
+        bound = 2.0 ** -18 * scale + 2.0 ** -22 * np.abs(ref)
+        for kind in ("h2", "h2_loose"):
+            worst = float(np.max(err[kind] - bound))
+            assert worst <= 0, f"{kind}: error above 2^-18 sum|a||w| by {worst:.3e}"
+        print(f"h2 {M}x{N}x{K} epi{epi}: max|d| {err['h2'].max():.3e} rms {np.sqrt(np.mean(err['h2'] ** 2)):.3e}"
+              f" | loose bound max|d| {err['h2_loose'].max():.3e}"
+              f" | fp32 MFMA max|d| {err['fp32'].max():.3e} rms {np.sqrt(np.mean(err['fp32'] ** 2)):.3e}")
+        assert err["h2"].max() <= 1.5 * err["fp32"].max() + 1e-7
+        assert np.sqrt(np.mean(err["h2"] ** 2)) <= 1.25 * np.sqrt(np.mean(err["fp32"] ** 2)) + 1e-8
+    else:
+        f = (lambda v: O.gelu(v.astype(np.float32)).astype(np.float64)) if epi == native.EPI_GELU else np.tanh
+        ref = f(pre)
+        e_h2 = np.abs(outs["h2"] - ref).max()
+        e_fp32 = np.abs(outs["fp32"] - ref).max()
+        print(f"h2 {M}x{N}x{K} epi{epi}: max|d| {e_h2:.3e} | fp32 MFMA {e_fp32:.3e}")
+        assert e_h2 <= 1.5 * e_fp32 + 1e-6
+
+
+def test_gemm_h2_geglu(ctx, rng):
+    M, F, K = 333, 192, 384
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (0.05 * rng.standard_normal((2 * F, K))).astype(np.float32)
+    b = (0.1 * rng.standard_normal(2 * F)).astype(np.float32)
+    ref = O.geglu(_ref64(x, w, b).astype(np.float32)).astype(np.float64)
+    perm = np.empty(2 * F, dtype=np.int64)  # the library's 32-row value/gate interleave
+    for c in range(F):
+        perm[(c // 32) * 64 + (c % 32)] = c
+        perm[(c // 32) * 64 + 32 + (c % 32)] = F + c
+    planes = _pieces(ctx, np.ascontiguousarray(w[perm]))
+    dc = empty_dev((M, F))
+    ctx.gemm_h2(to_dev(x), planes, dc, M, 2 * F, K, bias=to_dev(np.ascontiguousarray(b[perm])),
+                epilogue=native.EPI_GEGLU)
+    err = np.abs(from_dev(dc) - ref)
+    assert err.max() <= 2e-5, err.max()
+
+
+def test_gemm_h2_rejects_bad_shapes(ctx):
+    x = torch.zeros(8, 24, device="cuda:0")
+    pieces = torch.zeros(ctx.h2_bytes(8, 32) // 2, dtype=torch.float16, device="cuda:0")
+    c = torch.zeros(8, 8, device="cuda:0")
+    with pytest.raises(native.NativeError, match="unsupported shape"):
+        ctx.gemm_h2(x, pieces, c, 8, 8, 24, a_bound=1.0)  # K must be a multiple of 16
+    with pytest.raises(native.NativeError, match="unsupported shape"):
+        ctx.gemm_h2(x, pieces, c, 8, 8, 16, lda=14, a_bound=1.0)  # lda must be a multiple of 4 and >= K
+    with pytest.raises(native.NativeError, match="bad shape"):
+        ctx.split_weights_h2(torch.zeros(8, 24, device="cuda:0"), pieces, 8, 24)  # K % 16
+
+
+@pytest.mark.parametrize("square", [False, True])
+def test_operand_bounds(ctx, rng, square):
+    D, N, T = 384, 520, 2000
+    gamma = (1.0 + 0.3 * rng.standard_normal(D)).astype(np.float32)
+    w = (0.05 * rng.standard_normal((N, D))).astype(np.float32)
+    b = (0.2 * rng.standard_normal(N)).astype(np.float32)
+    out = torch.zeros(2, device="cuda:0")
+    ctx.operand_bounds(to_dev(gamma), D, out, W=to_dev(w), N=N, bias=to_dev(b), square=square)
+    got = from_dev(out).astype(np.float64)
+    b0 = np.sqrt(D) * np.abs(gamma).max()
+    eps = 2.0 ** -10  # the kernel's allowance for its own rounding, applied at each step
+    assert abs(got[0] / (b0 * (1 + eps)) - 1) < 1e-6
+    t_ref = (b0 * (1 + eps) * np.sqrt((w.astype(np.float64) ** 2).sum(1)).max() + np.abs(b).max()) * (1 + eps)
+    assert abs(got[1] / (t_ref ** 2 if square else t_ref) - 1) < 1e-5
+    # the bounds hold for RMSNorm outputs, their linear and its GELU-GLU --
+    # including rows built to reach them (all mass on the largest gain)
+    x = rng.standard_normal((T, D)).astype(np.float32) * np.exp(rng.standard_normal((T, 1))).astype(np.float32)
+    x[0] = 0.0
+    x[0, np.argmax(np.abs(gamma))] = 5.0
+    y = O.rms_norm(x, gamma)
+    assert np.abs(y).max() <= got[0]
+    assert np.abs(y).max() >= 0.99 * got[0] / (1 + 2.0 ** -10)  # reached by row 0: the bound is tight
+    z = y.astype(np.float64) @ w.astype(np.float64).T + b
+    assert np.abs(z).max() <= (np.sqrt(got[1]) if square else got[1])
+    if square:
+        g = O.geglu(z.astype(np.float32))  # value = first half, gate = second half
+        assert np.abs(g).max() <= got[1]
+    no_w = torch.full((2,), 7.0, device="cuda:0")
+    ctx.operand_bounds(to_dev(gamma), D, no_w)
+    assert from_dev(no_w)[1] == 0.0
