@@ -7,9 +7,11 @@ depth 12, 62 bands, 8 heads x 64, GELU-GLU FFN (mult 4), hop 441, n_fft 2048:
 8 s windows with 2 s overlap (50 windows), 8 windows per device pass, linear
 cross-fade.  The input waveform is resident in HBM when the timed region
 starts; the output waveform is in HBM when it ends.  fp32 accuracy for
-`value`: the transformer linears run on the bf16 matrix cores as exact
-three-piece splits of their fp32 operands (six piece products per fp32
-product, fp32 accumulation), everything else on fp32 MFMA / fp32 / fp64.
+`value`: the transformer and mask-estimator linears run on the fp16 matrix
+cores as two-piece splits of their power-of-two-scaled fp32 operands (three
+piece products per fp32 product, fp32 accumulation), the time-axis attention
+on the bf16 matrix cores as three-piece splits (six products), everything
+else on fp32 MFMA / fp32 / fp64.
 Timed after it and reported separately: "fp32_mfma_variant", the same job
 with every product on the fp32 MFMA instruction, and "bf16_variant" (bf16
 operands at the matrix cores, fp32 accumulation and everything else fp32),
@@ -108,7 +110,7 @@ def measured_traffic() -> tuple[int | None, str | None]:
     """HBM bytes per launch of the dominant kernel, from the committed
     calibrated rocprofv3 counter summary (FETCH_SIZE/WRITE_SIZE scaled by a
     plain copy); None if that summary is absent."""
-    path = ROOT / "profiles" / "gemm-split-ff1-geglu_traffic.md"
+    path = ROOT / "profiles" / "gemm-h2-ff1-geglu_traffic.md"
     if not path.exists():
         return None, None
     for line in path.read_text().splitlines():
@@ -269,15 +271,16 @@ def main() -> int:
     achieved = flops / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
     traffic, traffic_src = measured_traffic()
     roofline = {
-        "kernel": "gemm_split_kernel<GELU-GLU> (FFN up-projection, M=397296 K=384 N=3072 per 8-window pass)",
+        "kernel": "gemm_h2_kernel<GELU-GLU> (FFN up-projection, M=397296 K=384 N=3072 per 8-window pass)",
         "bound": "mfma",
         "achieved": round(achieved, 2),
         "peak": MFMA_FP32_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
-        "note": "fp32 products as 6 exact bf16 piece products on the bf16 matrix cores; achieved counts the "
-                "algorithmic 2*M*K*N fp32 FLOPs, so frac can exceed 1 against the fp32 MFMA instruction peak",
-        "bf16_matrix_core_frac": round(6 * achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+        "note": "fp32 products as 3 fp16 piece products (two-piece splits of power-of-two-scaled operands) on "
+                "the fp16 matrix cores; achieved counts the algorithmic 2*M*K*N fp32 FLOPs, so frac can exceed 1 "
+                "against the fp32 MFMA instruction peak",
+        "matrix_core_frac": round(3 * achieved / MFMA_BF16_PEAK_TFLOPS, 4),
         "traffic": traffic,
         "traffic_unit": "bytes per full 8-window launch (beyond L2; algorithmic 3.058e9)",
         "traffic_source": traffic_src,
@@ -310,9 +313,10 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "precision_note": "fp32 accuracy: transformer linears as exact 3-piece bf16 splits (6 products, fp32 "
-                          "accumulation; error vs fp64 at or below the fp32 MFMA GEMM's), attention, band split, "
-                          "mask estimator on fp32 MFMA, DSP in fp64/fp32",
+        "precision_note": "fp32 accuracy: transformer and mask-estimator linears as 2-piece fp16 splits of "
+                          "power-of-two-scaled operands (3 products, fp32 accumulation; error vs fp64 at or below "
+                          "the fp32 MFMA GEMM's), time-axis attention as 3-piece bf16 splits (6 products), band "
+                          "split and band-axis attention on fp32 MFMA, DSP in fp64/fp32",
         "data": "synthetic (seeded sine+noise mix, random-init weights N(0,0.02), gammas N(1,0.02))",
         "config": {
             "workload": "full BS-RoFormer separation, 5 min stereo 44.1 kHz, 8 s windows / 2 s overlap, "

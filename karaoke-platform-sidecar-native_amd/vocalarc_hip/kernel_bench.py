@@ -63,9 +63,9 @@ def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | N
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,split,attn,bf16")
+    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,h2,split,attn,bf16")
     args = ap.parse_args()
-    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "split", "attn", "bf16"}
+    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "h2", "split", "attn", "bf16"}
 
     import torch
 
@@ -137,7 +137,7 @@ def main() -> int:
                   gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}")
             del a, w, b, c
 
-    if "split" in groups or "ff1" in groups:
+    if "split" in groups:
         # the same four GEMMs in fp32 accuracy on the bf16 matrix cores (three
         # bf16 pieces per fp32 operand, six piece products): algorithmic fp32
         # FLOPs against the fp32 MFMA peak, and the matrix-core work (6x)
@@ -147,8 +147,6 @@ def main() -> int:
                   ("gemm_split_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
                   ("gemm_split_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
                   ("gemm_split_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384))
-        if "split" not in groups:
-            shapes = shapes[2:3]  # the dominant kernel alone (counter runs)
         for name, K, N, epi, ocols in shapes:
             a = torch.randn(M, K, device=dev, generator=g)
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
@@ -161,6 +159,31 @@ def main() -> int:
             _emit(name, ms, gflop=gflop, shape=f"M={M} K={K} N={N}",
                   extra={"bf16_matrix_core_frac": round(6 * gflop / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
             del a, w, ws, b, c
+
+    if "h2" in groups or "ff1" in groups:
+        # the same four GEMMs as the default fp32 path runs them: fp16 two-piece
+        # splits (three products), A bounded by its maximum
+        M = 8 * 801 * 62
+        shapes = (("gemm_h2_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
+                  ("gemm_h2_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
+                  ("gemm_h2_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536),
+                  ("gemm_h2_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384))
+        if "h2" not in groups:
+            shapes = shapes[2:3]  # the dominant kernel alone (counter runs)
+        for name, K, N, epi, ocols in shapes:
+            a = torch.randn(M, K, device=dev, generator=g)
+            w = 0.05 * torch.randn(N, K, device=dev, generator=g)
+            wp = torch.empty(ctx.h2_bytes(N, K) // 2, dtype=torch.float16, device=dev)
+            ctx.split_weights_h2(w, wp, N, K)
+            b = torch.randn(N, device=dev, generator=g)
+            c = torch.zeros(M, ocols, device=dev)
+            bound = float(a.abs().max())
+            ms = _event_time(lambda: ctx.gemm_h2(a, wp, c, M, N, K, bias=b, epilogue=epi, a_bound=bound),
+                             max(3, reps // 4))
+            gflop = 2.0 * M * K * N / 1e9
+            _emit(name, ms, gflop=gflop, shape=f"M={M} K={K} N={N}",
+                  extra={"matrix_core_frac": round(3 * gflop / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
+            del a, w, wp, b, c
 
     if "bf16" in groups:
         # the same four GEMMs on bf16 matrix-core operands, with the operand

@@ -19,6 +19,14 @@ from pathlib import Path
 # kernel-name patterns (demangled or mangled) -> what the launch computes in
 # the separation pass
 ROLES = [
+    (r"gemm_h2_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via two-piece fp16)"),
+    (r"gemm_h2_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via two-piece fp16)"),
+    (r"gemm_h2_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via two-piece fp16)"),
+    (r"gemm_h2_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32 via two-piece fp16)"),
+    (r"gemm_h2_batched_kernel(<|ILi)0", "mask estimator layer 2, batched over bands (fp32 via two-piece fp16)"),
+    (r"split_weight_h2_kernel", "weight split into fp16 pieces (model load)"),
+    (r"absmax_kernel", "weight maximum for the fp16 pieces (model load)"),
+    (r"operand_bounds_kernel", "operand bounds of the fp16 two-piece GEMMs (model load)"),
     (r"gemm_split_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via split bf16)"),

@@ -2,7 +2,7 @@
 
 Two `rocprofv3 --pmc` runs of `python -m vocalarc_hip.kernel_bench --only copy,ff1`
 (one with FETCH_SIZE, one with WRITE_SIZE) give KiB per dispatch for the
-FFN up-projection GEMM (fp32 on bf16 matrix cores by operand splitting) at
+FFN up-projection GEMM (fp32 on fp16 matrix cores by two-piece operand splitting) at
 the 8-window pass shape and for a plain device copy
 of 1.27 GB.  Each counter is scaled by what it reads for the copy (known
 bytes read and written), and the result is written as a short summary:
@@ -18,10 +18,10 @@ import sys
 from pathlib import Path
 
 COPY_BYTES = 496 * 801 * 801 * 4          # read once and written once by the copy
-GEMM_KERNEL = "gemm_split_kernel<4>"      # GELU-GLU epilogue: the FFN up-projection
+GEMM_KERNEL = "gemm_h2_kernel<4>"         # GELU-GLU epilogue: the FFN up-projection
 COPY_KERNEL = "__amd_rocclr_copyBuffer"  # torch copy_ of a contiguous tensor is a runtime blit
-# A fp32, W as three bf16 planes, bias fp32, output fp32
-FF1_ALGORITHMIC = 397296 * 384 * 4 + 3 * 3072 * 384 * 2 + 3072 * 4 + 397296 * 1536 * 4
+# A fp32, W as two fp16 planes, bias fp32, output fp32
+FF1_ALGORITHMIC = 397296 * 384 * 4 + 2 * 3072 * 384 * 2 + 3072 * 4 + 397296 * 1536 * 4
 
 
 def _per_dispatch(run_dir: str, counter: str, needle: str, grid: int | None = None) -> float:
@@ -52,7 +52,7 @@ def main() -> int:
         f" -> factors {kf:.4f} (fetch), {kw:.4f} (write)",
         f"* GEMM M=397296 K=384 N=3072 (median per dispatch): FETCH_SIZE {f_gemm / 1e9:.4f} GB, WRITE_SIZE {w_gemm / 1e9:.4f} GB",
         f"* calibrated traffic per launch: {traffic / 1e9:.4f} GB "
-        f"(algorithmic: {FF1_ALGORITHMIC / 1e9:.4f} GB = A 610.3 MB + W planes 7.1 MB + output 2440.6 MB)",
+        f"(algorithmic: {FF1_ALGORITHMIC / 1e9:.4f} GB = A 610.3 MB + W planes 4.7 MB + output 2440.6 MB)",
         "", f"traffic_bytes_per_launch: {int(traffic)}",
     ]
     Path(out).write_text("\n".join(lines) + "\n")
