@@ -136,11 +136,15 @@ int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *
    takes qkv as bf16 and runs the bf16-MFMA kernel (q, k, v and the
    probabilities as bf16 operands, fp32 softmax statistics); VH_ATT_SPLIT
    (fp32 qkv, length > 64) runs the products in fp32 accuracy as exact
-   three-piece bf16 splits on the bf16 matrix cores (the default fp32 path's
-   time-axis attention). */
+   three-piece bf16 splits on the bf16 matrix cores; VH_ATT_H2 (fp32 qkv,
+   length > 64) runs them in fp32 accuracy as two-piece fp16 splits of
+   power-of-two-scaled operands, the scales from max|qkv| computed on the
+   device (the default fp32 path's time-axis attention, which takes its
+   bound from the projection's weights instead). */
 #define VH_ATT_OUT_BF16 1
 #define VH_ATT_BF16 2
 #define VH_ATT_SPLIT 4
+#define VH_ATT_H2 8
 int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                  int apply_rotary, int flags);
 

@@ -39,6 +39,7 @@ struct AttnArgs {
     int inner;      // H * 64
     int gate_col;   // < 0: no gates
     float scale;    // 1/sqrt(64)
+    const float *bound;  // device bound on |q|, |k|, |v| (attention_h2_kernel only)
 };
 
 constexpr int ATT_DH = 64;

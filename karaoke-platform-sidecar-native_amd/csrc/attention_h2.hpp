@@ -1,0 +1,320 @@
+// Fused axial attention in fp32 accuracy on fp16 matrix cores: the
+// time-axis attention of the default fp32 path.  Same task decomposition,
+// layout, rotary, online softmax, gate and software pipeline as
+// attention_split_kernel (attention_split.hpp); every operand is instead
+// scaled by a power of two and split into two fp16 pieces (gemm_h2.hpp):
+//   S^T = K * Q^T: k (rotated) times 2^ek and q (rotated, times the softmax
+//     scale and log2 e) times 2^eq, so both stay below 2^14; three
+//     v_mfma_f32_32x32x16_f16 per 32-key block and 16 head dims (km.qh,
+//     kh.qm, kh.qh); the block's scores are scaled back by 2^-(ek+eq).
+//   O^T += V^T * P^T: v times 2^ev, the probabilities (at most 2^8: the
+//     running maximum is raised lazily) times 2^5; three products per 16
+//     keys and 32 dims; the output is scaled back by 2^-(ev+5).
+// The exponents come from one bound B on |q|, |k| and |v| before rotation
+// (a.bound, a device float; a rotated pair keeps its 2-norm, so rotated
+// values stay below sqrt(2) B).  The probabilities, statistics,
+// normalisation and gate are fp32 as in the fp32 kernel.  LDS holds two
+// pieces per operand (38 KB), so three workgroups share a CU: three waves per
+// SIMD within 168 VGPRs (a few spilled outside the key loop; 5% faster than
+// two waves per SIMD without spills).
+#pragma once
+
+#include "attention.hpp"
+#include "attention_bf16.hpp"
+#include "gemm_h2.hpp"
+
+namespace vh {
+
+// OFF32 as attention_split_kernel.
+template <int WAVES, typename TO, bool ROPE, bool OFF32>
+__global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a) {
+    constexpr int NT = 64 * WAVES;
+    constexpr int CHUNKS = ATT_KB * ATT_DH / 8;  // 8-element chunks per K (or V) tile: 256
+    constexpr int PER_T = CHUNKS / NT;
+    static_assert(CHUNKS % NT == 0, "tile must divide evenly");
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][2][ATT_KB][ATB_KPITCH];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][2][ATT_DH][ATB_VPITCH];
+
+    const float *qkv = static_cast<const float *>(a.qkv);
+    const int qgroups = (a.L + 32 * WAVES - 1) / (32 * WAVES);
+    const int task = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);  // neighbouring tasks share K/V rows: same XCD
+    const int qg = task % qgroups;
+    const int sh = task / qgroups;
+    const int h = sh % a.H;
+    const int s = sh / a.H;
+
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int li = lane & 31, lh = lane >> 5;
+    const int q0 = (qg * WAVES + wave) * 32;
+
+    const int kcol = a.inner + h * ATT_DH;
+    const int vcol = 2 * a.inner + h * ATT_DH;
+
+    // power-of-two scales from the bound on |q|, |k|, |v|
+    const float qs = a.scale * 1.4426950408889634f;
+    const float bnd = *a.bound;
+    const int ek = h2_exponent(1.4142135f * 1.0001f * bnd);
+    const int eq = h2_exponent(1.4142135f * 1.0001f * bnd * qs);
+    const int ev = h2_exponent(bnd);
+    constexpr int EP = 5;  // probabilities <= 2^8: 2^8 * 2^5 < 2^14
+    const float k_scale = ldexpf(1.0f, ek), v_scale = ldexpf(1.0f, ev);
+    const float s_unscale = ldexpf(1.0f, -(ek + eq)), o_unscale = ldexpf(1.0f, -(ev + EP)), p_scale = ldexpf(1.0f, EP);
+
+    // Q of query q0+li, dims 16g + 8lh .. +7, rotated, scaled (log2 domain), split.
+    halfx8 qh[4], qm[4];
+    float gate_logit = 0.0f;  // loaded with Q so the store does not wait on it
+    {
+        const int q = min(q0 + li, a.L - 1);
+        const float *qp = qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+        if (a.gate_col >= 0) gate_logit = qkv[(size_t)attn_row(a, s, q) * a.ld + a.gate_col + h];
+        const float q_scale = qs * ldexpf(1.0f, eq);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int d0 = 16 * g + 8 * lh;
+            floatx4 lo = ld4(qp + d0), hi = ld4(qp + d0 + 4);
+            if constexpr (ROPE) {
+                lo = rope4_table(lo, a.rope, q, d0);
+                hi = rope4_table(hi, a.rope, q, d0 + 4);
+            }
+            split8_h2(lo, hi, q_scale, qh[g], qm[g]);
+        }
+    }
+
+    // Staging.  The stage holds one K block and one V block in registers as
+    // loaded (K runs one block ahead of V, below); rotation and the split
+    // happen when it is written to LDS, an iteration after its loads were
+    // issued, so no wait on them falls inside the iteration's MFMA work.
+    // Chunk c of the K tile is key c/8, dims 8*(c%8); chunk c of the V tile
+    // is keys 2*(c%16) and 2*(c%16)+1, dims 4*(c/16) .. +3.  Keys past L (and
+    // blocks past the last) load the row of key L-1: no branch around the
+    // loads, and nothing to zero -- their scores are masked to -inf, so their
+    // probabilities are exactly 0 and their (finite) V rows add nothing.
+    struct Stage {
+        floatx4 k[PER_T][2], kr[PER_T][2], v[PER_T][2];
+    };
+    const char *qkv_b = reinterpret_cast<const char *>(qkv);
+    const uint32_t row_s_bytes = (uint32_t)attn_row(a, s, 0) * (uint32_t)a.ld * 4u;  // used when OFF32
+    const uint32_t pos_bytes = (uint32_t)a.pos_stride * (uint32_t)a.ld * 4u;
+    auto row_ptr = [&](int p, int col) -> const float * {
+        if constexpr (OFF32)
+            return reinterpret_cast<const float *>(qkv_b + (__umul24((uint32_t)p, pos_bytes) + row_s_bytes + 4u * col));
+        else
+            return qkv + (size_t)attn_row(a, s, p) * a.ld + col;
+    };
+    auto load = [&](Stage &st, int kbk, int kbv) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) {
+            const int c = tid + NT * i;
+            const int kk = c >> 3, kd = 8 * (c & 7);
+            const int pkc = min(kbk * ATT_KB + kk, a.L - 1);
+            const float *kp = row_ptr(pkc, kcol + kd);
+            st.k[i][0] = ld4(kp);
+            st.k[i][1] = ld4(kp + 4);
+            if constexpr (ROPE) {
+                const float *tp = reinterpret_cast<const float *>(reinterpret_cast<const char *>(a.rope) +
+                                                                  (__umul24((uint32_t)pkc, 4u * ATT_DH) + 4u * kd));
+                st.kr[i][0] = ld4(tp);
+                st.kr[i][1] = ld4(tp + 4);
+            }
+            const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
+#pragma unroll
+            for (int e = 0; e < 2; e++) st.v[i][e] = ld4(row_ptr(min(kbv * ATT_KB + vk + e, a.L - 1), vcol + vd));
+        }
+    };
+    // rotate and split: K block kbk into Ks[kbk%2], and (with_v) V block kbv
+    // transposed into Vt[kbv%2]
+    auto store = [&](const Stage &st, int kbk, int kbv, bool with_v) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) {
+            const int c = tid + NT * i;
+            floatx4 k0 = st.k[i][0], k1 = st.k[i][1];
+            if constexpr (ROPE) {
+                k0 = rope_pairs(k0, st.kr[i][0]);
+                k1 = rope_pairs(k1, st.kr[i][1]);
+            }
+            halfx8 p[2];
+            split8_h2(k0, k1, k_scale, p[0], p[1]);
+#pragma unroll
+            for (int k = 0; k < 2; k++) *reinterpret_cast<halfx8 *>(&Ks[kbk & 1][k][c >> 3][8 * (c & 7)]) = p[k];
+            if (with_v) {
+                // the two keys' values interleaved, so dword e of each piece is
+                // the (key vk, key vk+1) pair of dim vd+e: one 32-bit write each
+                const floatx4 &v0 = st.v[i][0], &v1 = st.v[i][1];
+                split8_h2(floatx4{v0[0], v1[0], v0[1], v1[1]}, floatx4{v0[2], v1[2], v0[3], v1[3]}, v_scale, p[0], p[1]);
+                const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
+                const int pos = (vk & 16) | split_k_slot(vk & 15);  // even: the pair stays adjacent
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const u32x4 w = __builtin_bit_cast(u32x4, p[k]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) *reinterpret_cast<uint32_t *>(&Vt[kbv & 1][k][vd + e][pos]) = w[e];
+                }
+            }
+        }
+    };
+    // S^T block of 32 keys x 32 queries from Ks[kbuf], scaled back; each
+    // 16-dim group's K pieces are read while the previous group's products run
+    auto qk = [&](int kbuf) {
+        floatx16 sc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+        halfx8 kp[2][2];
+        auto read = [&](int g, halfx8 (&k)[2]) {
+#pragma unroll
+            for (int p = 0; p < 2; p++) k[p] = *reinterpret_cast<const halfx8 *>(&Ks[kbuf][p][li][16 * g + 8 * lh]);
+        };
+        read(0, kp[0]);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            if (g < 3) read(g + 1, kp[(g + 1) & 1]);
+            const halfx8 &kh = kp[g & 1][0], &km = kp[g & 1][1];
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(km, qh[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qm[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[g], sc, 0, 0, 0);
+        }
+        return sc * s_unscale;  // exact: a power of two
+    };
+
+    floatx16 o[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[t][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // First half of the online softmax of block kb (its scores just
+    // computed): mask keys past L, raise the running maximum (and rescale o
+    // and l) as online_softmax_block does.
+    auto soft_max = [&](floatx16 &sc, int kb) {
+        const int valid = a.L - kb * ATT_KB;
+        if (valid < ATT_KB) {
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
+        }
+        float mb = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
+        {
+            // the other half-wave's maximum (lanes l and l^32 hold one query):
+            // one v_permlane32_swap instead of an LDS permute round trip
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
+            mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const bool grow = mb > m_run + 8.0f;
+        if (__ballot(grow)) {
+            const float m_new = grow ? mb : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+            o[0] *= alpha;
+            o[1] *= alpha;
+            m_run = m_new;
+        }
+    };
+    // Second half (probabilities, row sum) and O^T += V^T P^T from Vt[vbuf].
+    auto soft_pv = [&](floatx16 &sc, int vbuf) {
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_run);
+            ls += sc[r];
+        }
+        l_run += ls;
+        // the lane's probabilities of keys 16st + {4lh..4lh+3, 8+4lh..8+4lh+3}
+        // (registers 8st..8st+7) as pieces; V^T pieces for (st, t) read one
+        // step ahead of their products
+        halfx8 pp[2][2];
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+            split8_h2(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
+                      floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, p_scale, pp[st][0],
+                      pp[st][1]);
+        halfx8 vp[2][2];
+        auto read = [&](int step, halfx8 (&v)[2]) {
+            const int st = step >> 1, t = step & 1;
+#pragma unroll
+            for (int k = 0; k < 2; k++)
+                v[k] = *reinterpret_cast<const halfx8 *>(&Vt[vbuf][k][32 * t + li][16 * st + 8 * lh]);
+        };
+        read(0, vp[0]);
+#pragma unroll
+        for (int step = 0; step < 4; step++) {
+            if (step < 3) read(step + 1, vp[(step + 1) & 1]);
+            const int st = step >> 1, t = step & 1;
+            const halfx8(&v)[2] = vp[step & 1];
+            const halfx8 &ph = pp[st][0], &pm = pp[st][1];
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v[1], ph, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v[0], pm, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v[0], ph, o[t], 0, 0, 0);
+        }
+    };
+
+    // Pipeline over key blocks kb = 0 .. nkb-1.  Entering iteration kb:
+    // Ks[(kb+1)%2] holds K(kb+1), Vt[kb%2] holds V(kb), the stage registers
+    // hold the loads of K(kb+2) and V(kb+1), and S holds block kb's scores
+    // with its maximum applied.  The iteration computes block kb+1's scores
+    // (their MFMAs run beside block kb's exponentials), accumulates block
+    // kb's P V, stages K(kb+2) into Ks[kb%2] and V(kb+1) into Vt[(kb+1)%2]
+    // (read last in iteration kb-1), issues the loads of K(kb+3) and
+    // V(kb+2), and after the barrier applies block kb+1's maximum.  Blocks
+    // past the last are computed from staged zeros and never used.
+    const int nkb = (a.L + ATT_KB - 1) / ATT_KB;
+    Stage st;
+    load(st, 0, 0);
+    store(st, 0, 0, true);
+    load(st, 1, 1);
+    store(st, 1, 0, false);
+    load(st, 2, 1);
+    __syncthreads();
+    auto run = [&](auto active_c) {
+        constexpr bool ACTIVE = decltype(active_c)::value;
+        floatx16 s0, s1;
+        if constexpr (ACTIVE) {
+            s0 = qk(0);
+            soft_max(s0, 0);
+        }
+        __syncthreads();  // every wave has read K(0): iteration 0 restages Ks[0]
+        auto iteration = [&](int kb, floatx16 &sc, floatx16 &sn) {
+            if constexpr (ACTIVE) {
+                sn = qk((kb + 1) & 1);
+                soft_pv(sc, kb & 1);
+            }
+            store(st, kb + 2, kb + 1, true);
+            load(st, kb + 3, kb + 2);
+            __syncthreads();
+            if constexpr (ACTIVE) {
+                if (kb + 1 < nkb) soft_max(sn, kb + 1);
+            }
+        };
+        for (int kb = 0; kb < nkb; kb += 2) {
+            iteration(kb, s0, s1);
+            if (kb + 1 < nkb) iteration(kb + 1, s1, s0);
+        }
+    };
+    if (q0 < a.L) run(std::true_type());
+    else {
+        run(std::false_type());
+        return;
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const int q = q0 + li;
+    if (q >= a.L) return;
+    const float inv = (1.0f / l_tot) * o_unscale;
+    const int row = attn_row(a, s, q);
+    const float gate = a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f;
+    TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            floatx4 v;
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = (o[t][4 * rq + r] * inv) * gate;
+            st4(op + 32 * t + 8 * rq + 4 * lh, v);
+        }
+}
+
+}  // namespace vh

@@ -12,6 +12,7 @@
 #include "attention.hpp"
 #include "attention_bf16.hpp"
 #include "attention_split.hpp"
+#include "attention_h2.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
 #include "gemm_bf16.hpp"
@@ -648,6 +649,20 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
                                (last_row + 1) * a.ld * 4 <= (int64_t)UINT32_MAX &&
                                (int64_t)a.pos_stride * a.ld * 4 < (1 << 24);
             auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, dim3(grid), block, 0, s, a); };
+            if (a.bound) {  // fp16 two-piece products
+                if (a.rope) {
+                    if (out_bf16) off32 ? go(attention_h2_kernel<WAVES, bf16, true, true>)
+                                        : go(attention_h2_kernel<WAVES, bf16, true, false>);
+                    else off32 ? go(attention_h2_kernel<WAVES, float, true, true>)
+                               : go(attention_h2_kernel<WAVES, float, true, false>);
+                } else {
+                    if (out_bf16) off32 ? go(attention_h2_kernel<WAVES, bf16, false, true>)
+                                        : go(attention_h2_kernel<WAVES, bf16, false, false>);
+                    else off32 ? go(attention_h2_kernel<WAVES, float, false, true>)
+                               : go(attention_h2_kernel<WAVES, float, false, false>);
+                }
+                return;
+            }
             if (a.rope) {
                 if (out_bf16) off32 ? go(attention_split_kernel<WAVES, bf16, true, true>)
                                     : go(attention_split_kernel<WAVES, bf16, true, false>);
@@ -672,7 +687,7 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
 }
 
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
-               int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split) {
+               int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split, const float *bound) {
     if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
@@ -683,6 +698,7 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     a.S = lay.S; a.L = lay.L; a.H = heads;
     a.group = lay.group; a.group_stride = lay.group_stride; a.seq_stride = lay.seq_stride; a.pos_stride = lay.pos_stride;
     a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
+    a.bound = split && !qkv_bf16 ? bound : nullptr;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
     if (lay.L <= 64 && !qkv_bf16) {
         // persistent: four workgroups per CU loop over the (sequence, head) tasks
@@ -826,7 +842,8 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     if (!lin(normed, D, w.wqkvg, w.wqkvg_p, 0, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
     // rotary + attention + gates (long sequences: products as split bf16 on
     // the default fp32 path)
-    if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32))
+    if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32,
+                   w.bounds ? w.bounds + 1 : nullptr))
         return false;
     // out projection added to the residual stream
     if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;

@@ -214,13 +214,21 @@ extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *
 
 extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                             int apply_rotary, int flags) {
-    if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16 | VH_ATT_SPLIT))) return 0;
+    if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16 | VH_ATT_SPLIT | VH_ATT_H2))) return 0;
     const float *rt = nullptr;
     if (apply_rotary && !ctx->rope.get_interleaved(length, 64, ctx->stream, &rt)) return 0;
     const int inner = heads * 64;
+    const bool h2 = (flags & VH_ATT_H2) && !(flags & VH_ATT_BF16);
+    if (h2) {  // the operands' own maximum bounds them
+        if (sequences <= 0 || length <= 0 || heads <= 0 || !qkv ||
+            !ctx->bounds.ensure((64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bound)") ||
+            !absmax(ctx->stream, static_cast<const float *>(qkv), (int64_t)sequences * length * 3 * inner,
+                    ctx->bounds.f() + 64, ctx->bounds.f()))
+            return 0;
+    }
     return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
                      &ctx->timer, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0,
-                     (flags & VH_ATT_SPLIT) != 0)
+                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2 ? ctx->bounds.f() : nullptr)
                ? 1
                : 0;
 }

@@ -33,7 +33,7 @@ ABI_SYMBOLS = [
 EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16, PRECISION_FP32_MFMA = 0, 1, 2
 BF16_A, BF16_C, BF16_STAGED = 1, 2, 4  # vh_gemm_bf16 operand flags; STAGED forces the register-staged kernel
-ATT_OUT_BF16, ATT_BF16, ATT_SPLIT = 1, 2, 4  # vh_attention flags
+ATT_OUT_BF16, ATT_BF16, ATT_SPLIT, ATT_H2 = 1, 2, 4, 8  # vh_attention flags
 SPEC_REFERENCE, SPEC_FRAME_MAJOR = 0, 1  # spectrum layouts: [F][C][T][2] / [C][T][F][2]
 
 _P = ctypes.c_void_p
@@ -227,10 +227,12 @@ class Context:
         _ok(lib().vh_to_bf16(self.h, rows, cols, ptr(src), ptr(dst), ld), "vh_to_bf16")
 
     def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True, out_bf16: bool = False,
-                  bf16: bool = False, split: bool = False):
+                  bf16: bool = False, split: bool = False, h2: bool = False):
         """bf16: qkv is bf16 and the bf16-MFMA kernel runs; out_bf16: out is bf16; split: fp32 accuracy on the
-        bf16 matrix cores (length > 64)."""
-        flags = (ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0) | (ATT_SPLIT if split else 0)
+        bf16 matrix cores (three-piece splits); h2: fp32 accuracy on the fp16 matrix cores (two-piece splits,
+        scales from max|qkv|); both for length > 64."""
+        flags = ((ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0) | (ATT_SPLIT if split else 0) |
+                 (ATT_H2 if h2 else 0))
         _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), flags),
             "vh_attention")
 
