@@ -55,6 +55,13 @@ const char *vh_device_name(vh_context *ctx);
 int vh_rmsnorm(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, float *y);
 /* Same, y written as bf16 (round to nearest even): the bf16 variant's GEMM operand. */
 int vh_rmsnorm_bf16(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, void *y);
+/* Same, y written as h2 rows for vh_gemm_h2 with VH_H2_A_ROWS: the values
+   times 2^e (e: the largest with bound * 2^e < 2^14, bound the device float
+   *bound, e.g. vh_operand_bounds' out[0]) split into fp16 pieces h, m; every
+   16 k of a row take the row's 64 fp32 bytes: h of k 0-3, 8-11 | h of k 4-7,
+   12-15 | m of k 0-3, 8-11 | m of k 4-7, 12-15 (dim a multiple of 16). */
+int vh_rmsnorm_h2(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma, const float *bound,
+                  float *y);
 /* Row softmax over [rows][len] (native/native_gpu_cuda.cu:357-381). */
 int vh_softmax_rows(vh_context *ctx, int64_t rows, int len, const float *in, float *out);
 /* Rotary embedding in place on [bh][len][dim_head] with base 10000
@@ -109,8 +116,9 @@ int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, 
    K a multiple of 16, lda a multiple of 4 and at most 2^21, A 16-byte
    aligned.  The token-wise linear of native/vocalarc_separation.c:631-636,
    as vh_gemm; the default fp32 path's linears. */
+#define VH_H2_A_ROWS 1 /* flags of vh_gemm_h2: A given as h2 rows (vh_rmsnorm_h2), scaled from a_bound */
 int vh_gemm_h2(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, float a_bound, const void *Wp,
-               const float *bias, float *C, int ldc, int epilogue);
+               const float *bias, float *C, int ldc, int epilogue, int flags);
 /* Bytes of the fp16 pieces of an N x K weight: a 256-byte header, then two
    planes (N rounded up to 128 rows). */
 size_t vh_h2_bytes(int N, int K);

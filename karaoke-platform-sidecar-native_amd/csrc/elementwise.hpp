@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "h2.hpp"
 
 namespace vh {
 
@@ -37,6 +38,41 @@ static __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__rest
     for (int i = 0; i < MAXV; i++) {
         const int c = lane + 64 * i;
         if (c < nv) st4(yr + 4 * c, (v[i] * inv) * ld4(gamma + 4 * c));
+    }
+}
+
+// The same RMSNorm writing y as h2 rows (h2.hpp) scaled by
+// 2^h2_exponent(*bound): the A operand of the fp16 two-piece GEMMs, split
+// once here instead of in every column tile of the GEMM.  dim a multiple of
+// 16; ldy in fp32 units (an h2 row takes the bytes of its fp32 row).
+template <int MAXV>
+static __global__ __launch_bounds__(256) void rmsnorm_h2_kernel(const float *__restrict__ x, int ldx,
+                                                               const float *__restrict__ gamma,
+                                                               float *__restrict__ y, int ldy, int rows, int dim,
+                                                               const float *__restrict__ bound) {
+    const int row = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
+    const int lane = (int)threadIdx.x & 63;
+    if (row >= rows) return;
+    const float s = ldexpf(1.0f, h2_exponent(*bound));
+    const float *xr = x + (size_t)row * ldx;
+    unsigned char *yr = reinterpret_cast<unsigned char *>(y + (size_t)row * ldy);
+    const int nv = dim >> 2;
+    floatx4 v[MAXV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) {
+        const int c = lane + 64 * i;
+        if (c < nv) {
+            v[i] = ld4(xr + 4 * c);
+            ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = sqrtf((float)dim) / sqrtf(ss + 1.0e-12f);
+#pragma unroll
+    for (int i = 0; i < MAXV; i++) {
+        const int c = lane + 64 * i;
+        if (c < nv) store4_h2(yr + 64 * (c >> 2), c & 3, (v[i] * inv) * ld4(gamma + 4 * c), s);
     }
 }
 

@@ -40,10 +40,9 @@
 #pragma once
 
 #include "gemm_split.hpp"
+#include "h2.hpp"
 
 namespace vh {
-
-typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
 struct GemmDescH2 {
     const float *A;  // fp32 [M][lda]
@@ -62,41 +61,9 @@ struct H2Bound {
 constexpr int H2_HEADER = 256;                // bytes before the planes: float max|W|
 constexpr int H2_WBLOCK = 2 * GS_BN * GS_BK;  // fp16 per (row tile, K chunk) block of W pieces
 
-// The exponent e with bound * 2^e < 2^14 (the largest such, clamped to
-// [-100, 100]); 0 for a zero, infinite or NaN bound.
-VH_HOST_DEVICE inline int h2_exponent(float bound) {
-    if (!(bound > 0.0f) || !(bound <= 3.4e38f)) return 0;
-    int E;
-    (void)frexpf(bound, &E);  // bound < 2^E
-    const int e = 14 - E;
-    return e < -100 ? -100 : (e > 100 ? 100 : e);
-}
-
-// Two fp32 -> two fp16 (nearest even) in one dword: one v_cvt_pk_f16_f32.
-VH_DEVICE uint32_t pack_f16x2(float a, float b) {
-    typedef float floatx2 __attribute__((ext_vector_type(2)));
-    typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, halfx2));
-}
-VH_DEVICE float f16_lo(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p & 0xffffu)); }
-VH_DEVICE float f16_hi(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p >> 16)); }
-
-// Eight fp32 values times s -> their h and m fp16 pieces, packed as the MFMA
-// operand wants them (a lane's eight k-values): 4 VALU per value.
-VH_DEVICE void split8_h2(floatx4 lo, floatx4 hi, float s, halfx8 &h, halfx8 &m) {
-    const float x[8] = {lo[0] * s, lo[1] * s, lo[2] * s, lo[3] * s, hi[0] * s, hi[1] * s, hi[2] * s, hi[3] * s};
-    uint32_t ph[4], pm[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        ph[e] = pack_f16x2(x[2 * e], x[2 * e + 1]);
-        pm[e] = pack_f16x2(x[2 * e] - f16_lo(ph[e]), x[2 * e + 1] - f16_hi(ph[e]));
-    }
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    h = __builtin_bit_cast(halfx8, (u32x4){ph[0], ph[1], ph[2], ph[3]});
-    m = __builtin_bit_cast(halfx8, (u32x4){pm[0], pm[1], pm[2], pm[3]});
-}
-
-template <int EPI>
+// A_H2: A arrives as h2 rows (h2.hpp) scaled by 2^h2_exponent(a_bound) -- its
+// producer split it -- and the K loop only reads the pieces.
+template <int EPI, bool A_H2>
 __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound, int tile) {
     constexpr int A_BYTES = GS_BM * GS_BK * 4;  // 16 KB: fp32 rows of 64 B
     constexpr int P_BYTES = GS_BN * GS_BK * 2;  // 4 KB per W plane: fp16 rows of 32 B
@@ -166,10 +133,16 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
             if (kt + 1 < nk) issue(kt + 1);
             const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
             const int r = wave * 32 + li;
-            const floatx4 lo = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * (lh ^ swz_a(r)));
-            const floatx4 hi = *reinterpret_cast<const floatx4 *>(sbuf + r * 64 + 16 * ((2 + lh) ^ swz_a(r)));
+            const unsigned char *ar = sbuf + r * 64;
             halfx8 ah, am;
-            split8_h2(lo, hi, a_scale, ah, am);
+            if constexpr (A_H2) {
+                ah = *reinterpret_cast<const halfx8 *>(ar + 16 * (lh ^ swz_a(r)));
+                am = *reinterpret_cast<const halfx8 *>(ar + 16 * ((2 + lh) ^ swz_a(r)));
+            } else {
+                const floatx4 lo = *reinterpret_cast<const floatx4 *>(ar + 16 * (lh ^ swz_a(r)));
+                const floatx4 hi = *reinterpret_cast<const floatx4 *>(ar + 16 * ((2 + lh) ^ swz_a(r)));
+                split8_h2(lo, hi, a_scale, ah, am);
+            }
             // W column tiles two at a time: their pieces, then (m,h) (h,m) (h,h)
 #pragma unroll
             for (int jp = 0; jp < (NJ + 1) / 2; jp++) {
@@ -207,9 +180,9 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh);
 }
 
-template <int EPI>
+template <int EPI, bool A_H2>
 __global__ __launch_bounds__(GS_THREADS, 2) void gemm_h2_kernel(GemmDescH2 d, H2Bound b) {
-    gemm_h2_body<EPI>(d, b.ptr ? *b.ptr : b.value, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+    gemm_h2_body<EPI, A_H2>(d, b.ptr ? *b.ptr : b.value, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
 // Ragged batch (the mask estimator's per-band linears): problem blockIdx.z,
@@ -221,7 +194,7 @@ struct GemmBatchH2 {
 
 template <int EPI>
 __global__ __launch_bounds__(GS_THREADS, 2) void gemm_h2_batched_kernel(GemmBatchH2 b) {
-    gemm_h2_body<EPI>(b.d[blockIdx.z], b.b.ptr ? *b.b.ptr : b.b.value, (int)blockIdx.x);
+    gemm_h2_body<EPI, false>(b.d[blockIdx.z], b.b.ptr ? *b.b.ptr : b.b.value, (int)blockIdx.x);
 }
 
 // max |W| over W [N][ldw] (first K columns) into out[0]; one workgroup of

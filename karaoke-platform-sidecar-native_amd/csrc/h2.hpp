@@ -1,0 +1,76 @@
+// Two-piece fp16 representation of fp32 values (the default fp32 path's
+// operands on the fp16 matrix cores): a value x of an operand whose elements
+// are all bounded by B is scaled by 2^e, e = h2_exponent(B) (so |x 2^e| < 2^14),
+// and y = x 2^e is held as h = fp16(y), m = fp16(y - h), both nearest even;
+// y - h is exact in fp32 and h + m carries 22 significant bits (exact to
+// 2^-25 absolute where m is subnormal).
+//
+// "h2 rows": a fp32 matrix [rows][K] (K a multiple of 16) re-encoded in place
+// of its fp32 bytes (the same row pitch): every chunk of 16 k-values of a row
+// is 64 bytes -- 16-byte slot 0 holds h of k 0-3 and 8-11, slot 1 h of k 4-7
+// and 12-15, slots 2 and 3 the same for m.  A lane of a 32x32x16 MFMA takes k
+// {4j..4j+3, 8+4j..8+4j+3} for its half j, so its h operand is slot j and its
+// m operand slot 2+j: one 16-byte read each, the read pattern of the fp32
+// rows the GEMMs split themselves.
+#pragma once
+
+#include "common.hpp"
+
+namespace vh {
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+
+// The exponent e with bound * 2^e < 2^14 (the largest such, clamped to
+// [-100, 100]); 0 for a zero, infinite or NaN bound.
+VH_HOST_DEVICE inline int h2_exponent(float bound) {
+    if (!(bound > 0.0f) || !(bound <= 3.4e38f)) return 0;
+    int E;
+    (void)frexpf(bound, &E);  // bound < 2^E
+    const int e = 14 - E;
+    return e < -100 ? -100 : (e > 100 ? 100 : e);
+}
+
+// Two fp32 -> two fp16 (nearest even) in one dword: one v_cvt_pk_f16_f32.
+VH_DEVICE uint32_t pack_f16x2(float a, float b) {
+    typedef float floatx2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, halfx2));
+}
+VH_DEVICE float f16_lo(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p & 0xffffu)); }
+VH_DEVICE float f16_hi(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p >> 16)); }
+
+// Eight fp32 values times s -> their h and m fp16 pieces, packed as the MFMA
+// operand wants them (a lane's eight k-values): 4 VALU per value.
+VH_DEVICE void split8_h2(floatx4 lo, floatx4 hi, float s, halfx8 &h, halfx8 &m) {
+    const float x[8] = {lo[0] * s, lo[1] * s, lo[2] * s, lo[3] * s, hi[0] * s, hi[1] * s, hi[2] * s, hi[3] * s};
+    uint32_t ph[4], pm[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        ph[e] = pack_f16x2(x[2 * e], x[2 * e + 1]);
+        pm[e] = pack_f16x2(x[2 * e] - f16_lo(ph[e]), x[2 * e + 1] - f16_hi(ph[e]));
+    }
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    h = __builtin_bit_cast(halfx8, (u32x4){ph[0], ph[1], ph[2], ph[3]});
+    m = __builtin_bit_cast(halfx8, (u32x4){pm[0], pm[1], pm[2], pm[3]});
+}
+
+// Byte offsets, inside the 64-byte chunk of an h2 row, of the h piece of the
+// four consecutive k-values 4j..4j+3 (j = 0..3 within the chunk); the m
+// piece lies 32 bytes further.
+VH_HOST_DEVICE inline int h2_row_offset(int j) { return 16 * (j & 1) + 8 * (j >> 1); }
+
+// Four consecutive values (k 4j..4j+3 of the chunk at `chunk`) times s into
+// an h2 row: 8 bytes of h and 8 of m.
+VH_DEVICE void store4_h2(unsigned char *chunk, int j, floatx4 v, float s) {
+    const float y0 = v[0] * s, y1 = v[1] * s, y2 = v[2] * s, y3 = v[3] * s;
+    const uint32_t h01 = pack_f16x2(y0, y1), h23 = pack_f16x2(y2, y3);
+    const uint32_t m01 = pack_f16x2(y0 - f16_lo(h01), y1 - f16_hi(h01));
+    const uint32_t m23 = pack_f16x2(y2 - f16_lo(h23), y3 - f16_hi(h23));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const int o = h2_row_offset(j);
+    *reinterpret_cast<u32x2 *>(chunk + o) = u32x2{h01, h23};
+    *reinterpret_cast<u32x2 *>(chunk + 32 + o) = u32x2{m01, m23};
+}
+
+}  // namespace vh

@@ -431,8 +431,9 @@ static GemmDescH2 to_desc_h2(const GemmArgsH2 &g) {
 }
 
 template <int EPI>
-static void launch_h2(hipStream_t s, const GemmDescH2 &d, const H2Bound &b, unsigned tiles) {
-    hipLaunchKernelGGL(gemm_h2_kernel<EPI>, dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
+static void launch_h2(hipStream_t s, const GemmDescH2 &d, const H2Bound &b, unsigned tiles, bool a_h2) {
+    if (a_h2) hipLaunchKernelGGL((gemm_h2_kernel<EPI, true>), dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
+    else hipLaunchKernelGGL((gemm_h2_kernel<EPI, false>), dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
 }
 
 bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int epilogue, KernelTimer *t,
@@ -446,11 +447,11 @@ bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int 
     const unsigned tiles = (unsigned)(((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
     Scope sc(t, s, name);
     switch (epilogue) {
-        case EPI_STORE: launch_h2<EPI_STORE>(s, d, b, tiles); break;
-        case EPI_GELU: launch_h2<EPI_GELU>(s, d, b, tiles); break;
-        case EPI_TANH: launch_h2<EPI_TANH>(s, d, b, tiles); break;
-        case EPI_RESIDUAL: launch_h2<EPI_RESIDUAL>(s, d, b, tiles); break;
-        case EPI_GEGLU: launch_h2<EPI_GEGLU>(s, d, b, tiles); break;
+        case EPI_STORE: launch_h2<EPI_STORE>(s, d, b, tiles, g.a_h2); break;
+        case EPI_GELU: launch_h2<EPI_GELU>(s, d, b, tiles, g.a_h2); break;
+        case EPI_TANH: launch_h2<EPI_TANH>(s, d, b, tiles, g.a_h2); break;
+        case EPI_RESIDUAL: launch_h2<EPI_RESIDUAL>(s, d, b, tiles, g.a_h2); break;
+        case EPI_GEGLU: launch_h2<EPI_GEGLU>(s, d, b, tiles, g.a_h2); break;
         default: set_error("unknown GEMM epilogue %d", epilogue); return false;
     }
     return sync_debug(s, "gemm_h2_kernel");
@@ -557,6 +558,22 @@ static bool rmsnorm_any(hipStream_t s, const float *x, int ldx, const float *gam
     else if (nv <= 256) hipLaunchKernelGGL((rmsnorm_kernel<4, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
     else hipLaunchKernelGGL((rmsnorm_kernel<8, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
     return sync_debug(s, "rmsnorm_kernel");
+}
+
+bool rmsnorm_h2(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
+                const float *bound, KernelTimer *t) {
+    if (dim % 16 || dim > 2048 || rows <= 0 || rows > INT32_MAX / 2 || !bound) {
+        set_error("rmsnorm_h2: unsupported dim %d", dim);
+        return false;
+    }
+    Scope sc(t, s, "rmsnorm");
+    const unsigned grid = blocks_for(rows, 4);
+    const int nv = dim / 4;
+    if (nv <= 64) hipLaunchKernelGGL((rmsnorm_h2_kernel<1>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
+    else if (nv <= 128) hipLaunchKernelGGL((rmsnorm_h2_kernel<2>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
+    else if (nv <= 256) hipLaunchKernelGGL((rmsnorm_h2_kernel<4>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
+    else hipLaunchKernelGGL((rmsnorm_h2_kernel<8>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
+    return sync_debug(s, "rmsnorm_h2_kernel");
 }
 
 bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
@@ -829,28 +846,40 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
         return lin(hid, d.ff_dim, w.w2_h, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, false, "gemm_ff2");
     }
     // fp32 linears: fp16 two-piece planes on the matrix cores (A bounded by
-    // bounds[slot]), or the fp32 MFMA GEMM
+    // bounds[slot]; a_h2: A arrives split by its producer), or the fp32 MFMA GEMM
+    auto use_h2 = [&](const void *Wp, int K) {
+        return Wp && w.bounds && precision == PREC_FP32 && K % SPLIT_K_MULTIPLE == 0;
+    };
     auto lin = [&](const float *A, int lda, const float *W, const void *Wp, int slot, const float *bias, float *C,
-                   int ldc, int N, int K, int epi, const char *name) {
-        if (Wp && w.bounds && precision == PREC_FP32 && K % SPLIT_K_MULTIPLE == 0)
-            return gemm_h2(s, {A, lda, Wp, bias, C, ldc, tokens, N, K}, OperandBound{w.bounds + slot, 0.0f}, epi, t,
-                           name);
+                   int ldc, int N, int K, int epi, bool a_h2, const char *name) {
+        if (use_h2(Wp, K)) {
+            GemmArgsH2 g{A, lda, Wp, bias, C, ldc, tokens, N, K};
+            g.a_h2 = a_h2;
+            return gemm_h2(s, g, OperandBound{w.bounds + slot, 0.0f}, epi, t, name);
+        }
         return gemm(s, {A, lda, W, K, bias, C, ldc, tokens, N, K}, epi, t, name);
     };
-    // pre-norm -> fused QKV (+gate logits with their bias)
-    if (!rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)) return false;
-    if (!lin(normed, D, w.wqkvg, w.wqkvg_p, 0, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, "gemm_qkv")) return false;
-    // rotary + attention + gates (long sequences: products as split bf16 on
-    // the default fp32 path)
+    // pre-norm (split into fp16 pieces for the two-piece GEMM) -> fused QKV
+    // (+gate logits with their bias)
+    const bool qkv_h2 = use_h2(w.wqkvg_p, D);
+    if (!(qkv_h2 ? rmsnorm_h2(s, x, D, w.gamma, normed, D, tokens, D, w.bounds, t)
+                 : rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)))
+        return false;
+    if (!lin(normed, D, w.wqkvg, w.wqkvg_p, 0, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, qkv_h2, "gemm_qkv")) return false;
+    // rotary + attention + gates (long sequences: products as fp16 two-piece
+    // splits on the default fp32 path)
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32,
                    w.bounds ? w.bounds + 1 : nullptr))
         return false;
     // out projection added to the residual stream
-    if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, "gemm_out")) return false;
+    if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;
     // FFN
-    if (!rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)) return false;
-    if (!lin(normed, D, w.w1, w.w1_p, 2, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, "gemm_ff1")) return false;
-    return lin(hid, d.ff_dim, w.w2, w.w2_p, 3, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, "gemm_ff2");
+    const bool ff1_h2 = use_h2(w.w1_p, D);
+    if (!(ff1_h2 ? rmsnorm_h2(s, x, D, w.ff_gamma, normed, D, tokens, D, w.bounds + 2, t)
+                 : rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)))
+        return false;
+    if (!lin(normed, D, w.w1, w.w1_p, 2, w.b1, hid, d.ff_dim, d.ff1_out(), D, ff1_epi, ff1_h2, "gemm_ff1")) return false;
+    return lin(hid, d.ff_dim, w.w2, w.w2_p, 3, w.b2, x, D, D, d.ff_dim, EPI_RESIDUAL, false, "gemm_ff2");
 }
 
 // ---------------------------------------------------------------- upload

@@ -138,6 +138,7 @@ struct GemmArgsH2 {
     const float *bias;
     float *C; int ldc;
     int64_t M; int N, K;
+    bool a_h2 = false;  // A given as h2 rows (h2.hpp) scaled from the same bound
 };
 struct OperandBound {
     const float *dev = nullptr;
@@ -175,6 +176,10 @@ bool rmsnorm(hipStream_t s, const float *x, int ldx, const float *gamma, float *
 // Same, bf16 output (y is bf16 [rows][ldy]).
 bool rmsnorm_bf16(hipStream_t s, const float *x, int ldx, const float *gamma, void *y, int ldy, int64_t rows, int dim,
                   KernelTimer *t = nullptr);
+// Same, y written as h2 rows (h2.hpp) scaled by 2^h2_exponent(*bound) for a
+// fp16 two-piece GEMM with a_h2 (dim a multiple of 16).
+bool rmsnorm_h2(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
+                const float *bound, KernelTimer *t = nullptr);
 bool softmax_rows(hipStream_t s, const float *in, float *out, int64_t rows, int len, KernelTimer *t = nullptr);
 bool rope_bhld(hipStream_t s, float *x, const float *cs, const float *sn, int64_t bh, int len,
                KernelTimer *t = nullptr);

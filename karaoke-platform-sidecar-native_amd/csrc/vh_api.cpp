@@ -114,6 +114,12 @@ extern "C" int vh_rmsnorm_bf16(vh_context *ctx, int64_t rows, int dim, const flo
     return rmsnorm_bf16(ctx->stream, x, dim, gamma, y, dim, rows, dim, &ctx->timer) ? 1 : 0;
 }
 
+extern "C" int vh_rmsnorm_h2(vh_context *ctx, int64_t rows, int dim, const float *x, const float *gamma,
+                             const float *bound, float *y) {
+    if (!ctx) return 0;
+    return rmsnorm_h2(ctx->stream, x, dim, gamma, y, dim, rows, dim, bound, &ctx->timer) ? 1 : 0;
+}
+
 extern "C" int vh_softmax_rows(vh_context *ctx, int64_t rows, int len, const float *in, float *out) {
     if (!ctx) return 0;
     return softmax_rows(ctx->stream, in, out, rows, len, &ctx->timer) ? 1 : 0;
@@ -173,10 +179,15 @@ extern "C" int vh_split_weights(vh_context *ctx, int N, int K, const float *W, i
 }
 
 extern "C" int vh_gemm_h2(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, float a_bound,
-                          const void *Wp, const float *bias, float *C, int ldc, int epilogue) {
-    if (!ctx) return 0;
+                          const void *Wp, const float *bias, float *C, int ldc, int epilogue, int flags) {
+    if (!ctx || (flags & ~VH_H2_A_ROWS)) return 0;
     GemmArgsH2 g{A, lda, Wp, bias, C, ldc, M, N, K};
+    g.a_h2 = (flags & VH_H2_A_ROWS) != 0;
     OperandBound b{nullptr, a_bound};
+    if (g.a_h2 && !(a_bound > 0.0f)) {
+        set_error("vh_gemm_h2: h2 rows need the bound they were split with");
+        return 0;
+    }
     if (!(a_bound > 0.0f)) {
         // the caller gave no bound: A's own maximum
         if (M <= 0 || K <= 0 || lda < K || !A) {

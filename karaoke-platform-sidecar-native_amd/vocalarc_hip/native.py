@@ -19,7 +19,7 @@ LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
 # Every entry point declared in include/vocalarc_hip.h and include/native_gpu.h.
 HARNESS_SYMBOLS = [
     "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
-    "vh_rmsnorm", "vh_rmsnorm_bf16", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
+    "vh_rmsnorm", "vh_rmsnorm_bf16", "vh_rmsnorm_h2", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
     "vh_gemm_split", "vh_split_bytes", "vh_split_weights", "vh_gemm_h2", "vh_h2_bytes", "vh_split_weights_h2", "vh_operand_bounds", "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
     "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
 ]
@@ -58,6 +58,7 @@ def lib():
         "vh_create": (_P, []), "vh_destroy": (None, [_P]), "vh_set_stream": (_I, [_P, _P]),
         "vh_synchronize": (_I, [_P]), "vh_last_error": (ctypes.c_char_p, []), "vh_device_name": (ctypes.c_char_p, [_P]),
         "vh_rmsnorm": (_I, [_P, _I64, _I, _P, _P, _P]), "vh_rmsnorm_bf16": (_I, [_P, _I64, _I, _P, _P, _P]),
+        "vh_rmsnorm_h2": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
         "vh_softmax_rows": (_I, [_P, _I64, _I, _P, _P]),
         "vh_rope_bhld": (_I, [_P, _I64, _I, _I, _P]),
         "vh_geglu": (_I, [_P, _I64, _I, _P, _P]),
@@ -67,7 +68,7 @@ def lib():
         "vh_gemm_split": (_I, [_P, _I64, _I, _I, _P, _I, _P, _P, _P, _I, _I]),
         "vh_split_bytes": (ctypes.c_size_t, [_I, _I]),
         "vh_split_weights": (_I, [_P, _I, _I, _P, _I, _P]),
-        "vh_gemm_h2": (_I, [_P, _I64, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _I, _I]),
+        "vh_gemm_h2": (_I, [_P, _I64, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _I, _I, _I]),
         "vh_h2_bytes": (ctypes.c_size_t, [_I, _I]),
         "vh_split_weights_h2": (_I, [_P, _I, _I, _P, _I, _P]),
         "vh_operand_bounds": (_I, [_P, _P, _I, _P, _I, _P, _I, _P]),
@@ -160,6 +161,10 @@ class Context:
     def rmsnorm_bf16(self, x, gamma, y, rows: int, dim: int):
         _ok(lib().vh_rmsnorm_bf16(self.h, rows, dim, ptr(x), ptr(gamma), ptr(y)), "vh_rmsnorm_bf16")
 
+    def rmsnorm_h2(self, x, gamma, bound, y, rows: int, dim: int):
+        """y as h2 rows (fp16 pieces of y * 2^e, e from the device float bound[0]) for gemm_h2(a_rows=True)."""
+        _ok(lib().vh_rmsnorm_h2(self.h, rows, dim, ptr(x), ptr(gamma), ptr(bound), ptr(y)), "vh_rmsnorm_h2")
+
     def softmax_rows(self, x, y, rows: int, length: int):
         _ok(lib().vh_softmax_rows(self.h, rows, length, ptr(x), ptr(y)), "vh_softmax_rows")
 
@@ -211,11 +216,13 @@ class Context:
         _ok(lib().vh_split_weights_h2(self.h, N, K, ptr(W), ldw_in or K, ptr(Wp)), "vh_split_weights_h2")
 
     def gemm_h2(self, A, Wp, C, M: int, N: int, K: int, bias=None, epilogue: int = EPI_STORE,
-                lda: int | None = None, ldc: int | None = None, a_bound: float = 0.0):
-        """fp32-accurate linear on fp16 matrix cores; Wp from split_weights_h2; a_bound bounds |A| (0: max|A|)."""
+                lda: int | None = None, ldc: int | None = None, a_bound: float = 0.0, a_rows: bool = False):
+        """fp32-accurate linear on fp16 matrix cores; Wp from split_weights_h2; a_bound bounds |A| (0: max|A|);
+        a_rows: A is given as h2 rows split with a_bound (rmsnorm_h2)."""
         _ok(lib().vh_gemm_h2(self.h, M, N, K, ptr(A), lda or K, float(a_bound), ptr(Wp),
                              ptr(bias) if bias is not None else None, ptr(C),
-                             ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm_h2")
+                             ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue, 1 if a_rows else 0),
+            "vh_gemm_h2")
 
     def operand_bounds(self, gamma, D: int, out, W=None, N: int = 0, bias=None, square: bool = False):
         """Device bounds out[0..1] of the A operands after an RMSNorm with gain gamma (see vh_operand_bounds)."""

@@ -232,3 +232,52 @@ def test_operand_bounds(ctx, rng, square):
     no_w = torch.full((2,), 7.0, device="cuda:0")
     ctx.operand_bounds(to_dev(gamma), D, no_w)
     assert from_dev(no_w)[1] == 0.0
+
+
+def _decode_h2_rows(raw: np.ndarray, rows: int, dim: int) -> tuple[np.ndarray, np.ndarray]:
+    """h, m [rows][dim] from h2 rows (fp16 view of the buffer, 2*dim halves per row)."""
+    r = raw.reshape(rows, dim // 16, 32)
+    k = np.arange(16)
+    pos = _slot(k)  # position of k inside its 16: slot 8*s + element e
+    return r[:, :, pos].reshape(rows, dim).astype(np.float32), r[:, :, 16 + pos].reshape(rows, dim).astype(np.float32)
+
+
+def test_rmsnorm_h2_rows_and_gemm(ctx, rng):
+    """The RMSNorm's h2 rows are the fp16 pieces of the fp32 RMSNorm output
+    times 2^e (e from the gain bound), at the documented positions; a GEMM
+    fed those rows gives the same bits as the GEMM splitting the fp32 output
+    itself with the same bound."""
+    rows, D, N = 1000, 384, 1568
+    x = (rng.standard_normal((rows, D)) * np.exp(rng.standard_normal((rows, 1)))).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    dx, dg = to_dev(x), to_dev(gamma)
+    bound = torch.zeros(2, device="cuda:0")
+    ctx.operand_bounds(dg, D, bound)
+    y = empty_dev((rows, D))
+    ctx.rmsnorm(dx, dg, y, rows, D)
+    yh = torch.full((rows, D), 7.0, device="cuda:0")
+    ctx.rmsnorm_h2(dx, dg, bound, yh, rows, D)
+    torch.cuda.synchronize()
+    b = float(from_dev(bound)[0])
+    yf = from_dev(y)
+    assert np.abs(yf).max() <= b
+    e = _exponent(b)
+    h, m = _decode_h2_rows(yh.cpu().numpy().view(np.float16).ravel(), rows, D)
+    ys = yf * np.float32(2.0 ** e)
+    h_ref = ys.astype(np.float16).astype(np.float32)
+    m_ref = (ys - h_ref).astype(np.float16).astype(np.float32)
+    for got, want in ((h, h_ref), (m, m_ref)):
+        nz = want != 0
+        assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32))
+        assert np.all(got[~nz] == 0.0)
+    # the GEMM on the rows equals the GEMM splitting the fp32 values itself
+    w = (0.05 * rng.standard_normal((N, D))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    planes, db = _pieces(ctx, w), to_dev(bias)
+    c_rows, c_fp32 = empty_dev((rows, N)), empty_dev((rows, N))
+    ctx.gemm_h2(yh, planes, c_rows, rows, N, D, bias=db, a_bound=b, a_rows=True)
+    ctx.gemm_h2(y, planes, c_fp32, rows, N, D, bias=db, a_bound=b)
+    torch.cuda.synchronize()
+    assert torch.equal(c_rows, c_fp32)
+    with pytest.raises(native.NativeError, match="bound"):
+        ctx.gemm_h2(yh, planes, c_rows, rows, N, D, a_rows=True)  # rows need the bound they were split with
