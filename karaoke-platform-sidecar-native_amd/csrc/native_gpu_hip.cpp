@@ -99,13 +99,40 @@ struct native_gpu {
     bool transposed = false;   // physical [ll][ls]
     // mask + matmul scratch
     DeviceBuffer normed, hidden, proj, mask, io_in, io_out, tables;
-    // A-operand bounds of the fp16 two-piece GEMMs: [0..3] the current layer
-    // (layer_bounds), [4..5] the mask features, [6] a matmul input, then
-    // absmax scratch
+    // A-operand bounds of the fp16 two-piece GEMMs outside the layers: [4..5]
+    // the mask features, [6] a matmul input, then absmax scratch
     DeviceBuffer bounds;
     float *bound(int i) { return bounds.f() + i; }
     bool ensure_bounds() {
         return bounds.ensure((64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bounds)");
+    }
+    // Layer bounds per set of cached device tensors they derive from (gains,
+    // fused projection and its bias, FFN up matrix and its bias): computed
+    // once, dropped whenever a cached tensor is replaced.
+    struct LayerBounds {
+        const void *keys[6];
+        float *dev;
+    };
+    std::vector<LayerBounds> layer_bounds_cache;
+    void drop_layer_bounds() {
+        for (auto &b : layer_bounds_cache) (void)hipFree(b.dev);
+        layer_bounds_cache.clear();
+    }
+    float *bounds_of(const LayerWeights &L) {
+        const void *keys[6] = {L.gamma, L.wqkvg, L.bqkvg, L.ff_gamma, L.w1, L.b1};
+        for (auto &b : layer_bounds_cache)
+            if (memcmp(b.keys, keys, sizeof(keys)) == 0) return b.dev;
+        float *dev = nullptr;
+        if (!check(hipMalloc((void **)&dev, 4 * sizeof(float)), "hipMalloc(layer bounds)")) return nullptr;
+        if (!layer_bounds(stream, d, L, dev)) {
+            (void)hipFree(dev);
+            return nullptr;
+        }
+        LayerBounds e;
+        memcpy(e.keys, keys, sizeof(keys));
+        e.dev = dev;
+        layer_bounds_cache.push_back(e);
+        return dev;
     }
 
     // Report, disable for the rest of the process, and tell the host to
@@ -122,6 +149,7 @@ struct native_gpu {
             if (e.key == k && e.key2 == k2 && e.in == in && e.out == out && e.mode == mode) {
                 if (e.fp == fp) return &e;
                 // same address, different contents: a reloaded pack
+                drop_layer_bounds();
                 (void)hipFree(e.dev);
                 if (e.dev_bias) (void)hipFree(e.dev_bias);
                 if (e.dev_split) (void)hipFree(e.dev_split);
@@ -232,11 +260,10 @@ struct native_gpu {
         L.wout_p = const_cast<void *>(split(L.wout, d.inner(), D));
         L.w1_p = const_cast<void *>(split(L.w1, D, d.ff1_out()));
         L.w2_p = const_cast<void *>(split(L.w2, d.ff_dim, D));
-        // the bounds follow this call's gains and matrices (a few microseconds
-        // of device work, ordered before the layer's GEMMs on the stream)
-        if (!ensure_bounds() || !layer_bounds(stream, d, L, bound(0))) return false;
-        L.bounds = bound(0);
-        return true;
+        // the bounds of this layer's gains and matrices (computed on the
+        // first call that uses them, ordered before the GEMMs on the stream)
+        L.bounds = bounds_of(L);
+        return L.bounds != nullptr;
     }
 
     // ---- resident layout ----------------------------------------------------
@@ -301,6 +328,7 @@ extern "C" void native_gpu_destroy(native_gpu *gpu) {
         if (e.dev_split) (void)hipFree(e.dev_split);
     }
     gpu->cache.clear();
+    gpu->drop_layer_bounds();
     hipStream_t s = gpu->stream;
     delete gpu;  // buffers release themselves
     if (s) (void)hipStreamDestroy(s);

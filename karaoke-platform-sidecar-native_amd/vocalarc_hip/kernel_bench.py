@@ -162,7 +162,8 @@ def main() -> int:
 
     if "h2" in groups or "ff1" in groups:
         # the same four GEMMs as the default fp32 path runs them: fp16 two-piece
-        # splits (three products), A bounded by its maximum
+        # splits (three products); QKV and FFN up read A as RMSNorm h2 rows,
+        # the others split fp32 A bounded by its maximum
         M = 8 * 801 * 62
         shapes = (("gemm_h2_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
                   ("gemm_h2_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
@@ -177,8 +178,18 @@ def main() -> int:
             ctx.split_weights_h2(w, wp, N, K)
             b = torch.randn(N, device=dev, generator=g)
             c = torch.zeros(M, ocols, device=dev)
-            bound = float(a.abs().max())
-            ms = _event_time(lambda: ctx.gemm_h2(a, wp, c, M, N, K, bias=b, epilogue=epi, a_bound=bound),
+            rows = K == 384  # QKV and FFN up take their A as RMSNorm h2 rows, as in the model
+            if rows:
+                gamma = 1.0 + 0.02 * torch.randn(K, device=dev, generator=g)
+                bnd = torch.zeros(2, device=dev)
+                ctx.operand_bounds(gamma, K, bnd)
+                ah = torch.empty_like(a)
+                ctx.rmsnorm_h2(a, gamma, bnd, ah, M, K)
+                bound = float(bnd[0])
+                a = ah
+            else:
+                bound = float(a.abs().max())
+            ms = _event_time(lambda: ctx.gemm_h2(a, wp, c, M, N, K, bias=b, epilogue=epi, a_bound=bound, a_rows=rows),
                              max(3, reps // 4))
             gflop = 2.0 * M * K * N / 1e9
             _emit(name, ms, gflop=gflop, shape=f"M={M} K={K} N={N}",
