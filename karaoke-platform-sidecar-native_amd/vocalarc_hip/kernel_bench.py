@@ -228,6 +228,10 @@ def main() -> int:
                 ms = _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True, split=True), max(3, reps // 4))
                 _emit("attention_split", ms, gflop=gf, shape=f"S={S} L={L} H=8",
                       extra={"bf16_matrix_core_frac": round(6 * gf / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
+                # the default path's kernel: fp16 two-piece products (scales from max|qkv|)
+                ms = _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True, h2=True), max(3, reps // 4))
+                _emit("attention_h2", ms, gflop=gf, shape=f"S={S} L={L} H=8",
+                      extra={"matrix_core_frac": round(3 * gf / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
             del qkv, o
 
     if "c2" in groups or "c3" in groups:
