@@ -32,11 +32,14 @@
 // one costs precision only for elements more than 2^17 below it.
 //
 // Operands and pipeline as gemm_split.hpp (256x128 block, 8 waves of 32x128,
-// K chunks of 16 in a 2-chunk global->LDS DMA ring, A fp32 in LDS split by
-// each wave in registers): W's pieces are two fp16 planes per tile-major
-// block (8 KB per 128 rows x 16 k, the same row/slot permutation), one 1 KB
-// load per wave per chunk; 48 KB of LDS; per wave and chunk 12 MFMAs
-// (v_mfma_f32_32x32x16_f16) and 4 VALU per A value for the scale and split.
+// K chunks of 16 in a global->LDS DMA ring, A fp32 in LDS split by each wave
+// in registers, or h2 rows read as they are): W's pieces are two fp16 planes
+// per tile-major block (8 KB per 128 rows x 16 k, the same row/slot
+// permutation), one 1 KB load per wave per chunk; a 3-chunk ring (two chunks
+// in flight while one is multiplied: 72 KB of LDS, two workgroups per CU;
+// 0-2.4% faster than two chunks, bit-identical); per wave and chunk 12 MFMAs
+// (v_mfma_f32_32x32x16_f16) and, for fp32 A, 4 VALU per A value for the scale
+// and split.
 #pragma once
 
 #include "gemm_split.hpp"
@@ -63,12 +66,13 @@ constexpr int H2_WBLOCK = 2 * GS_BN * GS_BK;  // fp16 per (row tile, K chunk) bl
 
 // A_H2: A arrives as h2 rows (h2.hpp) scaled by 2^h2_exponent(a_bound) -- its
 // producer split it -- and the K loop only reads the pieces.
-template <int EPI, bool A_H2>
+// RING: K chunks held in LDS, RING - 1 of them in flight while one is multiplied.
+template <int EPI, bool A_H2, int RING = 3>
 __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound, int tile) {
     constexpr int A_BYTES = GS_BM * GS_BK * 4;  // 16 KB: fp32 rows of 64 B
     constexpr int P_BYTES = GS_BN * GS_BK * 2;  // 4 KB per W plane: fp16 rows of 32 B
     constexpr int STAGE_BYTES = A_BYTES + 2 * P_BYTES;
-    __shared__ __attribute__((aligned(1024))) unsigned char ring[2 * STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char ring[RING * STAGE_BYTES];
 
     const int tiles_n = (d.N + GS_BN - 1) / GS_BN;
     const int tiles_m = (d.M + GS_BM - 1) / GS_BM;
@@ -107,7 +111,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
                              (size_t)(n0 / GS_BN) * (d.K / GS_BK) * H2_WBLOCK;
     const uint32_t w_voff = 16 * lane;
     auto issue = [&](int kt) {
-        const uint32_t sb = ring_base + (kt & 1) * STAGE_BYTES;
+        const uint32_t sb = ring_base + (kt % RING) * STAGE_BYTES;
         const float *ab = a_base + kt * GS_BK;
         lds_dma16s(a_voff[0], ab, sb + wave * 1024);
         lds_dma16s(a_voff[1], ab, sb + (wave + 8) * 1024);
@@ -121,17 +125,25 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
         for (int r = 0; r < 16; r++) acc[0][j][r] = 0.0f;
 
     const int nk = d.K / GS_BK;
-    issue(0);
-    wait_vmcnt<0>();
+#pragma unroll
+    for (int i = 0; i < RING - 1; i++)
+        if (i < nk) issue(i);
+    if constexpr (RING > 2) {
+        if (nk > 1) wait_vmcnt<3 * (RING - 2)>();  // chunk 0 has landed
+        else wait_vmcnt<0>();
+    } else {
+        wait_vmcnt<0>();
+    }
     __syncthreads();
     // NJ live 32-column accumulators, chosen once per tile (as gemm_split_body)
     auto k_loop = [&](auto nj_c) {
         constexpr int NJ = decltype(nj_c)::value;
         for (int kt = 0; kt < nk; kt++) {
-            // chunk kt+1 goes to the slot chunk kt-1 used: every wave finished
-            // reading it before the barrier that ended the previous iteration
-            if (kt + 1 < nk) issue(kt + 1);
-            const unsigned char *sbuf = ring + (kt & 1) * STAGE_BYTES;
+            // chunk kt+RING-1 goes to the slot chunk kt-1 used: every wave
+            // finished reading it before the barrier that ended the previous
+            // iteration
+            if (kt + RING - 1 < nk) issue(kt + RING - 1);
+            const unsigned char *sbuf = ring + (kt % RING) * STAGE_BYTES;
             const int r = wave * 32 + li;
             const unsigned char *ar = sbuf + r * 64;
             halfx8 ah, am;
@@ -165,7 +177,13 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
                 for (int jj = 0; jj < NJJ; jj++)
                     acc[0][2 * jp + jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wh[jj], acc[0][2 * jp + jj], 0, 0, 0);
             }
-            wait_vmcnt<0>();  // chunk kt+1 has landed
+            // chunk kt+1 has landed (3 loads per wave and chunk; later chunks may fly)
+            if constexpr (RING > 2) {
+                if (kt + RING - 1 < nk) wait_vmcnt<3 * (RING - 2)>();
+                else wait_vmcnt<0>();
+            } else {
+                wait_vmcnt<0>();
+            }
             __syncthreads();
         }
     };
