@@ -115,22 +115,31 @@ struct native_gpu {
     };
     std::vector<LayerBounds> layer_bounds_cache;
     void drop_layer_bounds() {
-        for (auto &b : layer_bounds_cache) (void)hipFree(b.dev);
+        for (auto &b : layer_bounds_cache)
+            if (b.dev) (void)hipFree(b.dev);
         layer_bounds_cache.clear();
     }
-    float *bounds_of(const LayerWeights &L) {
+    float *bounds_of(const LayerWeights &L, bool *ok) {
         const void *keys[6] = {L.gamma, L.wqkvg, L.bqkvg, L.ff_gamma, L.w1, L.b1};
         for (auto &b : layer_bounds_cache)
             if (memcmp(b.keys, keys, sizeof(keys)) == 0) return b.dev;
         float *dev = nullptr;
+        *ok = false;
         if (!check(hipMalloc((void **)&dev, 4 * sizeof(float)), "hipMalloc(layer bounds)")) return nullptr;
         if (!layer_bounds(stream, d, L, dev)) {
             (void)hipFree(dev);
             return nullptr;
         }
+        const int usable = bounds_usable(stream, dev, 4);
+        if (usable <= 0) {  // beyond the scale range: the layer's linears run on fp32 MFMA
+            (void)hipFree(dev);
+            if (usable < 0) return nullptr;
+            dev = nullptr;
+        }
+        *ok = true;
         LayerBounds e;
         memcpy(e.keys, keys, sizeof(keys));
-        e.dev = dev;
+        e.dev = dev;  // null: recorded as unusable, so the check is not repeated
         layer_bounds_cache.push_back(e);
         return dev;
     }
@@ -261,9 +270,11 @@ struct native_gpu {
         L.w1_p = const_cast<void *>(split(L.w1, D, d.ff1_out()));
         L.w2_p = const_cast<void *>(split(L.w2, d.ff_dim, D));
         // the bounds of this layer's gains and matrices (computed on the
-        // first call that uses them, ordered before the GEMMs on the stream)
-        L.bounds = bounds_of(L);
-        return L.bounds != nullptr;
+        // first call that uses them; none when they are beyond the fp16
+        // two-piece scale range, and the fp32 MFMA GEMM runs)
+        bool ok = true;
+        L.bounds = bounds_of(L, &ok);
+        return ok;
     }
 
     // ---- resident layout ----------------------------------------------------
@@ -384,11 +395,15 @@ extern "C" int native_gpu_matmul(native_gpu *gpu, int64_t rows, int in, int out,
     const size_t ib = (size_t)rows * in * sizeof(float), ob = (size_t)rows * out * sizeof(float);
     hipStream_t s = gpu->stream;
     auto product = [&]() {
-        if (Ws)  // the input's own maximum bounds it
-            return gpu->ensure_bounds() &&
-                   absmax(s, gpu->io_in.f(), rows * in, gpu->bound(64), gpu->bound(6)) &&
-                   gemm_h2(s, {gpu->io_in.f(), in, Ws, B, gpu->io_out.f(), out, rows, out, in},
-                           OperandBound{gpu->bound(6), 0.0f}, EPI_STORE);
+        if (Ws) {  // the input's own maximum bounds it (beyond the scale range: fp32 MFMA)
+            if (!gpu->ensure_bounds() || !absmax(s, gpu->io_in.f(), rows * in, gpu->bound(64), gpu->bound(6)))
+                return false;
+            const int usable = bounds_usable(s, gpu->bound(6), 1);
+            if (usable < 0) return false;
+            if (usable)
+                return gemm_h2(s, {gpu->io_in.f(), in, Ws, B, gpu->io_out.f(), out, rows, out, in},
+                               OperandBound{gpu->bound(6), 0.0f}, EPI_STORE);
+        }
         return gemm(s, {gpu->io_in.f(), in, W, in, B, gpu->io_out.f(), out, rows, out, in}, EPI_STORE);
     };
     bool ok = gpu->io_in.ensure(ib, "hipMalloc(matmul input)") && gpu->io_out.ensure(ob, "hipMalloc(matmul output)") &&
@@ -505,7 +520,13 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
     if (!ok) return gpu->fail("mask buffers");
     std::vector<GemmArgs> g1, g2;
     std::vector<GemmArgsH2> s1, s2;  // the same products on the fp16 two-piece GEMM
-    bool sp = true;
+    // layer 1's A is the final RMSNorm's output: its bound from the gain
+    // (beyond the fp16 two-piece scale range: fp32 MFMA instead)
+    bool sp = gpu->ensure_bounds() && operand_bounds(s, gamma, D, nullptr, 0, nullptr, false, gpu->bound(4));
+    if (!sp) return gpu->fail("mask bounds");
+    const int usable = bounds_usable(s, gpu->bound(4), 1);
+    if (usable < 0) return gpu->fail("mask bounds");
+    sp = usable == 1;
     MaskTable tab;
     memset(&tab, 0, sizeof(tab));
     int64_t off = 0;
@@ -531,11 +552,9 @@ extern "C" int native_gpu_resident_mask(native_gpu *gpu, int frames, const float
         off += (int64_t)M * 2 * dim;
         maxdim = std::max(maxdim, dim);
     }
-    // layer 1's A: the final RMSNorm's output (bound from its gain); layer
-    // 2's A: tanh, within [-1, 1]
+    // layer 1's A bounded by bound(4); layer 2's A: tanh, within [-1, 1]
     ok = rmsnorm(s, gpu->x.f(), D, gamma, gpu->normed.f(), D, gpu->tokens, D) &&
-         (sp ? gpu->ensure_bounds() && operand_bounds(s, gamma, D, nullptr, 0, nullptr, false, gpu->bound(4)) &&
-                   gemm_h2_batched(s, s1, OperandBound{gpu->bound(4), 0.0f}, EPI_TANH) &&
+         (sp ? gemm_h2_batched(s, s1, OperandBound{gpu->bound(4), 0.0f}, EPI_TANH) &&
                    gemm_h2_batched(s, s2, OperandBound{nullptr, 1.0f}, EPI_STORE)
              : gemm_batched(s, g1, EPI_TANH) && gemm_batched(s, g2, EPI_STORE)) &&
          check(hipMemcpyAsync(gpu->tables.ptr, &tab, sizeof(tab), hipMemcpyHostToDevice, s), "hipMemcpy(mask table)");

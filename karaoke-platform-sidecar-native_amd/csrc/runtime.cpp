@@ -526,6 +526,16 @@ bool layer_bounds(hipStream_t s, const Dims &d, const LayerWeights &w, float *bo
            operand_bounds(s, w.ff_gamma, d.dim, w.w1, d.ff1_out(), w.b1, d.ffn_glu != 0, bounds + 2);
 }
 
+int bounds_usable(hipStream_t s, const float *dev, int n) {
+    float h[8];
+    if (n > 8 || !check(hipMemcpyAsync(h, dev, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpy(bounds)") ||
+        !check(hipStreamSynchronize(s), "hipStreamSynchronize(bounds)"))
+        return -1;
+    for (int i = 0; i < n; i++)
+        if (!(h[i] >= 0.0f && h[i] <= 1.0e30f)) return 0;  // NaN, infinite or beyond the scale range
+    return 1;
+}
+
 bool operand_bounds(hipStream_t s, const float *gamma, int D, const float *W, int N, const float *b, bool square,
                     float *out) {
     if (!gamma || D <= 0 || (W && N <= 0) || !out) {

@@ -239,6 +239,10 @@ struct LayerWeights {
 // bounds[0..3] (operand_bounds on its two RMSNorm gains and the matrices they
 // feed; the attention output is bounded by the fused projection's bound).
 bool layer_bounds(hipStream_t s, const Dims &d, const LayerWeights &w, float *bounds);
+// Reads n (<= 8) device bounds back: 1 when all are finite and within the
+// fp16 two-piece scale range (<= 1e30), 0 when not (those products then run
+// on the fp32 MFMA instruction), -1 on a runtime error.  Synchronous.
+int bounds_usable(hipStream_t s, const float *dev, int n);
 
 // Arithmetic of the matrix products.  PREC_FP32 (the parity path): fp32
 // accuracy, the transformer linears on fp16 matrix cores by two-piece operand

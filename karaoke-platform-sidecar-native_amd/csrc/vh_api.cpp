@@ -479,6 +479,8 @@ bool prepare_split(vh_model *m) {
     if (!m->bounds.ensure((4 * m->layers.size() + 64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bounds)"))
         return false;
     if (!operand_bounds(s, m->final_gamma, D, nullptr, 0, nullptr, false, mask_feature_bound(m))) return false;
+    const int mask_ok = bounds_usable(s, mask_feature_bound(m), 1);
+    if (mask_ok < 0) return false;
     if (total == 0) return true;
     if (!m->weights_s.ensure(total, "hipMalloc(split weights)")) return false;
     char *cur = static_cast<char *>(m->weights_s.ptr);
@@ -495,8 +497,11 @@ bool prepare_split(vh_model *m) {
             return false;
         w.bounds = m->bounds.f() + 4 * i;
         if (!layer_bounds(s, d, w, w.bounds)) return false;
+        const int ok = bounds_usable(s, w.bounds, 4);
+        if (ok < 0) return false;
+        if (ok == 0) w.bounds = nullptr;  // weights beyond the scale range: this layer's linears on fp32 MFMA
     }
-    for (int b = 0; b < d.bands; b++)
+    for (int b = 0; b < d.bands && mask_ok; b++)  // no pieces: the mask estimator stays on fp32 MFMA
         if (!split(m->mask_w1[b], Hm, D, &m->mask_w1_s[b]) || !split(m->mask_w2[b], 2 * d.in_dim(b), Hm, &m->mask_w2_s[b]))
             return false;
     return check(hipStreamSynchronize(s), "hipStreamSynchronize(split weights)");

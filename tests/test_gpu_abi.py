@@ -165,6 +165,19 @@ def test_matmul(provider, views, rng, monkeypatch):
         assert L.native_gpu_matmul(g, 37, in_dim, RD.dim, x.ctypes.data, w.ctypes.data, bias.ctypes.data,
                                    out.ctypes.data) == 1
         assert_close(ref, out, rtol=2e-5, atol=2e-6, what=f"matmul band {b}")
+    # inputs beyond the fp16 two-piece scale range (max |x| > 1e30) take the
+    # fp32 MFMA GEMM instead of overflowing a piece
+    b = 60
+    in_dim = RD.input_dims()[b]
+    assert in_dim % 16 == 0  # a width the two-piece GEMM would otherwise serve
+    x = rng.standard_normal((37, in_dim), dtype=np.float32) * np.float32(1e33)
+    w, bias = views[f"bands.{b}.weight"], views[f"bands.{b}.bias"]
+    ref = O.matmul(x, w, RD.dim, bias)
+    out = np.empty((37, RD.dim), np.float32)
+    assert L.native_gpu_matmul(g, 37, in_dim, RD.dim, x.ctypes.data, w.ctypes.data, bias.ctypes.data,
+                               out.ctypes.data) == 1
+    assert np.all(np.isfinite(out))
+    assert_close(ref, out, rtol=2e-5, atol=2e27, what="matmul beyond the scale range")
     monkeypatch.setenv("VOCALARC_GPU_MIN_WORK", str(1 << 40))
     assert L.native_gpu_matmul(g, 37, 8, RD.dim, x.ctypes.data, w.ctypes.data, None, out.ctypes.data) == 0
 
