@@ -44,7 +44,8 @@ static __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__rest
 // The same RMSNorm writing y as h2 rows (h2.hpp) scaled by
 // 2^h2_exponent(*bound): the A operand of the fp16 two-piece GEMMs, split
 // once here instead of in every column tile of the GEMM.  dim a multiple of
-// 16; ldy in fp32 units (an h2 row takes the bytes of its fp32 row).
+// 16 (so the quads of lanes that share a chunk are whole); ldy in fp32 units
+// (an h2 row takes the bytes of its fp32 row).
 template <int MAXV>
 static __global__ __launch_bounds__(256) void rmsnorm_h2_kernel(const float *__restrict__ x, int ldx,
                                                                const float *__restrict__ gamma,
@@ -72,7 +73,7 @@ static __global__ __launch_bounds__(256) void rmsnorm_h2_kernel(const float *__r
 #pragma unroll
     for (int i = 0; i < MAXV; i++) {
         const int c = lane + 64 * i;
-        if (c < nv) store4_h2(yr + 64 * (c >> 2), c & 3, (v[i] * inv) * ld4(gamma + 4 * c), s);
+        if (c < nv) store4_h2_quad(yr + 64 * (c >> 2), c & 3, (v[i] * inv) * ld4(gamma + 4 * c), s);
     }
 }
 

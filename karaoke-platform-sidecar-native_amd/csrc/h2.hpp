@@ -73,4 +73,22 @@ VH_DEVICE void store4_h2(unsigned char *chunk, int j, floatx4 v, float s) {
     *reinterpret_cast<u32x2 *>(chunk + 32 + o) = u32x2{m01, m23};
 }
 
+// The same for a quad of lanes holding the four groups 4j..4j+3 (lane j of the
+// quad, j = lane % 4) of one chunk: lanes j and j^2 swap one piece, so each
+// lane writes a whole 16-byte slot -- lanes 0, 1 the h slots, lanes 2, 3 the
+// m slots -- instead of two 8-byte halves.  Every lane of the quad takes part.
+VH_DEVICE void store4_h2_quad(unsigned char *chunk, int j, floatx4 v, float s) {
+    const float y0 = v[0] * s, y1 = v[1] * s, y2 = v[2] * s, y3 = v[3] * s;
+    const uint32_t h01 = pack_f16x2(y0, y1), h23 = pack_f16x2(y2, y3);
+    const uint32_t m01 = pack_f16x2(y0 - f16_lo(h01), y1 - f16_hi(h01));
+    const uint32_t m23 = pack_f16x2(y2 - f16_lo(h23), y3 - f16_hi(h23));
+    const bool h_slot = j < 2;
+    const uint32_t r0 = (uint32_t)__shfl_xor((int)(h_slot ? m01 : h01), 2, 64);
+    const uint32_t r1 = (uint32_t)__shfl_xor((int)(h_slot ? m23 : h23), 2, 64);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    // slot j = h of groups j, j+2; slot 2 + (j-2) = m of groups j-2, j
+    if (h_slot) *reinterpret_cast<u32x4 *>(chunk + 16 * j) = u32x4{h01, h23, r0, r1};
+    else *reinterpret_cast<u32x4 *>(chunk + 32 + 16 * (j - 2)) = u32x4{r0, r1, m01, m23};
+}
+
 }  // namespace vh
