@@ -78,7 +78,9 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     const int tiles_m = (d.M + GS_BM - 1) / GS_BM;
     if (tile >= tiles_m * tiles_n) return;
     // column-fastest order within groups of row tiles (see gemm.hpp)
-    const int gsz = (size_t)d.N * d.K * 4 <= (3u << 20) ? 1 : 8;
+    // groups of 4 row tiles for the wide GEMMs (measured against 1, 2, 8, 16:
+    // best by 0.3-1.3% on N = 1568 and 3072), one for N = 384
+    const int gsz = d.N >= 1024 ? 4 : 1;
     const int group = tile / (gsz * tiles_n);
     const int in_group = tile % (gsz * tiles_n);
     const int group_rows = min(gsz, tiles_m - group * gsz);
