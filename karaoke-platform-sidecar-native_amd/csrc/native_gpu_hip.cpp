@@ -185,12 +185,15 @@ struct native_gpu {
     // fp16 two-piece planes (gemm_h2) of a cached device matrix [out][in];
     // null when `in` is not a multiple of 16 (the fp32 MFMA GEMM serves it).
     // VOCALARC_GPU_SPLIT=0 keeps every product on the fp32 MFMA instruction.
-    const void *split(const float *dev, int in, int out) {
+    static bool split_off() {
         static const bool off = [] {
             const char *v = getenv("VOCALARC_GPU_SPLIT");
             return v && strcmp(v, "0") == 0;
         }();
-        if (off || !dev || in % SPLIT_K_MULTIPLE) return nullptr;
+        return off;
+    }
+    const void *split(const float *dev, int in, int out) {
+        if (split_off() || !dev || in % SPLIT_K_MULTIPLE) return nullptr;
         for (auto &e : cache) {
             if (e.dev != dev) continue;
             if (e.dev_split) return e.dev_split;
@@ -419,7 +422,9 @@ static int run_block(native_gpu *gpu, float *x, int64_t tokens, const AttnLayout
                      const native_gpu_transformer_weights *w) {
     LayerWeights L;
     if (!gpu->layer(w, L)) return gpu->fail("weight upload");
-    if (!transformer_block(gpu->stream, gpu->d, L, x, tokens, lay, gpu->scratch, gpu->rope))
+    // VOCALARC_GPU_SPLIT=0: every product (the attention's too) on the fp32 MFMA instruction
+    if (!transformer_block(gpu->stream, gpu->d, L, x, tokens, lay, gpu->scratch, gpu->rope, nullptr,
+                           native_gpu::split_off() ? PREC_FP32_MFMA : PREC_FP32))
         return gpu->fail("transformer");
     return 1;
 }

@@ -249,6 +249,20 @@ def test_reference_host_nonresident_groups(host_setup):
     assert snr_db(cpu_v, v) >= 80
 
 
+def test_reference_host_fp32_mfma_products(host_setup):
+    """VOCALARC_GPU_SPLIT=0: every product of the provider (linears and
+    attention) on the fp32 MFMA instruction; the same parity bar, and close to
+    the default fp16 two-piece output."""
+    tmp, pack_path, wav, (_, cpu_v, _) = host_setup
+    resp, v, _ = _run_host(O.REF_GPU_EXE, pack_path, wav, tmp, "gpu-fp32", env={"VOCALARC_GPU_SPLIT": "0"})
+    assert resp["backend"] == "native-hip-fused"
+    assert float(np.max(np.abs(v.astype(np.float64) - cpu_v))) <= 1e-4
+    assert snr_db(cpu_v, v) >= 80
+    _, v_default, _ = _run_host(O.REF_GPU_EXE, pack_path, wav, tmp, "gpu-default")
+    print(f"host path, fp32 MFMA products vs default: SNR {snr_db(v_default, v):.1f} dB")
+    assert snr_db(v_default, v) >= 100
+
+
 def test_reference_host_gpu_off_is_cpu_path(host_setup):
     """VOCALARC_GPU=off: no provider; the gpu executable is the CPU path."""
     tmp, pack_path, wav, (_, cpu_v, _) = host_setup
