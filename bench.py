@@ -221,7 +221,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs the separation path on a single GPU "
-              "(multi-GPU sharding by windows is described in DESIGN.md, not implemented)", file=sys.stderr)
+              "(sharding the windows over several GPUs is not implemented)", file=sys.stderr)
         return 2
 
     import numpy as np

@@ -4,7 +4,7 @@
    it (native/vocalarc_separation.c:1356-1406), checked against the oracle.
 2. The reference C11 host itself (compiled from the reference sources into
    oracle/_ref and linked against lib/libvocalarc_hip.so) checked against the
-   reference CPU executable on the same pack and WAV: the north-star bar,
+   reference CPU executable on the same pack and WAV: the fp32 parity bar,
    max |delta| <= 1e-4 and SNR >= 80 dB on the vocals and instrumental.
 """
 

@@ -1,8 +1,8 @@
 """Device pipeline (vocalarc_hip.h model entry points) vs the oracle.
 
 Stage tests compare one stage at a time on identical inputs; the forward and
-chunked tests compare whole waveforms at the north-star bar for the fp32
-path: per-sample max |delta| <= 1e-4 and SNR >= 80 dB.
+chunked tests compare whole waveforms at the fp32 parity bar: per-sample
+max |delta| <= 1e-4 and SNR >= 80 dB.
 """
 
 import numpy as np
