@@ -315,8 +315,8 @@ def main() -> int:
         "dtype": "fp32",
         "precision_note": "fp32 accuracy: transformer and mask-estimator linears as 2-piece fp16 splits of "
                           "power-of-two-scaled operands (3 products, fp32 accumulation; error vs fp64 at or below "
-                          "the fp32 MFMA GEMM's), time-axis attention as 3-piece bf16 splits (6 products), band "
-                          "split and band-axis attention on fp32 MFMA, DSP in fp64/fp32",
+                          "the fp32 MFMA GEMM's), time- and band-axis attention the same way (bound from the "
+                          "QKV projection's weights), band split on fp32 MFMA, DSP in fp64/fp32",
         "data": "synthetic (seeded sine+noise mix, random-init weights N(0,0.02), gammas N(1,0.02))",
         "config": {
             "workload": "full BS-RoFormer separation, 5 min stereo 44.1 kHz, 8 s windows / 2 s overlap, "

@@ -145,9 +145,9 @@ int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *
    probabilities as bf16 operands, fp32 softmax statistics); VH_ATT_SPLIT
    (fp32 qkv, length > 64) runs the products in fp32 accuracy as exact
    three-piece bf16 splits on the bf16 matrix cores; VH_ATT_H2 (fp32 qkv,
-   length > 64) runs them in fp32 accuracy as two-piece fp16 splits of
+   any length) runs them in fp32 accuracy as two-piece fp16 splits of
    power-of-two-scaled operands, the scales from max|qkv| computed on the
-   device (the default fp32 path's time-axis attention, which takes its
+   device (the default fp32 path's attention on both axes, which takes its
    bound from the projection's weights instead). */
 #define VH_ATT_OUT_BF16 1
 #define VH_ATT_BF16 2

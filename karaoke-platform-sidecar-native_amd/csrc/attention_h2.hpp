@@ -317,4 +317,181 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
         }
 }
 
+// Short sequences (L <= 64: the band axis) in fp32 accuracy on the fp16
+// matrix cores: the persistent task loop, prefetch, query layout and
+// single-pass softmax of attention_short_kernel (attention.hpp), with every
+// product as three v_mfma_f32_16x16x32_f16 on two-piece operands scaled as in
+// attention_h2_kernel (the probabilities are at most 1 here: scale 2^13).  A
+// lane of a 16x16x32 MFMA supplies eight k-values, assigned to (lane group,
+// slot) the same way for both operands, so the summed index may be relabelled
+// freely as long as both operands agree:
+//   S^T tile kt = K * Q^T, step s (head dims 32s..32s+31): slot 4c + e of
+//     lane group g is dim 32s + 16c + 4g + e -- the lane's own rotated q
+//     registers j = 2s + c -- and LDS holds each key's pieces in that order
+//     (position 8(4s + g) + 4c + e), so a lane reads 16 bytes per piece.
+//   O^T tile dt += V^T * P^T, step u (keys 32u..32u+31): slot 4c + r of lane
+//     group g is key 32u + 16c + 4g + r -- the lane's own probabilities
+//     sc[2u + c][r] -- and LDS holds V transposed, keys in that order; tile
+//     row m is dim m + 16 dt, so lane (n, g) ends with dims 16 dt + 4g + r
+//     (one 16-byte store per tile).
+// LDS rows are 72 halves (36 dwords): the 16 rows one read touches fall on
+// distinct 4-bank groups.  Two pieces of K and of V^T: 36 KB, four
+// workgroups per CU.
+VH_DEVICE void split4_h2(floatx4 v, float s, uint32_t &h01, uint32_t &h23, uint32_t &m01, uint32_t &m23) {
+    const float y0 = v[0] * s, y1 = v[1] * s, y2 = v[2] * s, y3 = v[3] * s;
+    h01 = pack_f16x2(y0, y1);
+    h23 = pack_f16x2(y2, y3);
+    m01 = pack_f16x2(y0 - f16_lo(h01), y1 - f16_hi(h01));
+    m23 = pack_f16x2(y2 - f16_lo(h23), y3 - f16_hi(h23));
+}
+
+template <typename TO>
+__global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) {
+    constexpr int KEYS = 64;
+    constexpr int PITCH = ATT_DH + 8;
+    __shared__ __attribute__((aligned(16))) _Float16 Kp[2][KEYS][PITCH];
+    __shared__ __attribute__((aligned(16))) _Float16 Vp[2][ATT_DH][PITCH];
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+    const float *qkv = static_cast<const float *>(a.qkv);
+    const int tasks = a.S * a.H;
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int q = 16 * wave + n;
+    const int qc = min(q, a.L - 1);
+    // staging: K keys tid/16 + 16i with dims d_st..d_st+3; V keys vk, vk + 1
+    // with dims vd..vd+3 and vd+32..vd+35
+    const int d_st = 4 * (tid & 15);
+    const int k_pos = 8 * (4 * (d_st >> 5) + ((d_st >> 2) & 3)) + 4 * ((d_st >> 4) & 1);
+    const int vk = 2 * (tid & 31), vd = 4 * (tid >> 5);
+    const int v_pos = 8 * (4 * (vk >> 5) + ((vk >> 2) & 3)) + 4 * ((vk >> 4) & 1) + (vk & 3);
+
+    // power-of-two scales from the bound on |q|, |k|, |v|
+    const float qs = a.scale * 1.4426950408889634f;
+    const float bnd = *a.bound;
+    const int ek = h2_exponent(1.4142135f * 1.0001f * bnd);
+    const int eq = h2_exponent(1.4142135f * 1.0001f * bnd * qs);
+    const int ev = h2_exponent(bnd);
+    constexpr int EP = 13;  // probabilities <= 1: 2^13 < 2^14
+    const float k_scale = ldexpf(1.0f, ek), v_scale = ldexpf(1.0f, ev), q_scale = qs * ldexpf(1.0f, eq);
+    const float s_unscale = ldexpf(1.0f, -(ek + eq)), o_unscale = ldexpf(1.0f, -(ev + EP)), p_scale = ldexpf(1.0f, EP);
+
+    floatx4 kpre[4], vpre[4], qpre[4];
+    float gpre = 0.0f;
+    auto prefetch = [&](int task) {
+        const int h = task % a.H, s = task / a.H;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key = (tid >> 4) + 16 * i;
+            kpre[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (key < a.L) kpre[i] = ld4(qkv + (size_t)attn_row(a, s, key) * a.ld + a.inner + h * ATT_DH + d_st);
+            const int vkey = vk + (i & 1);
+            vpre[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (vkey < a.L)
+                vpre[i] = ld4(qkv + (size_t)attn_row(a, s, vkey) * a.ld + 2 * a.inner + h * ATT_DH + vd + 32 * (i >> 1));
+        }
+        const size_t qrow = (size_t)attn_row(a, s, qc) * a.ld;
+#pragma unroll
+        for (int j = 0; j < 4; j++) qpre[j] = ld4(qkv + qrow + h * ATT_DH + 16 * j + 4 * g);
+        if (a.gate_col >= 0) gpre = qkv[qrow + a.gate_col + h];
+    };
+
+    const int per = (tasks + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int t_end = min(tasks, ((int)blockIdx.x + 1) * per);
+    int task = (int)blockIdx.x * per;
+    if (task < t_end) prefetch(task);
+    for (; task < t_end; task++) {
+        const int h = task % a.H, s = task / a.H;
+        // keys past L are zeros, rotated with the table's last row
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key = (tid >> 4) + 16 * i;
+            uint32_t h01, h23, m01, m23;
+            split4_h2(rope4(kpre[i], a.rope, min(key, a.L - 1), d_st), k_scale, h01, h23, m01, m23);
+            *reinterpret_cast<u32x2 *>(&Kp[0][key][k_pos]) = u32x2{h01, h23};
+            *reinterpret_cast<u32x2 *>(&Kp[1][key][k_pos]) = u32x2{m01, m23};
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float y0 = vpre[2 * c][e] * v_scale, y1 = vpre[2 * c + 1][e] * v_scale;
+                const uint32_t hp = pack_f16x2(y0, y1);
+                const uint32_t mp = pack_f16x2(y0 - f16_lo(hp), y1 - f16_hi(hp));
+                const int dim = vd + 32 * c + e;
+                *reinterpret_cast<uint32_t *>(&Vp[0][dim][v_pos]) = hp;
+                *reinterpret_cast<uint32_t *>(&Vp[1][dim][v_pos]) = mp;
+            }
+        halfx8 qh[2], qm[2];
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+            split8_h2(rope4(qpre[2 * st], a.rope, qc, 32 * st + 4 * g),
+                      rope4(qpre[2 * st + 1], a.rope, qc, 32 * st + 16 + 4 * g), q_scale, qh[st], qm[st]);
+        const float gate_logit = gpre;
+        __syncthreads();
+        if (task + 1 < t_end) prefetch(task + 1);
+
+        floatx4 sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            sc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const halfx8 kh = *reinterpret_cast<const halfx8 *>(&Kp[0][16 * kt + n][8 * (4 * st + g)]);
+                const halfx8 km = *reinterpret_cast<const halfx8 *>(&Kp[1][16 * kt + n][8 * (4 * st + g)]);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(km, qh[st], sc[kt], 0, 0, 0);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qm[st], sc[kt], 0, 0, 0);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[st], sc[kt], 0, 0, 0);
+            }
+            sc[kt] = sc[kt] * s_unscale;  // exact: a power of two
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                if (16 * kt + 4 * g + r >= a.L) sc[kt][r] = -INFINITY;
+                m = fmaxf(m, sc[kt][r]);
+            }
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float l = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sc[kt][r] = __builtin_amdgcn_exp2f(sc[kt][r] - m);
+                l += sc[kt][r];
+            }
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+
+        floatx4 o[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            halfx8 ph, pm;
+            split8_h2(sc[2 * u], sc[2 * u + 1], p_scale, ph, pm);
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const halfx8 vh = *reinterpret_cast<const halfx8 *>(&Vp[0][n + 16 * dt][8 * (4 * u + g)]);
+                const halfx8 vm = *reinterpret_cast<const halfx8 *>(&Vp[1][n + 16 * dt][8 * (4 * u + g)]);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vm, ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pm, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, o[dt], 0, 0, 0);
+            }
+        }
+
+        if (q < a.L) {
+            const float f = (1.0f / l) * (a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f) * o_unscale;
+            TO *op = static_cast<TO *>(a.out) + (size_t)attn_row(a, s, q) * a.ld_out + h * ATT_DH + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) st4(op + 16 * dt, o[dt] * f);
+        }
+        __syncthreads();  // LDS is refilled for the next task
+    }
+}
+
 }  // namespace vh

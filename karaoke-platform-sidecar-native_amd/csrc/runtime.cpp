@@ -732,7 +732,10 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
         static int cus = 0;
         if (cus == 0 && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
         const unsigned grid = (unsigned)std::min<int64_t>((int64_t)lay.S * heads, 4 * (int64_t)cus);
-        if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
+        if (a.bound) {  // fp16 two-piece products
+            if (out_bf16) hipLaunchKernelGGL((attention_short_h2_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((attention_short_h2_kernel<float>), dim3(grid), dim3(256), 0, s, a);
+        } else if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((attention_short_kernel<float>), dim3(grid), dim3(256), 0, s, a);
     } else if (lay.L <= 64)
         launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16,
@@ -876,8 +879,8 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
                  : rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)))
         return false;
     if (!lin(normed, D, w.wqkvg, w.wqkvg_p, 0, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, qkv_h2, "gemm_qkv")) return false;
-    // rotary + attention + gates (long sequences: products as fp16 two-piece
-    // splits on the default fp32 path)
+    // rotary + attention + gates (products as fp16 two-piece splits on the
+    // default fp32 path)
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32,
                    w.bounds ? w.bounds + 1 : nullptr))
         return false;

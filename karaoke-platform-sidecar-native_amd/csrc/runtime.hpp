@@ -195,10 +195,11 @@ struct AttnLayout {
     int group, group_stride, seq_stride, pos_stride;
 };
 // qkv fp32 (fp32 MFMA) or, with qkv_bf16, bf16 (bf16 MFMA); out fp32, or bf16
-// when out_bf16.  split (fp32 qkv, L > 64): the products in fp32 accuracy on
-// the matrix cores -- as two-piece fp16 splits when `bound` (a device float
-// bounding |q|, |k|, |v|) is given (attention_h2.hpp), else as exact
-// three-piece bf16 splits (attention_split.hpp).  rope: interleaved rotary
+// when out_bf16.  split (fp32 qkv): the products in fp32 accuracy on the
+// matrix cores -- as two-piece fp16 splits when `bound` (a device float
+// bounding |q|, |k|, |v|) is given (attention_h2.hpp, any L), else, for
+// L > 64, as exact three-piece bf16 splits (attention_split.hpp; L <= 64
+// keeps the fp32 MFMA kernel).  rope: interleaved rotary
 // table of length lay.L (or null).
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false,

@@ -28,6 +28,7 @@ ROLES = [
     (r"absmax_kernel", "weight maximum for the fp16 pieces (model load)"),
     (r"operand_bounds_kernel", "operand bounds of the fp16 two-piece GEMMs (model load)"),
     (r"attention_h2_kernel", "time-axis attention, L = 801 (fp32 via two-piece fp16)"),
+    (r"attention_short_h2_kernel", "band-axis attention, L = 62 (fp32 via two-piece fp16)"),
     (r"rmsnorm_h2_kernel", "pre-norms, written as fp16 pieces for the QKV / FFN-up GEMMs"),
     (r"gemm_split_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via split bf16)"),

@@ -236,8 +236,8 @@ class Context:
     def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True, out_bf16: bool = False,
                   bf16: bool = False, split: bool = False, h2: bool = False):
         """bf16: qkv is bf16 and the bf16-MFMA kernel runs; out_bf16: out is bf16; split: fp32 accuracy on the
-        bf16 matrix cores (three-piece splits); h2: fp32 accuracy on the fp16 matrix cores (two-piece splits,
-        scales from max|qkv|); both for length > 64."""
+        bf16 matrix cores (three-piece splits, length > 64); h2: fp32 accuracy on the fp16 matrix cores (two-piece
+        splits, scales from max|qkv|, any length)."""
         flags = ((ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0) | (ATT_SPLIT if split else 0) |
                  (ATT_H2 if h2 else 0))
         _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), flags),

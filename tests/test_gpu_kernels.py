@@ -229,6 +229,43 @@ def test_attention_split(ctx, rng, S, L, mode):
     assert e_split.max() <= 2.0 * e_fp32.max() + 1e-8
 
 
+@pytest.mark.parametrize("S,L", [(300, 62), (200, 64), (50, 1), (90, 17), (70, 33), (40, 63)])
+def test_attention_short_h2(ctx, rng, S, L):
+    """Band-axis attention (L <= 64: the persistent short kernel) with both
+    products as two-piece fp16 splits of power-of-two-scaled operands, the
+    default path's kernel: the fp32 bar against the oracle, and an error
+    against a float64 statement of the same rotated inputs no larger than the
+    fp32 MFMA kernel's (ragged lengths: keys past L masked, queries past L
+    not stored)."""
+    H = 8
+    qkv = rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32)
+    rot = _rotate_qk(qkv, L, H)
+    ref = O.attention(REFERENCE_DIMS, rot, S, L)
+    q = rot[:, :H * 64].reshape(S, L, H, 64).astype(np.float64)
+    k = rot[:, H * 64:2 * H * 64].reshape(S, L, H, 64).astype(np.float64)
+    v = rot[:, 2 * H * 64:].reshape(S, L, H, 64).astype(np.float64)
+    sc = np.einsum("slhd,smhd->shlm", q, k) * 0.125
+    p = np.exp(sc - sc.max(axis=-1, keepdims=True))
+    ref64 = np.einsum("shlm,smhd->slhd", p / p.sum(axis=-1, keepdims=True), v).reshape(S * L, H * 64)
+    outs = {}
+    for kind in ("h2", "fp32"):
+        dout = empty_dev((S * L, H * 64))
+        ctx.attention(to_dev(qkv), dout, S, L, H, rotary=True, h2=kind == "h2")
+        outs[kind] = from_dev(dout).astype(np.float64)
+    assert_close(ref, outs["h2"].astype(np.float32), rtol=2e-5, atol=2e-5, what=f"h2 short attention S={S} L={L}")
+    e_h2, e_fp32 = np.abs(outs["h2"] - ref64), np.abs(outs["fp32"] - ref64)
+    print(f"short attention S={S} L={L}: h2 max|d| {e_h2.max():.3e} rms {np.sqrt(np.mean(e_h2 ** 2)):.3e} | "
+          f"fp32 MFMA max|d| {e_fp32.max():.3e} rms {np.sqrt(np.mean(e_fp32 ** 2)):.3e}")
+    if L == 1:
+        # one key: the output is v itself, exact in fp32 and within the
+        # two-piece representation's 2^-22 relative error in h2
+        assert e_fp32.max() == 0.0
+        assert e_h2.max() <= 2.0 ** -22 * np.abs(v).max()
+        return
+    assert np.sqrt(np.mean(e_h2 ** 2)) <= 1.25 * np.sqrt(np.mean(e_fp32 ** 2)) + 1e-9
+    assert e_h2.max() <= 2.0 * e_fp32.max() + 1e-8
+
+
 @pytest.mark.parametrize("mode", ["split", "h2"])
 def test_attention_split_beyond_4gb(ctx, mode):
     """qkv larger than 4 GB takes the kernel's 64-bit staging addresses: its
