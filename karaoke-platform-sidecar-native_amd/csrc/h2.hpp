@@ -31,6 +31,17 @@ VH_HOST_DEVICE inline int h2_exponent(float bound) {
     return e < -100 ? -100 : (e > 100 ? 100 : e);
 }
 
+// Bounds for which the fp16 two-piece attention kernels may run.  They undo
+// the q and k scales with the single power of two 2^-(ek + eq), and the
+// output's with 2^-(ev + 5); with B in [2^-40, 2^60] every exponent lies in
+// [-62, 56], so ek + eq stays in [-125, 113] and ev + 5 in [-57, 61]: every
+// scale and unscale is a normal fp32 power of two.  Beyond that range the
+// attention runs on the kernels without piece scales (the three-piece bf16
+// split for long sequences, the fp32 MFMA kernel for short ones).
+constexpr float H2_ATT_BOUND_MIN = 0x1p-40f;
+constexpr float H2_ATT_BOUND_MAX = 0x1p60f;
+inline bool h2_attention_bound_ok(float b) { return b >= H2_ATT_BOUND_MIN && b <= H2_ATT_BOUND_MAX; }
+
 // Two fp32 -> two fp16 (nearest even) in one dword: one v_cvt_pk_f16_f32.
 VH_DEVICE uint32_t pack_f16x2(float a, float b) {
     typedef float floatx2 __attribute__((ext_vector_type(2)));

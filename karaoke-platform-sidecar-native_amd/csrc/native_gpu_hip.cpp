@@ -112,6 +112,7 @@ struct native_gpu {
     struct LayerBounds {
         const void *keys[6];
         float *dev;
+        bool att_h2;  // the fused projection's bound in the two-piece attention's range
     };
     std::vector<LayerBounds> layer_bounds_cache;
     void drop_layer_bounds() {
@@ -119,18 +120,23 @@ struct native_gpu {
             if (b.dev) (void)hipFree(b.dev);
         layer_bounds_cache.clear();
     }
-    float *bounds_of(const LayerWeights &L, bool *ok) {
+    float *bounds_of(const LayerWeights &L, bool *ok, bool *att_h2) {
         const void *keys[6] = {L.gamma, L.wqkvg, L.bqkvg, L.ff_gamma, L.w1, L.b1};
         for (auto &b : layer_bounds_cache)
-            if (memcmp(b.keys, keys, sizeof(keys)) == 0) return b.dev;
+            if (memcmp(b.keys, keys, sizeof(keys)) == 0) {
+                *att_h2 = b.att_h2;
+                return b.dev;
+            }
         float *dev = nullptr;
         *ok = false;
+        *att_h2 = false;
         if (!check(hipMalloc((void **)&dev, 4 * sizeof(float)), "hipMalloc(layer bounds)")) return nullptr;
         if (!layer_bounds(stream, d, L, dev)) {
             (void)hipFree(dev);
             return nullptr;
         }
-        const int usable = bounds_usable(stream, dev, 4);
+        float hb[4];
+        const int usable = bounds_usable(stream, dev, 4, hb);
         if (usable <= 0) {  // beyond the scale range: the layer's linears run on fp32 MFMA
             (void)hipFree(dev);
             if (usable < 0) return nullptr;
@@ -140,6 +146,8 @@ struct native_gpu {
         LayerBounds e;
         memcpy(e.keys, keys, sizeof(keys));
         e.dev = dev;  // null: recorded as unusable, so the check is not repeated
+        e.att_h2 = dev && h2_attention_bound_ok(hb[1]);
+        *att_h2 = e.att_h2;
         layer_bounds_cache.push_back(e);
         return dev;
     }
@@ -276,7 +284,7 @@ struct native_gpu {
         // first call that uses them; none when they are beyond the fp16
         // two-piece scale range, and the fp32 MFMA GEMM runs)
         bool ok = true;
-        L.bounds = bounds_of(L, &ok);
+        L.bounds = bounds_of(L, &ok, &L.att_h2);
         return ok;
     }
 

@@ -522,15 +522,19 @@ bool absmax(hipStream_t s, const float *x, int64_t n, float *scratch, float *out
 }
 
 bool layer_bounds(hipStream_t s, const Dims &d, const LayerWeights &w, float *bounds) {
-    return operand_bounds(s, w.gamma, d.dim, w.wqkvg, d.qkvg_dim(), w.bqkvg, false, bounds) &&
+    // bounds[1] covers the q, k, v rows of the fused projection only (their
+    // bias is zero): it scales q, k, v in the attention and bounds the
+    // attention output; the gate logits pass through a sigmoid
+    return operand_bounds(s, w.gamma, d.dim, w.wqkvg, d.qkv_dim(), w.bqkvg, false, bounds) &&
            operand_bounds(s, w.ff_gamma, d.dim, w.w1, d.ff1_out(), w.b1, d.ffn_glu != 0, bounds + 2);
 }
 
-int bounds_usable(hipStream_t s, const float *dev, int n) {
+int bounds_usable(hipStream_t s, const float *dev, int n, float *host) {
     float h[8];
     if (n > 8 || !check(hipMemcpyAsync(h, dev, n * sizeof(float), hipMemcpyDeviceToHost, s), "hipMemcpy(bounds)") ||
         !check(hipStreamSynchronize(s), "hipStreamSynchronize(bounds)"))
         return -1;
+    if (host) memcpy(host, h, n * sizeof(float));
     for (int i = 0; i < n; i++)
         if (!(h[i] >= 0.0f && h[i] <= 1.0e30f)) return 0;  // NaN, infinite or beyond the scale range
     return 1;
@@ -882,7 +886,7 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     // rotary + attention + gates (products as fp16 two-piece splits on the
     // default fp32 path)
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32,
-                   w.bounds ? w.bounds + 1 : nullptr))
+                   w.bounds && w.att_h2 ? w.bounds + 1 : nullptr))
         return false;
     // out projection added to the residual stream
     if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;

@@ -235,15 +235,21 @@ struct LayerWeights {
     // FFN up, FFN down} (layer_bounds); null: the fp32 MFMA GEMM runs instead
     void *wqkvg_p = nullptr, *wout_p = nullptr, *w1_p = nullptr, *w2_p = nullptr;
     float *bounds = nullptr;
+    // the fused projection's bound (bounds[1], which also bounds q, k and v)
+    // lies in the fp16 two-piece attention's range (h2_attention_bound_ok);
+    // false: the attention runs on the kernels without piece scales
+    bool att_h2 = false;
 };
 // The four A-operand bounds of a layer's linears into the device floats
 // bounds[0..3] (operand_bounds on its two RMSNorm gains and the matrices they
-// feed; the attention output is bounded by the fused projection's bound).
+// feed; bounds[1], on the fused projection's q, k, v rows, also bounds the
+// attention output).
 bool layer_bounds(hipStream_t s, const Dims &d, const LayerWeights &w, float *bounds);
-// Reads n (<= 8) device bounds back: 1 when all are finite and within the
-// fp16 two-piece scale range (<= 1e30), 0 when not (those products then run
-// on the fp32 MFMA instruction), -1 on a runtime error.  Synchronous.
-int bounds_usable(hipStream_t s, const float *dev, int n);
+// Reads n (<= 8) device bounds back (into host[0..n) when host is not
+// null): 1 when all are finite and within the fp16 two-piece GEMM's scale
+// range (<= 1e30), 0 when not (those products then run on the fp32 MFMA
+// instruction), -1 on a runtime error.  Synchronous.
+int bounds_usable(hipStream_t s, const float *dev, int n, float *host = nullptr);
 
 // Arithmetic of the matrix products.  PREC_FP32 (the parity path): fp32
 // accuracy, the transformer linears on fp16 matrix cores by two-piece operand

@@ -230,16 +230,22 @@ extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int head
     if (apply_rotary && !ctx->rope.get_interleaved(length, 64, ctx->stream, &rt)) return 0;
     const int inner = heads * 64;
     const bool h2 = (flags & VH_ATT_H2) && !(flags & VH_ATT_BF16);
+    bool h2_ok = false;
     if (h2) {  // the operands' own maximum bounds them
         if (sequences <= 0 || length <= 0 || heads <= 0 || !qkv ||
             !ctx->bounds.ensure((64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bound)") ||
             !absmax(ctx->stream, static_cast<const float *>(qkv), (int64_t)sequences * length * 3 * inner,
                     ctx->bounds.f() + 64, ctx->bounds.f()))
             return 0;
+        // outside the two-piece attention's scale range (or not finite): the
+        // products run on the kernels without piece scales
+        float b = 0.0f;
+        if (bounds_usable(ctx->stream, ctx->bounds.f(), 1, &b) < 0) return 0;
+        h2_ok = h2_attention_bound_ok(b);
     }
     return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
                      &ctx->timer, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0,
-                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2 ? ctx->bounds.f() : nullptr)
+                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2_ok ? ctx->bounds.f() : nullptr)
                ? 1
                : 0;
 }
@@ -497,9 +503,11 @@ bool prepare_split(vh_model *m) {
             return false;
         w.bounds = m->bounds.f() + 4 * i;
         if (!layer_bounds(s, d, w, w.bounds)) return false;
-        const int ok = bounds_usable(s, w.bounds, 4);
+        float hb[4];
+        const int ok = bounds_usable(s, w.bounds, 4, hb);
         if (ok < 0) return false;
         if (ok == 0) w.bounds = nullptr;  // weights beyond the scale range: this layer's linears on fp32 MFMA
+        w.att_h2 = w.bounds && h2_attention_bound_ok(hb[1]);
     }
     for (int b = 0; b < d.bands && mask_ok; b++)  // no pieces: the mask estimator stays on fp32 MFMA
         if (!split(m->mask_w1[b], Hm, D, &m->mask_w1_s[b]) || !split(m->mask_w2[b], 2 * d.in_dim(b), Hm, &m->mask_w2_s[b]))

@@ -28,6 +28,7 @@ REF_DIR = HERE / "_ref"
 REF_EXE = REF_DIR / "vocalarc-separation"
 REF_GPU_EXE = REF_DIR / "vocalarc-separation-gpu"
 REF_SIMD = REF_DIR / "libref_simd.so"
+REF_EMBED = REF_DIR / "embed-model"
 
 _F = ctypes.POINTER(ctypes.c_float)
 _I64 = ctypes.c_int64

@@ -53,3 +53,35 @@ def gpu_available() -> bool:
         return torch.cuda.is_available()
     except Exception:  # noqa: BLE001
         return False
+
+
+def fade64(chunk: int, step: int, index: int, count: int) -> np.ndarray:
+    """Closed form of the chunked separation's linear cross-fade over the
+    overlap O = chunk - step: every window but the first rises as
+    (i + 1/2)/O over its first O samples, every window but the last falls as
+    (chunk - i - 1/2)/O over its last O samples, 1 elsewhere (float64)."""
+    o = chunk - step
+    i = np.arange(chunk, dtype=np.float64)
+    w = np.ones(chunk)
+    if index > 0:
+        w[:o] = (i[:o] + 0.5) / o
+    if index + 1 < count:
+        w[chunk - o:] = (chunk - i[chunk - o:] - 0.5) / o
+    return w
+
+
+def compose_windows(outs, length: int, chunk: int, step: int, weights=None, starts=None) -> np.ndarray:
+    """float64 overlap-add of per-window outputs [C][chunk]:
+    sum_k w_k * out_k / sum_k w_k over the samples each window covers (the
+    part of the last window past `length` is dropped)."""
+    count = len(outs)
+    weights = weights or [fade64(chunk, step, k, count) for k in range(count)]
+    starts = starts or [k * step for k in range(count)]
+    num = np.zeros((outs[0].shape[0], length))
+    den = np.zeros(length)
+    for k in range(count):
+        a = starts[k]
+        n = min(length, a + chunk) - a
+        num[:, a:a + n] += weights[k][:n] * np.asarray(outs[k], np.float64)[:, :n]
+        den[a:a + n] += weights[k][:n]
+    return num / den

@@ -266,6 +266,24 @@ def test_attention_short_h2(ctx, rng, S, L):
     assert e_h2.max() <= 2.0 * e_fp32.max() + 1e-8
 
 
+@pytest.mark.parametrize("S,L", [(2, 801), (40, 62)])
+def test_attention_h2_outside_scale_range(ctx, rng, S, L):
+    """VH_ATT_H2 on a qkv whose maximum (v scaled by 1e25; q, k unscaled) lies
+    beyond the fp16 two-piece attention's range [2^-40, 2^60]: with one
+    unscale 2^-(ek+eq) = 2^142 the scores would be inf * 0 = NaN, so the
+    products run on the kernels without piece scales and the output is the
+    oracle's at the fp32 bar (relative to its 1e25 scale)."""
+    H = 8
+    qkv = rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32)
+    qkv[:, 2 * H * 64:] *= np.float32(1e25)
+    ref = O.attention(REFERENCE_DIMS, _rotate_qk(qkv, L, H), S, L)
+    dout = empty_dev((S * L, H * 64))
+    ctx.attention(to_dev(qkv), dout, S, L, H, rotary=True, h2=True)
+    out = from_dev(dout)
+    assert np.all(np.isfinite(out))
+    assert_close(ref, out, rtol=2e-5, atol=2e-5 * 1e25, min_snr=100, what=f"h2 attention, bound 1e25, L={L}")
+
+
 @pytest.mark.parametrize("mode", ["split", "h2"])
 def test_attention_split_beyond_4gb(ctx, mode):
     """qkv larger than 4 GB takes the kernel's 64-bit staging addresses: its

@@ -85,3 +85,34 @@ def test_operand_bounds_hold_and_are_reached(rng):
     assert np.abs(z).max() <= t
     g = O.geglu(z[:, : 2 * (N // 2)].astype(np.float32)).astype(np.float64)
     assert np.abs(g).max() <= t * t
+
+
+def _attention_exponents(bound: float):
+    """The fp16 two-piece attention's exponents for a bound B on |q|, |k|,
+    |v|: k and q scaled from the rotated bound sqrt(2) B (q also carrying the
+    softmax scale 1/8 and log2 e), v from B, the probabilities by 2^5."""
+    f32 = np.float32
+    qs = f32(0.125) * f32(1.4426950408889634)
+    ek = _exponent(float(f32(1.4142135) * f32(1.0001) * f32(bound)))
+    eq = _exponent(float(f32(1.4142135) * f32(1.0001) * f32(bound) * qs))
+    ev = _exponent(bound)
+    return ek, eq, ev
+
+
+def test_attention_scale_range():
+    """Within [2^-40, 2^60] (the range the library runs the fp16 two-piece
+    attention on) the single-constant unscales 2^-(ek+eq) and 2^-(ev+5) are
+    normal fp32 powers of two; a bound of 1e25 (or 1e-20) takes the scores'
+    unscale beyond fp32's exponent range, which is why such bounds run on the
+    kernels without piece scales."""
+    def normal(e):  # 2^e is a normal, finite fp32
+        return -126 <= e <= 127
+
+    for b in np.geomspace(2.0 ** -40, 2.0 ** 60, 997):
+        ek, eq, ev = _attention_exponents(float(b))
+        assert normal(-(ek + eq)) and normal(-(ev + 5)), b
+        assert normal(ek) and normal(eq) and normal(ev)
+    ek, eq, _ = _attention_exponents(1.0e25)
+    assert -(ek + eq) > 127  # 2^-(ek+eq) overflows to +inf
+    ek, eq, _ = _attention_exponents(1.0e-20)
+    assert -(ek + eq) < -149  # 2^-(ek+eq) underflows to 0

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from helpers import snr_db
+from helpers import compose_windows, fade64, snr_db
 from vocalarc_hip import audio, pack
 from vocalarc_hip.dims import BAND_WIDTHS_62, CONFIG_DIMS, REFERENCE_BAND_WIDTHS, REFERENCE_DIMS, ModelDims
 
@@ -214,9 +214,47 @@ def test_istft_perfect_reconstruction(dims):
     mask[..., 0] = 1
     y = O.istft(dims, src, mask, x.shape[1])
     assert np.max(np.abs(y - x)) < 1e-6
-    # a mask of j rotates every bin by 90 degrees: y = -H(x) style, energy kept
+    # a zero mask gives exact silence (the normalised envelope divides zeros)
     mask[..., 0], mask[..., 1] = 0, 0
     assert np.all(O.istft(dims, src, mask, x.shape[1]) == 0)
+
+
+def _istft64(d, source: np.ndarray, mask: np.ndarray, length: int) -> np.ndarray:
+    """float64 statement of the masked inverse STFT: Y = S*M per bin,
+    x_t = irfft(Y_t) (the imaginary parts of DC and Nyquist do not reach a
+    real signal), windowed by the periodic Hann, overlap-added at t*hop - N/2
+    and divided by the summed squared window where that exceeds 1e-12."""
+    N, hop = d.n_fft, d.hop
+    T = source.shape[2]
+    Y = (source[..., 0].astype(np.float64) + 1j * source[..., 1]) * (mask[..., 0] + 1j * mask[..., 1].astype(np.float64))
+    w = np.sin(np.pi * np.arange(N) / N) ** 2
+    out = np.zeros((d.channels, length))
+    env = np.zeros(length)
+    for t in range(T):
+        frames = np.fft.irfft(Y[:, :, t].T, n=N) * w  # [C][N]
+        s0 = t * hop - N // 2
+        a, b = max(0, s0), min(length, s0 + N)
+        out[:, a:b] += frames[:, a - s0:b - s0]
+        env[a:b] += w[a - s0:b - s0] ** 2
+    return np.where(env > 1e-12, out / np.where(env > 1e-12, env, 1.0), 0.0)
+
+
+@pytest.mark.parametrize("dims", [REFERENCE_DIMS, CONFIG_DIMS])
+def test_istft_random_complex_mask_matches_numpy(dims, rng):
+    """A random complex mask (both parts N(0,1), so the real/imaginary
+    cross terms of the complex product all matter) against the float64
+    irfft + overlap-add statement."""
+    x = audio.sine_mix(0.25, 14)
+    src = O.stft(dims, x)
+    mask = rng.standard_normal(src.shape).astype(np.float32)
+    got = O.istft(dims, src, mask, x.shape[1])
+    ref = _istft64(dims, src, mask, x.shape[1])
+    scale = float(np.max(np.abs(ref)))
+    assert np.max(np.abs(got - ref)) <= 2e-6 * scale
+    # a swapped sign in the complex product (S * conj(M)) is far outside that
+    conj = mask.copy()
+    conj[..., 1] *= -1
+    assert np.max(np.abs(_istft64(dims, src, conj, x.shape[1]) - ref)) > 0.1 * scale
 
 
 def test_band_tables():
@@ -264,6 +302,89 @@ def test_chunk_weights_partition_of_unity():
         total[k * step:k * step + chunk] += O.chunk_weights(chunk, step, k, count)
     assert np.allclose(total[:5000], 1.0, atol=1e-6)
     assert O.chunk_count(800, chunk, step) == 1
+
+
+def _fade64_swapped(chunk: int, step: int, index: int, count: int) -> np.ndarray:
+    """A planted mistake: the two fade shapes exchanged (falling over a
+    window's first O samples, rising over its last O) -- still a partition
+    of unity, so only a composition check can tell it apart."""
+    O_ = chunk - step
+    i = np.arange(chunk, dtype=np.float64)
+    w = np.ones(chunk)
+    if index > 0:
+        w[:O_] = (O_ - i[:O_] - 0.5) / O_
+    if index + 1 < count:
+        w[chunk - O_:] = (i[chunk - O_:] - (chunk - O_) + 0.5) / O_
+    return w
+
+
+@pytest.mark.parametrize("chunk,step,index,count", [(1000, 700, 0, 4), (1000, 700, 1, 4), (1000, 700, 3, 4),
+                                                    (1000, 700, 0, 1), (352800, 264600, 1, 50),
+                                                    (352800, 264600, 0, 50), (352800, 264600, 49, 50)])
+def test_chunk_weights_closed_form(chunk, step, index, count):
+    w = O.chunk_weights(chunk, step, index, count)
+    ref = fade64(chunk, step, index, count)
+    assert np.allclose(w, ref, rtol=0, atol=1e-7)
+    ov = chunk - step
+    # explicit positions: a rising edge starts at 1/(2O), a falling one ends there
+    assert w[0] == (np.float32(0.5) / np.float32(ov) if index > 0 else 1.0)
+    assert w[-1] == (np.float32(0.5) / np.float32(ov) if index + 1 < count else 1.0)
+    assert w[ov] == 1.0 and w[chunk - ov - 1] == 1.0
+    if index > 0:
+        assert w[ov - 1] == np.float32(ov - 0.5) / np.float32(ov)
+
+
+def test_chunked_separation_matches_numpy_composition():
+    """or_separate_chunked on 4 windows with a zero-padded tail against the
+    float64 statement sum_k w_k * forward(window_k) / sum_k w_k, each window
+    cut by numpy at k*step (zero-padded past the end), w_k the closed-form
+    fades of helpers.fade64.  Swapped fade branches or a window one step off move the
+    output far outside the tolerance (checked below on the statement)."""
+    d = CONFIG_DIMS.with_depth(1)
+    blob = pack.synthetic_pack(d, 41)
+    m = O.Model(d, blob)
+    chunk, step = 4410, 3087
+    length = chunk + 2 * step + 1000
+    x = audio.sine_mix(length / 44100.0, 15)
+    assert x.shape[1] == length
+    count = O.chunk_count(length, chunk, step)
+    assert count == 4 and (count - 1) * step + chunk > length
+
+    outs = []
+    for k in range(count):
+        win = np.zeros((2, chunk), np.float32)
+        seg = x[:, k * step:min(length, k * step + chunk)]
+        win[:, :seg.shape[1]] = seg
+        outs.append(m.forward(win).astype(np.float64))
+
+    def compose(weights, starts):
+        return compose_windows(outs, length, chunk, step, weights, starts)
+
+    def sum_overlapped(weights, starts):
+        den = np.zeros(length)
+        for k in range(count):
+            n = min(length, starts[k] + chunk) - starts[k]
+            den[starts[k]:starts[k] + n] += weights[k][:n]
+        return den
+
+    starts = [k * step for k in range(count)]
+    fades = [fade64(chunk, step, k, count) for k in range(count)]
+    ref = compose(fades, starts)
+    got = m.separate_chunked(x, chunk, step)
+    scale = float(np.max(np.abs(ref)))
+    tol = 1e-6 * scale
+    assert np.max(np.abs(got - ref)) <= tol
+
+    # the statement's power: planted mistakes land far outside the tolerance
+    swapped = [_fade64_swapped(chunk, step, k, count) for k in range(count)]
+    assert np.allclose(sum_overlapped(swapped, starts), 1.0)  # still a partition of unity
+    err_swapped = np.max(np.abs(compose(swapped, starts) - ref))
+    assert err_swapped > 100 * tol, err_swapped
+    # window 2's output composed one sample off where it was cut
+    shifted = list(starts)
+    shifted[2] += 1
+    err_shifted = np.max(np.abs(compose(fades, shifted) - ref))
+    assert err_shifted > 100 * tol, err_shifted
 
 
 def test_chunked_separation_of_one_window_is_forward():
