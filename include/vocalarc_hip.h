@@ -43,6 +43,7 @@ typedef struct vh_model vh_model;
 
 /* ---- context ----------------------------------------------------------- */
 vh_context *vh_create(void);
+/* Also frees every model loaded in ctx that vh_model_free has not freed. */
 void vh_destroy(vh_context *ctx);
 int vh_set_stream(vh_context *ctx, void *hip_stream);
 int vh_synchronize(vh_context *ctx);
@@ -160,6 +161,7 @@ int vh_attention(vh_context *ctx, int sequences, int length, int heads, const vo
 /* Upload a VSCNAT01 pack (native/vocalarc_separation.c:528-589) laid out for
    `dims` from host memory.  Returns NULL on a malformed pack. */
 vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const void *pack, size_t bytes);
+/* Before vh_destroy of its context (which frees the models left). */
 void vh_model_free(vh_model *model);
 /* Arithmetic of the model's matrix products (every linear of the transformer
    stack, band split and mask estimator):

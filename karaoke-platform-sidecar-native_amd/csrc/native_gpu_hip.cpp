@@ -330,7 +330,10 @@ extern "C" native_gpu *native_gpu_create(void) {
     }
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, 0) == hipSuccess) {
-        snprintf(gpu->device_name, sizeof(gpu->device_name), "%s %s", prop.name, prop.gcnArchName);
+        // the marketing name can be empty where the driver's name table is
+        // missing: the architecture then names the device alone
+        if (prop.name[0]) snprintf(gpu->device_name, sizeof(gpu->device_name), "%s (%s)", prop.name, prop.gcnArchName);
+        else snprintf(gpu->device_name, sizeof(gpu->device_name), "HIP device %s", prop.gcnArchName);
         // printed raw inside JSON by the host: keep it free of quotes/backslashes
         for (char *c = gpu->device_name; *c; c++)
             if (*c == '"' || *c == '\\' || (unsigned char)*c < 0x20) *c = ' ';

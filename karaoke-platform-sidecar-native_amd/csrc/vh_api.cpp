@@ -25,8 +25,11 @@ static AttnLayout band_axis_layout(int chunks, int T, int B) {
 }
 static AttnLayout contiguous_layout(int S, int L) { return {S, L, 1, L, 0, 1}; }
 
+struct vh_model;
+
 struct vh_context {
     hipStream_t stream = nullptr;
+    std::vector<vh_model *> models;  // live models (vh_destroy frees those left)
     int device = 0;
     char name[256] = "";
     KernelTimer timer;
@@ -83,6 +86,8 @@ extern "C" vh_context *vh_create(void) {
 extern "C" void vh_destroy(vh_context *ctx) {
     if (!ctx) return;
     (void)hipStreamSynchronize(ctx->stream);
+    for (vh_model *m : ctx->models) delete m;  // models not freed by their owner
+    ctx->models.clear();
     ctx->timer.reset();
     delete ctx;
 }
@@ -754,6 +759,7 @@ extern "C" vh_model *vh_model_load(vh_context *ctx, const vh_dims *dims, const v
         delete m;
         return nullptr;
     }
+    ctx->models.push_back(m);
     return m;
 }
 
@@ -771,7 +777,10 @@ extern "C" int vh_model_set_precision(vh_model *m, int precision) {
 
 extern "C" void vh_model_free(vh_model *m) {
     if (!m) return;
-    (void)hipStreamSynchronize(m->ctx->stream);
+    vh_context *ctx = m->ctx;
+    (void)hipStreamSynchronize(ctx->stream);
+    auto it = std::find(ctx->models.begin(), ctx->models.end(), m);
+    if (it != ctx->models.end()) ctx->models.erase(it);
     delete m;
 }
 

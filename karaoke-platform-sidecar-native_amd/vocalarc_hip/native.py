@@ -9,6 +9,7 @@ if the library is missing the import of `lib()` raises.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from pathlib import Path
 
 from .dims import CDims, ModelDims, to_c
@@ -125,6 +126,7 @@ class Context:
     """vh_context bound to a HIP stream (default: torch's current stream)."""
 
     def __init__(self, stream: int | None = None):
+        self.models = weakref.WeakSet()  # vh_destroy frees them with the context
         self.h = lib().vh_create()
         if not self.h:
             raise NativeError(f"vh_create failed: {last_error()}")
@@ -138,6 +140,8 @@ class Context:
 
     def close(self):
         if self.h:
+            for m in list(self.models):  # freed by vh_destroy below
+                m.h = None
             lib().vh_destroy(self.h)
             self.h = None
 
@@ -269,6 +273,7 @@ class Model:
         self.h = lib().vh_model_load(ctx.h, ctypes.byref(self._cd), ptr(pack), pack.nbytes)
         if not self.h:
             raise NativeError(f"vh_model_load failed: {last_error()}")
+        ctx.models.add(self)
 
     def close(self):
         if self.h:
