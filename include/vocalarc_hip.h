@@ -156,6 +156,20 @@ int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *
 #define VH_ATT_H2 8
 int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                  int apply_rotary, int flags);
+/* vh_attention without any device allocation, for callers that cannot
+   allocate (code under HIP graph capture, tight serving loops, harnesses that
+   forbid hipMalloc).  No counterpart in the reference.  Same arguments,
+   kernels and results (bit for bit) as vh_attention; its scratch -- the
+   rotary table, the operand bound and its absmax partials -- lives in one
+   fixed device array per GPU (1.05 MB, held until the process ends), so
+   length is at most VH_NOALLOC_MAX_LENGTH (a longer one fails with an
+   error).  Every call on a GPU shares that array: calls that overlap on one
+   GPU (other threads, or other streams before this one's work has finished)
+   race.  Synchronises the stream when the table is copied (apply_rotary) and
+   when VH_ATT_H2 reads the bound back. */
+#define VH_NOALLOC_MAX_LENGTH 4096
+int vh_attention_noalloc(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
+                         int apply_rotary, int flags);
 
 /* ---- model -------------------------------------------------------------- */
 /* Upload a VSCNAT01 pack (native/vocalarc_separation.c:528-589) laid out for

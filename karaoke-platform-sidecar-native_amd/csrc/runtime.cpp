@@ -777,23 +777,32 @@ bool Dims::valid(char *why, size_t n) const {
 }
 
 // ------------------------------------------------------------------ rotary
+void rope_table_host(int length, int dim_head, float *cos_t, float *sin_t, float *interleaved) {
+    const int pairs = dim_head / 2;
+    float freq[512];
+    for (int i = 0; i < pairs && i < 512; i++) freq[i] = 1.0f / powf(10000.0f, (float)(2 * i) / (float)dim_head);
+    for (int p = 0; p < length; p++)
+        for (int k = 0; k < pairs; k++) {
+            const float angle = (float)p * freq[k];
+            const size_t e = (size_t)p * pairs + k;
+            const float c = cosf(angle), sn = sinf(angle);
+            if (cos_t) cos_t[e] = c;
+            if (sin_t) sin_t[e] = sn;
+            if (interleaved) {
+                interleaved[2 * e] = c;
+                interleaved[2 * e + 1] = sn;
+            }
+        }
+}
+
 bool RopeCache::get(int length, int dim_head, hipStream_t s, const float **cs, const float **sn) {
     auto it = tables.find(length);
     if (it == tables.end()) {
         const int pairs = dim_head / 2;
         const size_t n = (size_t)length * pairs;
-        std::vector<float> freq(pairs), h(4 * n);
+        std::vector<float> h(4 * n);
         float *hc = h.data(), *hs = hc + n, *hi = hs + n;
-        for (int i = 0; i < pairs; i++) freq[i] = 1.0f / powf(10000.0f, (float)(2 * i) / (float)dim_head);
-        for (int p = 0; p < length; p++)
-            for (int k = 0; k < pairs; k++) {
-                const float angle = (float)p * freq[k];
-                const size_t e = (size_t)p * pairs + k;
-                hc[e] = cosf(angle);
-                hs[e] = sinf(angle);
-                hi[2 * e] = hc[e];
-                hi[2 * e + 1] = hs[e];
-            }
+        rope_table_host(length, dim_head, hc, hs, hi);
         float *d = nullptr;
         const size_t bytes = h.size() * sizeof(float);
         if (!check(hipMalloc((void **)&d, bytes), "hipMalloc(rope tables)")) return false;

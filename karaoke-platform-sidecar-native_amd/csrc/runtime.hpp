@@ -264,6 +264,13 @@ enum Precision : int { PREC_FP32 = 0, PREC_BF16 = 1, PREC_FP32_MFMA = 2 };
 // float expressions (native/vocalarc_separation.c:726-731): cos[L][Dh/2],
 // sin[L][Dh/2] and the same values interleaved as (cos, sin) pairs
 // [L][Dh/2][2], so one 16-byte load gives what four rotated dims need.
+// The rotary tables of positions 0..length-1 with base 10000, built on the
+// host with the reference's float expressions (native/vocalarc_separation.c:
+// 726-731) so they are bit-exact: cos_t/sin_t [length][dim_head/2] and
+// interleaved [length][dim_head/2][cos, sin]; null outputs are skipped.
+// dim_head <= 1024.
+void rope_table_host(int length, int dim_head, float *cos_t, float *sin_t, float *interleaved);
+
 struct RopeCache {
     struct Tables { float *cos, *sin, *interleaved; };
     std::map<int, Tables> tables;

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "dsp.hpp"
@@ -67,6 +68,41 @@ struct vh_model {
 };
 
 // ------------------------------------------------------------------ context
+// ------------------------------------------------- no-allocation scratch
+// Device scratch of vh_attention_noalloc: float 0 the operand bound,
+// [64, 64 + ABSMAX_PARTIALS) the absmax partials, then the interleaved rotary
+// table of up to VH_NOALLOC_MAX_LENGTH positions (1.05 MB in all).  Each
+// device holds its own copy for the life of the process.  Host code never
+// uses the array's name as an address: noalloc_scratch[device] holds the
+// device address from hipGetSymbolAddress, resolved by vh_create with the
+// device current.
+constexpr size_t NOALLOC_ROPE_OFFSET = 64 + ABSMAX_PARTIALS;
+constexpr size_t NOALLOC_FLOATS = NOALLOC_ROPE_OFFSET + (size_t)VH_NOALLOC_MAX_LENGTH * 64;
+static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex noalloc_mutex;  // guards noalloc_scratch and noalloc_rope_host
+static float *noalloc_scratch[NOALLOC_MAX_DEVICES] = {};
+static float noalloc_rope_host[(size_t)VH_NOALLOC_MAX_LENGTH * 64];
+
+// With `device` current: its scratch address (once per device).
+static bool resolve_noalloc_scratch(int device) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) {
+        set_error("no-allocation scratch: device %d beyond %d", device, NOALLOC_MAX_DEVICES);
+        return false;
+    }
+    std::lock_guard<std::mutex> lock(noalloc_mutex);
+    if (noalloc_scratch[device]) return true;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        set_error("hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        return false;
+    }
+    noalloc_scratch[device] = static_cast<float *>(p);
+    return true;
+}
+
 extern "C" vh_context *vh_create(void) {
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
@@ -74,7 +110,7 @@ extern "C" vh_context *vh_create(void) {
         return nullptr;
     }
     vh_context *ctx = new vh_context();
-    if (!check(hipSetDevice(0), "hipSetDevice")) {
+    if (!check(hipSetDevice(0), "hipSetDevice") || !resolve_noalloc_scratch(0)) {
         delete ctx;
         return nullptr;
     }
@@ -251,6 +287,60 @@ extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int head
     return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
                      &ctx->timer, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0,
                      (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2_ok ? ctx->bounds.f() : nullptr)
+               ? 1
+               : 0;
+}
+
+extern "C" int vh_attention_noalloc(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
+                                    int apply_rotary, int flags) {
+    if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16 | VH_ATT_SPLIT | VH_ATT_H2))) {
+        set_error("vh_attention_noalloc: bad context or flags");
+        return 0;
+    }
+    if (sequences <= 0 || length <= 0 || heads <= 0 || !qkv || !out) {
+        set_error("vh_attention_noalloc: bad shape S=%d L=%d H=%d", sequences, length, heads);
+        return 0;
+    }
+    if (length > VH_NOALLOC_MAX_LENGTH) {
+        set_error("vh_attention_noalloc: length %d exceeds the %d positions of the no-allocation scratch", length,
+                  VH_NOALLOC_MAX_LENGTH);
+        return 0;
+    }
+    float *scr = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(noalloc_mutex);
+        scr = ctx->device >= 0 && ctx->device < NOALLOC_MAX_DEVICES ? noalloc_scratch[ctx->device] : nullptr;
+    }
+    if (!scr) {
+        set_error("vh_attention_noalloc: scratch of device %d not resolved", ctx->device);
+        return 0;
+    }
+    const float *rt = nullptr;
+    if (apply_rotary) {
+        // the same host-built table as vh_attention's, copied into the scratch
+        std::lock_guard<std::mutex> lock(noalloc_mutex);
+        rope_table_host(length, 64, nullptr, nullptr, noalloc_rope_host);
+        if (!check(hipMemcpyAsync(scr + NOALLOC_ROPE_OFFSET, noalloc_rope_host, (size_t)length * 64 * sizeof(float),
+                                  hipMemcpyHostToDevice, ctx->stream),
+                   "hipMemcpy(rotary table)") ||
+            !check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(rotary table)"))
+            return 0;
+        rt = scr + NOALLOC_ROPE_OFFSET;
+    }
+    const int inner = heads * 64;
+    const bool h2 = (flags & VH_ATT_H2) && !(flags & VH_ATT_BF16);
+    bool h2_ok = false;
+    if (h2) {  // as vh_attention: the operands' own maximum, every partial written before it is read
+        if (!absmax(ctx->stream, static_cast<const float *>(qkv), (int64_t)sequences * length * 3 * inner, scr + 64,
+                    scr))
+            return 0;
+        float b = 0.0f;
+        if (bounds_usable(ctx->stream, scr, 1, &b) < 0) return 0;
+        h2_ok = h2_attention_bound_ok(b);
+    }
+    return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
+                     nullptr, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0,
+                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2_ok ? scr : nullptr)
                ? 1
                : 0;
 }

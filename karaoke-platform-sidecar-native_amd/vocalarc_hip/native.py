@@ -21,7 +21,7 @@ LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
 HARNESS_SYMBOLS = [
     "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
     "vh_rmsnorm", "vh_rmsnorm_bf16", "vh_rmsnorm_h2", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
-    "vh_gemm_split", "vh_split_bytes", "vh_split_weights", "vh_gemm_h2", "vh_h2_bytes", "vh_split_weights_h2", "vh_operand_bounds", "vh_to_bf16", "vh_attention", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
+    "vh_gemm_split", "vh_split_bytes", "vh_split_weights", "vh_gemm_h2", "vh_h2_bytes", "vh_split_weights_h2", "vh_operand_bounds", "vh_to_bf16", "vh_attention", "vh_attention_noalloc", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
     "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
 ]
 ABI_SYMBOLS = [
@@ -35,6 +35,7 @@ EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16, PRECISION_FP32_MFMA = 0, 1, 2
 BF16_A, BF16_C, BF16_STAGED = 1, 2, 4  # vh_gemm_bf16 operand flags; STAGED forces the register-staged kernel
 ATT_OUT_BF16, ATT_BF16, ATT_SPLIT, ATT_H2 = 1, 2, 4, 8  # vh_attention flags
+NOALLOC_MAX_LENGTH = 4096  # VH_NOALLOC_MAX_LENGTH
 SPEC_REFERENCE, SPEC_FRAME_MAJOR = 0, 1  # spectrum layouts: [F][C][T][2] / [C][T][F][2]
 
 _P = ctypes.c_void_p
@@ -75,6 +76,7 @@ def lib():
         "vh_operand_bounds": (_I, [_P, _P, _I, _P, _I, _P, _I, _P]),
         "vh_to_bf16": (_I, [_P, _I64, _I, _P, _P, _I]),
         "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
+        "vh_attention_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
         "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
         "vh_model_free": (None, [_P]), "vh_model_set_precision": (_I, [_P, _I]),
         "vh_transformer": (_I, [_P, _P, _I, _I, _P, _I, _I]),
@@ -246,6 +248,13 @@ class Context:
                  (ATT_H2 if h2 else 0))
         _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), flags),
             "vh_attention")
+
+    def attention_noalloc(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True,
+                          out_bf16: bool = False, bf16: bool = False, split: bool = False, h2: bool = False) -> int:
+        """vh_attention_noalloc (no device allocation; length <= NOALLOC_MAX_LENGTH); returns its status."""
+        flags = ((ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0) | (ATT_SPLIT if split else 0) |
+                 (ATT_H2 if h2 else 0))
+        return lib().vh_attention_noalloc(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), flags)
 
     # -- timing --
     def timing(self, classes: str | None = "*"):
