@@ -9,7 +9,10 @@
 //     kh.qm, kh.qh); the block's scores are scaled back by 2^-(ek+eq).
 //   O^T += V^T * P^T: v times 2^ev, the probabilities (at most 2^8: the
 //     running maximum is raised lazily) times 2^5; three products per 16
-//     keys and 32 dims; the output is scaled back by 2^-(ev+5).
+//     keys and 32 dims.  Both power-of-two scales ride in the exponent's
+//     one FMA, p = exp2(s * 2^-(ek+eq) + 5 - m); the row sums carry the 2^5
+//     as well, so normalising cancels it and the output is scaled back by
+//     2^-ev only.
 // The exponents come from one bound B on |q|, |k| and |v| before rotation
 // (a.bound, a device float; a rotated pair keeps its 2-norm, so rotated
 // values stay below sqrt(2) B).  The probabilities, statistics,
@@ -54,20 +57,17 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
     // power-of-two scales from the bound on |q|, |k|, |v|
     const float qs = a.scale * 1.4426950408889634f;
     const float bnd = *a.bound;
-    const int ek = h2_exponent(1.4142135f * 1.0001f * bnd);
-    const int eq = h2_exponent(1.4142135f * 1.0001f * bnd * qs);
-    const int ev = h2_exponent(bnd);
+    int ek, eq, ev;
+    att_h2_exponents(bnd, qs, ek, eq, ev);
     constexpr int EP = 5;  // probabilities <= 2^8: 2^8 * 2^5 < 2^14
     const float k_scale = ldexpf(1.0f, ek), v_scale = ldexpf(1.0f, ev);
-    const float s_unscale = ldexpf(1.0f, -(ek + eq)), o_unscale = ldexpf(1.0f, -(ev + EP)), p_scale = ldexpf(1.0f, EP);
+    const float s_unscale = ldexpf(1.0f, -(ek + eq)), o_unscale = ldexpf(1.0f, -ev);
 
     // Q of query q0+li, dims 16g + 8lh .. +7, rotated, scaled (log2 domain), split.
     halfx8 qh[4], qm[4];
-    float gate_logit = 0.0f;  // loaded with Q so the store does not wait on it
     {
         const int q = min(q0 + li, a.L - 1);
         const float *qp = qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
-        if (a.gate_col >= 0) gate_logit = qkv[(size_t)attn_row(a, s, q) * a.ld + a.gate_col + h];
         const float q_scale = qs * ldexpf(1.0f, eq);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -154,8 +154,9 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
             }
         }
     };
-    // S^T block of 32 keys x 32 queries from Ks[kbuf], scaled back; each
-    // 16-dim group's K pieces are read while the previous group's products run
+    // S^T block of 32 keys x 32 queries from Ks[kbuf], still scaled by
+    // 2^(ek+eq); each 16-dim group's K pieces are read while the previous
+    // group's products run
     auto qk = [&](int kbuf) {
         floatx16 sc;
 #pragma unroll
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
             sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qm[g], sc, 0, 0, 0);
             sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[g], sc, 0, 0, 0);
         }
-        return sc * s_unscale;  // exact: a power of two
+        return sc;
     };
 
     floatx16 o[2];
@@ -185,14 +186,17 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
     float m_run = -INFINITY, l_run = 0.0f;
 
     // First half of the online softmax of block kb (its scores just
-    // computed): mask keys past L, raise the running maximum (and rescale o
-    // and l) as online_softmax_block does.
+    // computed, still scaled): mask keys past L, raise the running maximum
+    // (and rescale o and l) as online_softmax_block does.  The maximum is
+    // taken over the scaled scores and then scaled back: exact, the scale
+    // being a positive power of two.
     auto soft_max = [&](floatx16 &sc, int kb) {
         const int valid = a.L - kb * ATT_KB;
         if (valid < ATT_KB) {
+            const int vl = valid - 4 * lh;  // register r holds key 8(r/4) + 4lh + r%4
 #pragma unroll
             for (int r = 0; r < 16; r++)
-                if (8 * (r >> 2) + 4 * lh + (r & 3) >= valid) sc[r] = -INFINITY;
+                if (8 * (r >> 2) + (r & 3) >= vl) sc[r] = -INFINITY;
         }
         float mb = -INFINITY;
 #pragma unroll
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
             // the other half-wave's maximum (lanes l and l^32 hold one query):
             // one v_permlane32_swap instead of an LDS permute round trip
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
-            mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * s_unscale;
         }
         const bool grow = mb > m_run + 8.0f;
         if (__ballot(grow)) {
@@ -216,9 +220,10 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
     // Second half (probabilities, row sum) and O^T += V^T P^T from Vt[vbuf].
     auto soft_pv = [&](floatx16 &sc, int vbuf) {
         float ls = 0.0f;
+        const float c = (float)EP - m_run;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_run);
+            sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], s_unscale, c));  // 2^5 times the probability
             ls += sc[r];
         }
         l_run += ls;
@@ -229,7 +234,7 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
 #pragma unroll
         for (int st = 0; st < 2; st++)
             split8_h2(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
-                      floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, p_scale, pp[st][0],
+                      floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, 1.0f, pp[st][0],
                       pp[st][1]);
         halfx8 vp[2][2];
         auto read = [&](int step, halfx8 (&v)[2]) {
@@ -304,7 +309,8 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
     if (q >= a.L) return;
     const float inv = (1.0f / l_tot) * o_unscale;
     const int row = attn_row(a, s, q);
-    const float gate = a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f;
+    // the gate logit, loaded here rather than held through the key loop
+    const float gate = a.gate_col >= 0 ? sigmoid_dev(qkv[(size_t)row * a.ld + a.gate_col + h]) : 1.0f;
     TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
 #pragma unroll
     for (int t = 0; t < 2; t++)

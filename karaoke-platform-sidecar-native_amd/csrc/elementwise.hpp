@@ -10,70 +10,92 @@ namespace vh {
 // ---------------------------------------------------------------- RMSNorm
 // y = x * (sqrt(d) / sqrt(sum(x^2) + 1e-12)) * gamma
 // (native/vocalarc_separation.c:419-424, native/native_simd.c:98-121).
-// One wavefront per row, the row held in registers between the two passes.
+// One wavefront per pair of rows: rows 2p and 2p+1 lie back to back (the
+// row pitch is dim), so the pair is one contiguous span of 2*dim/4 float4s
+// and lane l loads span float4s l, l+64, ... -- every lane busy and twice
+// the bytes in flight of a wave per row (non-temporal: each byte is touched
+// once).  Each lane adds its float4s' squares into the sum of the row they
+// belong to; the pair is held in registers between the two passes.
 // TY: fp32, or bf16 when the output feeds a bf16-operand GEMM.
-template <int MAXV, typename TY>
-static __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, int ldx,
-                                                      const float *__restrict__ gamma,
-                                                      TY *__restrict__ y, int ldy, int rows, int dim) {
-    const int row = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
-    const int lane = (int)threadIdx.x & 63;
-    if (row >= rows) return;
-    const float *xr = x + (size_t)row * ldx;
-    TY *yr = y + (size_t)row * ldy;
-    const int nv = dim >> 2;
-    floatx4 v[MAXV];
-    float ss = 0.0f;
+template <typename TY>
+VH_DEVICE void st4_once(TY *p, floatx4 v) { st4(p, v); }
+template <>
+VH_DEVICE void st4_once<float>(float *p, floatx4 v) { st4_stream(p, v); }
+
+template <int MAXV>
+VH_DEVICE void rmsnorm_pair_load(const float *xs, int nv, int total, int lane, floatx4 (&v)[MAXV], float &s0,
+                                 float &s1) {
+    s0 = 0.0f;
+    s1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < MAXV; i++) {
         const int c = lane + 64 * i;
-        if (c < nv) {
-            v[i] = ld4(xr + 4 * c);
-            ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        if (c < total) {
+            v[i] = ld4_stream(xs + 4 * c);
+            const float q = v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+            if (c < nv) s0 += q;
+            else s1 += q;
         }
     }
-    ss = wave_sum(ss);
-    const float inv = sqrtf((float)dim) / sqrtf(ss + 1.0e-12f);
+    s0 = wave_sum(s0);
+    s1 = wave_sum(s1);
+}
+
+template <int MAXV, typename TY>
+static __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x,
+                                                             const float *__restrict__ gamma, TY *__restrict__ y,
+                                                             int rows, int dim) {
+    const int row0 = 2 * ((int)blockIdx.x * 4 + ((int)threadIdx.x >> 6));
+    const int lane = (int)threadIdx.x & 63;
+    if (row0 >= rows) return;
+    const int nv = dim >> 2;
+    const int total = (row0 + 1 < rows ? 2 : 1) * nv;
+    floatx4 v[MAXV];
+    float s0, s1;
+    rmsnorm_pair_load<MAXV>(x + (size_t)row0 * dim, nv, total, lane, v, s0, s1);
+    const float inv0 = sqrtf((float)dim) / sqrtf(s0 + 1.0e-12f);
+    const float inv1 = sqrtf((float)dim) / sqrtf(s1 + 1.0e-12f);
+    TY *ys = y + (size_t)row0 * dim;
 #pragma unroll
     for (int i = 0; i < MAXV; i++) {
         const int c = lane + 64 * i;
-        if (c < nv) st4(yr + 4 * c, (v[i] * inv) * ld4(gamma + 4 * c));
+        if (c < total) {
+            const bool second = c >= nv;
+            st4_once(ys + 4 * c, (v[i] * (second ? inv1 : inv0)) * ld4(gamma + 4 * (second ? c - nv : c)));
+        }
     }
 }
 
 // The same RMSNorm writing y as h2 rows (h2.hpp) scaled by
 // 2^h2_exponent(*bound): the A operand of the fp16 two-piece GEMMs, split
 // once here instead of in every column tile of the GEMM.  dim a multiple of
-// 16 (so the quads of lanes that share a chunk are whole); ldy in fp32 units
-// (an h2 row takes the bytes of its fp32 row).
+// 16 (so the quads of lanes that share a chunk are whole, in either row of
+// the pair: nv is a multiple of 4); an h2 row takes the bytes of its fp32 row.
 template <int MAXV>
-static __global__ __launch_bounds__(256) void rmsnorm_h2_kernel(const float *__restrict__ x, int ldx,
+static __global__ __launch_bounds__(256) void rmsnorm_h2_kernel(const float *__restrict__ x,
                                                                const float *__restrict__ gamma,
-                                                               float *__restrict__ y, int ldy, int rows, int dim,
+                                                               float *__restrict__ y, int rows, int dim,
                                                                const float *__restrict__ bound) {
-    const int row = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
+    const int row0 = 2 * ((int)blockIdx.x * 4 + ((int)threadIdx.x >> 6));
     const int lane = (int)threadIdx.x & 63;
-    if (row >= rows) return;
+    if (row0 >= rows) return;
     const float s = ldexpf(1.0f, h2_exponent(*bound));
-    const float *xr = x + (size_t)row * ldx;
-    unsigned char *yr = reinterpret_cast<unsigned char *>(y + (size_t)row * ldy);
     const int nv = dim >> 2;
+    const int total = (row0 + 1 < rows ? 2 : 1) * nv;
     floatx4 v[MAXV];
-    float ss = 0.0f;
+    float s0, s1;
+    rmsnorm_pair_load<MAXV>(x + (size_t)row0 * dim, nv, total, lane, v, s0, s1);
+    const float inv0 = sqrtf((float)dim) / sqrtf(s0 + 1.0e-12f);
+    const float inv1 = sqrtf((float)dim) / sqrtf(s1 + 1.0e-12f);
+    unsigned char *ys = reinterpret_cast<unsigned char *>(y + (size_t)row0 * dim);
 #pragma unroll
     for (int i = 0; i < MAXV; i++) {
         const int c = lane + 64 * i;
-        if (c < nv) {
-            v[i] = ld4(xr + 4 * c);
-            ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        if (c < total) {
+            const bool second = c >= nv;
+            store4_h2_quad(ys + 64 * (c >> 2), c & 3, (v[i] * (second ? inv1 : inv0)) * ld4(gamma + 4 * (second ? c - nv : c)),
+                           s);
         }
-    }
-    ss = wave_sum(ss);
-    const float inv = sqrtf((float)dim) / sqrtf(ss + 1.0e-12f);
-#pragma unroll
-    for (int i = 0; i < MAXV; i++) {
-        const int c = lane + 64 * i;
-        if (c < nv) store4_h2_quad(yr + 64 * (c >> 2), c & 3, (v[i] * inv) * ld4(gamma + 4 * c), s);
     }
 }
 
@@ -130,14 +152,16 @@ static __global__ __launch_bounds__(256) void softmax_rows_kernel(const float *_
 // --------------------------------------------------------- rotary [BH][L][64]
 // Interleaved-pair rotation (native/vocalarc_separation.c:692-711) with the
 // host-built cos/sin table [L][32] (native/vocalarc_separation.c:726-731).
+// One float4 (two pairs) per thread, x streamed (non-temporal: each byte is
+// touched once).
 static __global__ __launch_bounds__(256) void rope_bhld_kernel(float *__restrict__ x, const float *__restrict__ cs,
-                                                        const float *__restrict__ sn, int64_t n4, int len) {
+                                                               const float *__restrict__ sn, int64_t n4, int len) {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= n4) return;
     const int c4 = (int)(e & 15);           // float4 within the 64-wide head row
     const int pos = (int)((e >> 4) % len);  // position
     float *p = x + 4 * e;
-    floatx4 v = ld4(p);
+    const floatx4 v = ld4_stream(p);
     const int pi = pos * 32 + 2 * c4;
     const float c0 = cs[pi], s0 = sn[pi], c1 = cs[pi + 1], s1 = sn[pi + 1];
     floatx4 r;
@@ -145,7 +169,7 @@ static __global__ __launch_bounds__(256) void rope_bhld_kernel(float *__restrict
     r[1] = v[0] * s0 + v[1] * c0;
     r[2] = v[2] * c1 - v[3] * s1;
     r[3] = v[2] * s1 + v[3] * c1;
-    st4(p, r);
+    st4_stream(p, r);
 }
 
 // ------------------------------------------------------------- GELU-GLU

@@ -42,6 +42,17 @@ constexpr float H2_ATT_BOUND_MIN = 0x1p-40f;
 constexpr float H2_ATT_BOUND_MAX = 0x1p60f;
 inline bool h2_attention_bound_ok(float b) { return b >= H2_ATT_BOUND_MIN && b <= H2_ATT_BOUND_MAX; }
 
+// The fp16 two-piece attention's exponents for a bound B on |q|, |k|, |v|
+// (before rotation): k and q (times the softmax scale and log2 e, qs) from
+// the rotated bound sqrt(2) B, v from B.  One definition for the attention
+// kernels and for the fused-projection epilogue that splits k and v ahead of
+// them, so both scale alike.
+VH_HOST_DEVICE inline void att_h2_exponents(float bnd, float qs, int &ek, int &eq, int &ev) {
+    ek = h2_exponent(1.4142135f * 1.0001f * bnd);
+    eq = h2_exponent(1.4142135f * 1.0001f * bnd * qs);
+    ev = h2_exponent(bnd);
+}
+
 // Two fp32 -> two fp16 (nearest even) in one dword: one v_cvt_pk_f16_f32.
 VH_DEVICE uint32_t pack_f16x2(float a, float b) {
     typedef float floatx2 __attribute__((ext_vector_type(2)));

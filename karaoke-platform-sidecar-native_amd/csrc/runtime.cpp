@@ -557,36 +557,42 @@ bool to_bf16_rows(hipStream_t s, const float *src, int rows, int cols, void *dst
     return sync_debug(s, "to_bf16_kernel");
 }
 
+// Rows of x and y are contiguous (pitch dim): the kernels take rows in pairs
+// as one span.
 template <typename TY>
 static bool rmsnorm_any(hipStream_t s, const float *x, int ldx, const float *gamma, TY *y, int ldy, int64_t rows,
                         int dim, KernelTimer *t) {
-    if (dim % 4 || dim > 2048 || rows <= 0 || rows > INT32_MAX / 2) {
-        set_error("rmsnorm: unsupported dim %d", dim);
+    if (dim % 4 || dim > 2048 || rows <= 0 || rows > INT32_MAX / 2 || ldx != dim || ldy != dim) {
+        set_error("rmsnorm: unsupported dim %d or row pitches %d/%d", dim, ldx, ldy);
         return false;
     }
     Scope sc(t, s, "rmsnorm");
-    const unsigned grid = blocks_for(rows, 4);
-    const int nv = dim / 4;
-    if (nv <= 64) hipLaunchKernelGGL((rmsnorm_kernel<1, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
-    else if (nv <= 128) hipLaunchKernelGGL((rmsnorm_kernel<2, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
-    else if (nv <= 256) hipLaunchKernelGGL((rmsnorm_kernel<4, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
-    else hipLaunchKernelGGL((rmsnorm_kernel<8, TY>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim);
+    const unsigned grid = blocks_for((rows + 1) / 2, 4);
+    const int nv2 = dim / 2;  // float4s of a pair
+    if (nv2 <= 64) hipLaunchKernelGGL((rmsnorm_kernel<1, TY>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim);
+    else if (nv2 <= 128) hipLaunchKernelGGL((rmsnorm_kernel<2, TY>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim);
+    else if (nv2 <= 192) hipLaunchKernelGGL((rmsnorm_kernel<3, TY>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim);
+    else if (nv2 <= 256) hipLaunchKernelGGL((rmsnorm_kernel<4, TY>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim);
+    else if (nv2 <= 512) hipLaunchKernelGGL((rmsnorm_kernel<8, TY>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim);
+    else hipLaunchKernelGGL((rmsnorm_kernel<16, TY>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim);
     return sync_debug(s, "rmsnorm_kernel");
 }
 
 bool rmsnorm_h2(hipStream_t s, const float *x, int ldx, const float *gamma, float *y, int ldy, int64_t rows, int dim,
                 const float *bound, KernelTimer *t) {
-    if (dim % 16 || dim > 2048 || rows <= 0 || rows > INT32_MAX / 2 || !bound) {
-        set_error("rmsnorm_h2: unsupported dim %d", dim);
+    if (dim % 16 || dim > 2048 || rows <= 0 || rows > INT32_MAX / 2 || !bound || ldx != dim || ldy != dim) {
+        set_error("rmsnorm_h2: unsupported dim %d or row pitches %d/%d", dim, ldx, ldy);
         return false;
     }
     Scope sc(t, s, "rmsnorm");
-    const unsigned grid = blocks_for(rows, 4);
-    const int nv = dim / 4;
-    if (nv <= 64) hipLaunchKernelGGL((rmsnorm_h2_kernel<1>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
-    else if (nv <= 128) hipLaunchKernelGGL((rmsnorm_h2_kernel<2>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
-    else if (nv <= 256) hipLaunchKernelGGL((rmsnorm_h2_kernel<4>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
-    else hipLaunchKernelGGL((rmsnorm_h2_kernel<8>), dim3(grid), dim3(256), 0, s, x, ldx, gamma, y, ldy, (int)rows, dim, bound);
+    const unsigned grid = blocks_for((rows + 1) / 2, 4);
+    const int nv2 = dim / 2;
+    if (nv2 <= 64) hipLaunchKernelGGL((rmsnorm_h2_kernel<1>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim, bound);
+    else if (nv2 <= 128) hipLaunchKernelGGL((rmsnorm_h2_kernel<2>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim, bound);
+    else if (nv2 <= 192) hipLaunchKernelGGL((rmsnorm_h2_kernel<3>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim, bound);
+    else if (nv2 <= 256) hipLaunchKernelGGL((rmsnorm_h2_kernel<4>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim, bound);
+    else if (nv2 <= 512) hipLaunchKernelGGL((rmsnorm_h2_kernel<8>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim, bound);
+    else hipLaunchKernelGGL((rmsnorm_h2_kernel<16>), dim3(grid), dim3(256), 0, s, x, gamma, y, (int)rows, dim, bound);
     return sync_debug(s, "rmsnorm_h2_kernel");
 }
 
@@ -895,7 +901,7 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     // rotary + attention + gates (products as fp16 two-piece splits on the
     // default fp32 path)
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32,
-                   w.bounds && w.att_h2 ? w.bounds + 1 : nullptr))
+                   precision == PREC_FP32 && w.bounds && w.att_h2 ? w.bounds + 1 : nullptr))
         return false;
     // out projection added to the residual stream
     if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;

@@ -12,7 +12,13 @@ overlap-add, band split, mask estimator.
 
 Work per launch is algorithmic (each tensor read and written once; 2*M*K*N
 per GEMM); time is the mean over repetitions measured with HIP events on the
-launch stream.  One JSON line per kernel on stdout.
+launch stream.  The isolated elementwise kernels cycle over at least four
+buffer sets of at least 1 GB together, so no repetition finds its operands
+in the 256 MB Infinity Cache (cold-cache HBM figures).  One JSON line per
+kernel on stdout; each names the device kernel it times ("device", a regular
+expression) and how many of its dispatches the record made ("dispatches":
+warm-up, then the timed ones), so kernel_stats can pair it with a
+rocprofv3 kernel trace of the same run.
 
     PYTHONPATH=karaoke-platform-sidecar-native_amd python -m vocalarc_hip.kernel_bench
 """
@@ -28,32 +34,58 @@ import numpy as np
 HBM_GBS = 8000.0
 FP32_TFLOPS = 157.3
 BF16_TFLOPS = 2500.0
+FP16_TFLOPS = 2500.0
 
 
-def _event_time(fn, reps: int) -> float:
+def _event_time(fn, reps: int) -> tuple[float, int]:
+    """(mean ms per call, calls made) of `fn` after one untimed call."""
+    return _event_time_sets([fn], reps)
+
+
+def _event_time_sets(fns, reps: int) -> tuple[float, int]:
+    """Mean ms per call over `reps` calls cycling through `fns` (one per
+    buffer set), after one untimed call of each; returns (ms, calls made)."""
     import torch
-    fn()  # warm-up (also builds per-length tables)
+    for fn in fns:  # warm-up (also builds per-length tables)
+        fn()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(reps):
-        fn()
+    for i in range(reps):
+        fns[i % len(fns)]()
     b.record()
     b.synchronize()
-    return a.elapsed_time(b) / reps
+    return a.elapsed_time(b) / reps, len(fns) + reps
 
 
-def _emit(name: str, ms: float, *, gbytes: float | None = None, gflop: float | None = None, shape: str = "",
-          peak_tflops: float = FP32_TFLOPS, extra: dict | None = None) -> dict:
+def _sets_for(footprint_bytes: float) -> int:
+    """Buffer sets for a cold-cache measurement: at least 4, and at least
+    1 GB in all (four times the Infinity Cache)."""
+    return max(4, -(-int(1 << 30) // max(1, int(footprint_bytes))))
+
+
+def _emit(name: str, ms, *, gbytes: float | None = None, gflop: float | None = None, shape: str = "",
+          peak_tflops: float = FP32_TFLOPS, extra: dict | None = None, device: str | None = None,
+          per_call: int = 1, reps: int | None = None, mc_products: int = 1) -> dict:
+    """ms: (mean ms per call, calls made) from _event_time(_sets).  device:
+    regular expression of the kernel(s) one call launches, per_call of them
+    per call; reps: the timed calls among those made.  mc_products:
+    matrix-core products per algorithmic product (3 for the fp16 two-piece
+    kernels), giving the matrix-core fraction of peak."""
+    ms, calls = ms
     rec = {"kernel": name, "shape": shape, "ms": round(ms, 4)}
+    if device:
+        rec.update({"device": device, "per_call": per_call, "dispatches": calls * per_call,
+                    "timed_dispatches": reps * per_call})
     if gbytes is not None:
         gbs = gbytes / (ms * 1e-3)
         rec.update({"algorithmic_GB": round(gbytes, 4), "GB_per_s": round(gbs, 1),
                     "bound": "hbm", "frac_of_peak": round(gbs / HBM_GBS, 4)})
     if gflop is not None:
         tf = gflop / (ms * 1e-3) / 1e3
-        rec.update({"algorithmic_GFLOP": round(gflop, 2), "TFLOP_per_s": round(tf, 2),
-                    "bound": "mfma", "frac_of_peak": round(tf / peak_tflops, 4)})
+        rec.update({"algorithmic_GFLOP": round(gflop, 2), "TFLOP_per_s": round(tf, 2), "bound": "mfma",
+                    "peak_TFLOP_per_s": peak_tflops, "mc_products": mc_products,
+                    "frac_of_peak": round(mc_products * tf / peak_tflops, 4)})
     if extra:
         rec.update(extra)
     print(json.dumps(rec), flush=True)
@@ -91,34 +123,48 @@ def main() -> int:
         cs = torch.randn(496 * 801 * 801, device=dev, generator=g)
         cd = torch.empty_like(cs)
         _emit("copy_reference", _event_time(lambda: cd.copy_(cs), reps), gbytes=2 * cs.numel() * 4 / 1e9,
-              shape="1.27 GB -> 1.27 GB")
+              shape="1.27 GB -> 1.27 GB", device=r"__amd_rocclr_copyBuffer", reps=reps)
         del cs, cd
 
     if "c1" in groups:
         rows, dim = 49662, 384
-        x = torch.randn(rows, dim, device=dev, generator=g)
         gamma = 1 + 0.02 * torch.randn(dim, device=dev, generator=g)
-        y = torch.empty_like(x)
-        _emit("rmsnorm", _event_time(lambda: ctx.rmsnorm(x, gamma, y, rows, dim), reps),
-              gbytes=2 * rows * dim * 4 / 1e9, shape="[49662,384]")
-        s = torch.randn(496 * 801, 801, device=dev, generator=g)
-        so = torch.empty_like(s)
-        _emit("softmax_rows", _event_time(lambda: ctx.softmax_rows(s, so, 496 * 801, 801), reps),
-              gbytes=2 * s.numel() * 4 / 1e9, shape="[496,801,801]")
-        del s, so
+        n = _sets_for(2 * rows * dim * 4)
+        xs = [torch.randn(rows, dim, device=dev, generator=g) for _ in range(n)]
+        ys = [torch.empty_like(x) for x in xs]
+        _emit("rmsnorm", _event_time_sets([lambda x=x, y=y: ctx.rmsnorm(x, gamma, y, rows, dim)
+                                           for x, y in zip(xs, ys)], reps),
+              gbytes=2 * rows * dim * 4 / 1e9, shape=f"[49662,384], {n} buffer sets", device=r"rmsnorm_kernel", reps=reps)
+        del xs, ys
+        srows, slen = 496 * 801, 801
+        n = _sets_for(2 * srows * slen * 4)
+        ss = [torch.randn(srows, slen, device=dev, generator=g) for _ in range(n)]
+        sos = [torch.empty_like(t) for t in ss]
+        _emit("softmax_rows", _event_time_sets([lambda a=a, b=b: ctx.softmax_rows(a, b, srows, slen)
+                                                for a, b in zip(ss, sos)], reps),
+              gbytes=2 * srows * slen * 4 / 1e9, shape=f"[496,801,801], {n} buffer sets", device=r"softmax_rows_kernel", reps=reps)
+        del ss, sos
         for b, length in ((62, 801), (801, 62)):
-            r = torch.randn(b, 8, length, 64, device=dev, generator=g)
-            _emit("rope", _event_time(lambda: ctx.rope_bhld(r, b * 8, length), reps),
-                  gbytes=2 * r.numel() * 4 / 1e9, shape=f"[{b},8,{length},64]")
-        gi = torch.randn(rows, 3072, device=dev, generator=g)
-        go = torch.empty(rows, 1536, device=dev)
-        _emit("geglu", _event_time(lambda: ctx.geglu(gi, go, rows, 1536), reps),
-              gbytes=(gi.numel() + go.numel()) * 4 / 1e9, shape="[49662,3072]->[49662,1536]")
-        del gi, go
-        r = torch.randn(rows, dim, device=dev, generator=g)
-        _emit("residual_add", _event_time(lambda: ctx.residual_add(x, r, rows * dim), reps),
-              gbytes=3 * rows * dim * 4 / 1e9, shape="[49662,384]")
-        del x, y, r
+            n = _sets_for(2 * b * 8 * length * 64 * 4)
+            rs = [torch.randn(b, 8, length, 64, device=dev, generator=g) for _ in range(n)]
+            _emit("rope", _event_time_sets([lambda r=r: ctx.rope_bhld(r, b * 8, length) for r in rs], reps),
+                  gbytes=2 * rs[0].numel() * 4 / 1e9, shape=f"[{b},8,{length},64], {n} buffer sets",
+                  device=r"rope_bhld_kernel", reps=reps)
+            del rs
+        n = _sets_for(rows * (3072 + 1536) * 4)
+        gis = [torch.randn(rows, 3072, device=dev, generator=g) for _ in range(n)]
+        gos = [torch.empty(rows, 1536, device=dev) for _ in range(n)]
+        _emit("geglu", _event_time_sets([lambda a=a, b=b: ctx.geglu(a, b, rows, 1536) for a, b in zip(gis, gos)], reps),
+              gbytes=rows * (3072 + 1536) * 4 / 1e9, shape=f"[49662,3072]->[49662,1536], {n} buffer sets",
+              device=r"geglu_kernel", reps=reps)
+        del gis, gos
+        n = _sets_for(3 * rows * dim * 4)
+        xs = [torch.randn(rows, dim, device=dev, generator=g) for _ in range(n)]
+        rs = [torch.randn(rows, dim, device=dev, generator=g) for _ in range(n)]
+        _emit("residual_add", _event_time_sets([lambda x=x, r=r: ctx.residual_add(x, r, rows * dim)
+                                                for x, r in zip(xs, rs)], reps),
+              gbytes=3 * rows * dim * 4 / 1e9, shape=f"[49662,384], {n} buffer sets", device=r"residual_add_kernel", reps=reps)
+        del xs, rs
 
     if "gemm" in groups:
         # the transformer GEMMs of one 8-window pass (M = 8 * 801 * 62 tokens)
@@ -133,8 +179,9 @@ def main() -> int:
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
             b = torch.randn(N, device=dev, generator=g)
             c = torch.zeros(M, ocols, device=dev)
-            _emit(name, _event_time(lambda: ctx.gemm(a, w, c, M, N, K, bias=b, epilogue=epi), max(3, reps // 4)),
-                  gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}")
+            r = max(3, reps // 4)
+            _emit(name, _event_time(lambda: ctx.gemm(a, w, c, M, N, K, bias=b, epilogue=epi), r),
+                  gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", device=r"gemm_f32_kernel", reps=r)
             del a, w, b, c
 
     if "split" in groups:
@@ -154,10 +201,10 @@ def main() -> int:
             ctx.split_weights(w, ws, N, K)
             b = torch.randn(N, device=dev, generator=g)
             c = torch.zeros(M, ocols, device=dev)
-            ms = _event_time(lambda: ctx.gemm_split(a, ws, c, M, N, K, bias=b, epilogue=epi), max(3, reps // 4))
-            gflop = 2.0 * M * K * N / 1e9
-            _emit(name, ms, gflop=gflop, shape=f"M={M} K={K} N={N}",
-                  extra={"bf16_matrix_core_frac": round(6 * gflop / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
+            r = max(3, reps // 4)
+            t = _event_time(lambda: ctx.gemm_split(a, ws, c, M, N, K, bias=b, epilogue=epi), r)
+            _emit(name, t, gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=BF16_TFLOPS,
+                  mc_products=6, device=r"gemm_split_kernel", reps=r)
             del a, w, ws, b, c
 
     if "h2" in groups or "ff1" in groups:
@@ -189,11 +236,10 @@ def main() -> int:
                 a = ah
             else:
                 bound = float(a.abs().max())
-            ms = _event_time(lambda: ctx.gemm_h2(a, wp, c, M, N, K, bias=b, epilogue=epi, a_bound=bound, a_rows=rows),
-                             max(3, reps // 4))
-            gflop = 2.0 * M * K * N / 1e9
-            _emit(name, ms, gflop=gflop, shape=f"M={M} K={K} N={N}",
-                  extra={"matrix_core_frac": round(3 * gflop / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
+            r = max(3, reps // 4)
+            t = _event_time(lambda: ctx.gemm_h2(a, wp, c, M, N, K, bias=b, epilogue=epi, a_bound=bound, a_rows=rows), r)
+            _emit(name, t, gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=FP16_TFLOPS,
+                  mc_products=3, device=r"gemm_h2_kernel", reps=r)
             del a, w, wp, b, c
 
     if "bf16" in groups:
@@ -211,27 +257,39 @@ def main() -> int:
             b = torch.randn(N, device=dev, generator=g)
             c = torch.zeros(M, ocols, device=dev, dtype=torch.bfloat16 if c16 else torch.float32)
             flags = native.BF16_A | (native.BF16_C if c16 else 0)
-            _emit(name, _event_time(lambda: ctx.gemm_bf16(a, wh, c, M, N, K, K, bias=b, epilogue=epi, flags=flags),
-                                    max(3, reps // 4)),
-                  gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=BF16_TFLOPS)
+            r = max(3, reps // 4)
+            _emit(name, _event_time(lambda: ctx.gemm_bf16(a, wh, c, M, N, K, K, bias=b, epilogue=epi, flags=flags), r),
+                  gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=BF16_TFLOPS,
+                  device=r"gemm_bf16_(dma_)?kernel", reps=r)
             del a, w, wh, b, c
 
     if "attn" in groups:
+        # the two attention shapes of one 8-window pass; the fp16 two-piece
+        # calls also compute max|qkv| (absmax kernels, not counted in the
+        # rocprof pairing of the attention kernel itself)
+        r = max(3, reps // 4)
         for S, L in ((8 * 62, 801), (8 * 801, 62)):
             qkv = torch.randn(S * L, 3 * 512, device=dev, generator=g)
             o = torch.empty(S * L, 512, device=dev)
-            _emit("attention", _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True), max(3, reps // 4)),
-                  gflop=4.0 * S * 8 * L * L * 64 / 1e9, shape=f"S={S} L={L} H=8")
-            if L > 64:
-                # the default fp32 path's time-axis attention: split bf16 products
-                gf = 4.0 * S * 8 * L * L * 64 / 1e9
-                ms = _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True, split=True), max(3, reps // 4))
-                _emit("attention_split", ms, gflop=gf, shape=f"S={S} L={L} H=8",
-                      extra={"bf16_matrix_core_frac": round(6 * gf / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
-                # the default path's kernel: fp16 two-piece products (scales from max|qkv|)
-                ms = _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True, h2=True), max(3, reps // 4))
-                _emit("attention_h2", ms, gflop=gf, shape=f"S={S} L={L} H=8",
-                      extra={"matrix_core_frac": round(3 * gf / (ms * 1e-3) / 1e3 / BF16_TFLOPS, 4)})
+            gf = 4.0 * S * 8 * L * L * 64 / 1e9
+            long = L > 64
+            _emit("attention_fp32", _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True), r), gflop=gf,
+                  shape=f"S={S} L={L} H=8", reps=r,
+                  device=r"vh::attention_kernel<4" if long else r"attention_short_kernel<")
+            if long:
+                _emit("attention_split", _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True, split=True), r),
+                      gflop=gf, shape=f"S={S} L={L} H=8", peak_tflops=BF16_TFLOPS, mc_products=6,
+                      device=r"attention_split_kernel", reps=r)
+            # the default path's kernels: fp16 two-piece products; the band
+            # axis (15.5 FLOP per byte) is priced against HBM: q, k, v read
+            # and the output written once
+            t = _event_time(lambda: ctx.attention(qkv, o, S, L, 8, True, h2=True), r)
+            if long:
+                _emit("attention_h2", t, gflop=gf, shape=f"S={S} L={L} H=8", peak_tflops=FP16_TFLOPS, mc_products=3,
+                      reps=r, device=r"attention_h2_kernel")
+            else:
+                _emit("attention_short_h2", t, gbytes=S * L * 4 * 512 * 4 / 1e9, shape=f"S={S} L={L} H=8", reps=r,
+                      device=r"attention_short_h2_kernel", extra={"algorithmic_GFLOP": round(gf, 2)})
             del qkv, o
 
     if "c2" in groups or "c3" in groups:
@@ -245,11 +303,11 @@ def main() -> int:
             xt = torch.randn(B, T, D, device=dev, generator=g)
             att_t = 4.0 * B * 8 * T * T * 64 / 1e9
             _emit("time_transformer", _event_time(lambda: model.transformer(0, 0, xt, B, T), max(3, reps // 4)),
-                  gflop=lin + att_t, shape="62 seq x 801, dim 384")
+                  gflop=lin + att_t, shape="62 seq x 801, dim 384", peak_tflops=FP16_TFLOPS, mc_products=3)
             xb = torch.randn(T, B, D, device=dev, generator=g)
             att_b = 4.0 * T * 8 * B * B * 64 / 1e9
             _emit("band_transformer", _event_time(lambda: model.transformer(0, 1, xb, T, B), max(3, reps // 4)),
-                  gflop=lin + att_b, shape="801 seq x 62, dim 384")
+                  gflop=lin + att_b, shape="801 seq x 62, dim 384", peak_tflops=FP16_TFLOPS, mc_products=3)
             del xt, xb
         if "c3" in groups:
             x = torch.from_numpy(audio.sine_mix(60.0, 60)).to(dev)
@@ -259,19 +317,23 @@ def main() -> int:
             fm = native.SPEC_FRAME_MAJOR
             src = torch.empty(d.channels, Tf, d.freq_bins, 2, device=dev)
             _emit("stft", _event_time(lambda: model.stft(x, length, src, fm), reps),
-                  gbytes=(x.numel() + src.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}")
+                  gbytes=(x.numel() + src.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}", device=r"stft_kernel", reps=reps)
             mask = torch.randn_like(src)
             out = torch.empty_like(x)
             _emit("istft", _event_time(lambda: model.istft(src, mask, length, out, fm), reps),
-                  gbytes=(2 * src.numel() + out.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}")
+                  gbytes=(2 * src.numel() + out.numel()) * 4 / 1e9, shape=f"60 s, T={Tf}",
+                  device=r"istft_frames_kernel|ola_kernel", per_call=2, reps=reps)
             seq = torch.empty(d.bands, Tf, D, device=dev)
             _emit("band_split", _event_time(lambda: model.band_split(src, Tf, seq, fm), reps),
-                  gflop=2.0 * Tf * sum(d.input_dims()) * D / 1e9, shape=f"T={Tf}, 62 bands")
+                  gflop=2.0 * Tf * sum(d.input_dims()) * D / 1e9, shape=f"T={Tf}, 62 bands",
+                  device=r"band_gather_norm_kernel|gemm_f32_batched_kernel", per_call=2, reps=reps)
             feats = torch.randn(Tf, d.bands, D, device=dev, generator=g)
             mout = torch.empty_like(src)
             gf = 2.0 * Tf * (d.bands * D * d.mask_hidden + d.mask_hidden * 2 * sum(d.input_dims())) / 1e9
-            _emit("mask_estimator", _event_time(lambda: model.mask_estimate(feats, Tf, mout, fm), max(3, reps // 4)),
-                  gflop=gf, shape=f"T={Tf}, 62 bands")
+            r = max(3, reps // 4)
+            _emit("mask_estimator", _event_time(lambda: model.mask_estimate(feats, Tf, mout, fm), r),
+                  gflop=gf, shape=f"T={Tf}, 62 bands", peak_tflops=FP16_TFLOPS, mc_products=3,
+                  device=r"gemm_h2_batched_kernel|mask_glu_scatter_kernel", per_call=3, reps=r)
         model.close()
     ctx.close()
     return 0

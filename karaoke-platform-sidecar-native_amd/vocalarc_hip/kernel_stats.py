@@ -1,11 +1,20 @@
-"""Summarise a `rocprofv3 --kernel-trace --stats` run of bench.py as markdown.
+"""Summarise rocprofv3 runs as markdown.
 
-Reads `*_kernel_stats.csv` from the run directory and the bench.py JSON line
-the same command printed, and writes a short table (kernel, calls, total and
-average duration, share) plus the live HIP-event figure of the dominant
-kernel for comparison:
+bench.py under `rocprofv3 --kernel-trace --stats`: reads `*_kernel_stats.csv`
+from the run directory and the bench.py JSON line the same command printed,
+and writes a short table (kernel, calls, total and average duration, share)
+plus the live HIP-event figure of the dominant kernel for comparison:
 
     python -m vocalarc_hip.kernel_stats RUN_DIR BENCH_JSON OUT.md "<command>"
+
+kernel_bench under `rocprofv3 --kernel-trace`: pairs every kernel_bench
+record that names its device kernels with the trace's dispatches of those
+kernels, in order (the record's warm-up dispatches first, then its timed
+ones), and reports the rocprofv3 average per call beside the live HIP-event
+figure, with the achieved rate and fraction of peak from the record's
+algorithmic work:
+
+    python -m vocalarc_hip.kernel_stats kernels RUN_DIR BENCH_JSONL OUT.md "<command>"
 """
 
 from __future__ import annotations
@@ -70,7 +79,69 @@ def role(name: str) -> str:
     return ""
 
 
+def kernels(run_dir: str, jsonl: str, out: str, command: str) -> int:
+    path = next(Path(run_dir).rglob("*kernel_trace.csv"))
+    trace = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    recs = [json.loads(x) for x in Path(jsonl).read_text().splitlines() if x.startswith("{")]
+    lines = [
+        "# Per-kernel rocprofv3 time against the roofline (kernel_bench, command below)", "",
+        "Commands (repository root, MI355X box):", "", "```", command.strip(), "```", "",
+        f"Source: `{path.name}` (rocprofv3 kernel trace) paired in order with the kernel_bench JSON lines of the "
+        "same run: each record's device kernels, its warm-up dispatches, then its timed ones. `rocprof ms` is the "
+        "average per call over the timed dispatches (sum of the kernels one call launches); `live ms` is the "
+        "HIP-event mean over the same calls. Rates use the algorithmic work (each tensor read and written once; "
+        "2*M*K*N per GEMM); `frac` is against 8 TB/s HBM or the matrix-core peak of the instruction the kernel "
+        "runs (fp32 MFMA 157.3 TFLOP/s; bf16/fp16 2.5 PFLOP/s, times the piece products per fp32 product).", "",
+        "| kernel | shape | rocprof ms | live ms | algorithmic work | achieved | frac of peak |",
+        "|---|---|---:|---:|---:|---:|---:|",
+    ]
+    pos = 0
+    for r in recs:
+        rx = r.get("device")
+        live = r["ms"]
+        prof = None
+        if rx:
+            pat = re.compile(rx)
+            got = []
+            i = pos
+            while i < len(trace) and len(got) < r["dispatches"]:
+                if pat.search(trace[i]["Kernel_Name"]):
+                    got.append(trace[i])
+                i += 1
+            if len(got) == r["dispatches"]:
+                pos = i
+                timed = got[-r["timed_dispatches"]:]
+                ns = sum(int(t["End_Timestamp"]) - int(t["Start_Timestamp"]) for t in timed)
+                prof = ns / 1e6 / _timed_calls(r)
+        ms = prof if prof is not None else live
+        if "algorithmic_GB" in r and r.get("bound") == "hbm":
+            rate = r["algorithmic_GB"] / (ms * 1e-3)
+            work, ach, frac = f"{r['algorithmic_GB']:.3f} GB", f"{rate:.0f} GB/s", rate / 8000.0
+        elif "algorithmic_GFLOP" in r:
+            tf = r["algorithmic_GFLOP"] / (ms * 1e-3) / 1e3
+            k = r.get("mc_products", 1)
+            work = f"{r['algorithmic_GFLOP']:.1f} GFLOP"
+            ach = f"{tf:.1f} TFLOP/s" + (f" (x{k} = {k * tf:.0f} on the matrix cores)" if k > 1 else "")
+            frac = k * tf / r.get("peak_TFLOP_per_s", 157.3)
+        else:
+            work, ach, frac = "", "", None
+        lines.append(f"| {r['kernel']} | {r['shape']} | {'' if prof is None else f'{prof:.4f}'} | {live:.4f} | "
+                     f"{work} | {ach} | {'' if frac is None else f'{frac:.3f}'} |")
+    Path(out).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
+def _timed_calls(r: dict) -> int:
+    """Timed calls of a record: its timed dispatches over the dispatches one
+    call launches (dispatches = calls made x per call)."""
+    per_call = r.get("per_call", 1)
+    return max(1, r["timed_dispatches"] // per_call)
+
+
 def main() -> int:
+    if sys.argv[1] == "kernels":
+        return kernels(*sys.argv[2:6])
     run_dir, bench_json, out, command = sys.argv[1:5]
     path = next(Path(run_dir).rglob("*kernel_stats.csv"))
     rows = list(csv.DictReader(open(path)))

@@ -9,13 +9,15 @@ if the library is missing the import of `lib()` raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import weakref
 from pathlib import Path
 
 from .dims import CDims, ModelDims, to_c
 
 PKG = Path(__file__).resolve().parent.parent
-LIB_PATH = PKG / "lib" / "libvocalarc_hip.so"
+# VOCALARC_HIP_LIB names another build of the library (e.g. to compare two)
+LIB_PATH = Path(os.environ.get("VOCALARC_HIP_LIB", PKG / "lib" / "libvocalarc_hip.so"))
 
 # Every entry point declared in include/vocalarc_hip.h and include/native_gpu.h.
 HARNESS_SYMBOLS = [
