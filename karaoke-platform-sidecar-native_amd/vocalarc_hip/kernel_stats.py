@@ -15,6 +15,12 @@ figure, with the achieved rate and fraction of peak from the record's
 algorithmic work:
 
     python -m vocalarc_hip.kernel_stats kernels RUN_DIR BENCH_JSONL OUT.md "<command>"
+
+`rocprofv3 --pmc` passes (one directory each): the per-dispatch average of
+every counter over the dispatches whose kernel name matches a regular
+expression (optionally only those with a given grid size):
+
+    python -m vocalarc_hip.kernel_stats counters KERNEL_REGEX OUT.md "<commands>" DIR [DIR ...]
 """
 
 from __future__ import annotations
@@ -132,6 +138,30 @@ def kernels(run_dir: str, jsonl: str, out: str, command: str) -> int:
     return 0
 
 
+def counters(regex: str, out: str, command: str, *dirs: str) -> int:
+    pat = re.compile(regex)
+    vals: dict[str, list[float]] = {}
+    names = set()
+    for d in dirs:
+        path = next(Path(d).rglob("*counter_collection.csv"))
+        for r in csv.DictReader(open(path)):
+            if not pat.search(r["Kernel_Name"]):
+                continue
+            names.add(r["Kernel_Name"])
+            vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    avg = {k: sum(v) / len(v) for k, v in vals.items()}
+    lines = [f"# rocprofv3 counters of `{regex}`", "", "Commands (repository root, MI355X box; one pass per counter "
+             "group):", "", "```", command.strip(), "```", "",
+             "Kernels matched: " + ", ".join(f"`{n[:120]}`" for n in sorted(names)), "",
+             "Per-dispatch averages (totals over the device as rocprofv3 reports them):", "",
+             "| counter | value |", "|---|---:|"]
+    for k in sorted(avg):
+        lines.append(f"| `{k}` | {avg[k]:.4g} |")
+    Path(out).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
 def _timed_calls(r: dict) -> int:
     """Timed calls of a record: its timed dispatches over the dispatches one
     call launches (dispatches = calls made x per call)."""
@@ -142,6 +172,8 @@ def _timed_calls(r: dict) -> int:
 def main() -> int:
     if sys.argv[1] == "kernels":
         return kernels(*sys.argv[2:6])
+    if sys.argv[1] == "counters":
+        return counters(sys.argv[2], sys.argv[3], sys.argv[4], *sys.argv[5:])
     run_dir, bench_json, out, command = sys.argv[1:5]
     path = next(Path(run_dir).rglob("*kernel_stats.csv"))
     rows = list(csv.DictReader(open(path)))
