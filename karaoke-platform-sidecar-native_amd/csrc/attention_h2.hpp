@@ -233,9 +233,9 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
         halfx8 pp[2][2];
 #pragma unroll
         for (int st = 0; st < 2; st++)
-            split8_h2(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
-                      floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, 1.0f, pp[st][0],
-                      pp[st][1]);
+            split8_h2_unit(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
+                           floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, pp[st][0],
+                           pp[st][1]);
         halfx8 vp[2][2];
         auto read = [&](int step, halfx8 (&v)[2]) {
             const int st = step >> 1, t = step & 1;
@@ -344,11 +344,10 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
 // distinct 4-bank groups.  Two pieces of K and of V^T: 36 KB, four
 // workgroups per CU.
 VH_DEVICE void split4_h2(floatx4 v, float s, uint32_t &h01, uint32_t &h23, uint32_t &m01, uint32_t &m23) {
-    const float y0 = v[0] * s, y1 = v[1] * s, y2 = v[2] * s, y3 = v[3] * s;
-    h01 = pack_f16x2(y0, y1);
-    h23 = pack_f16x2(y2, y3);
-    m01 = pack_f16x2(y0 - f16_lo(h01), y1 - f16_hi(h01));
-    m23 = pack_f16x2(y2 - f16_lo(h23), y3 - f16_hi(h23));
+    h01 = pack_f16x2(v[0] * s, v[1] * s);
+    h23 = pack_f16x2(v[2] * s, v[3] * s);
+    m01 = m_pair_f16(v[0], v[1], s, h01);
+    m23 = m_pair_f16(v[2], v[3], s, h23);
 }
 
 template <typename TO>
@@ -422,9 +421,9 @@ __global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) 
         for (int c = 0; c < 2; c++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float y0 = vpre[2 * c][e] * v_scale, y1 = vpre[2 * c + 1][e] * v_scale;
-                const uint32_t hp = pack_f16x2(y0, y1);
-                const uint32_t mp = pack_f16x2(y0 - f16_lo(hp), y1 - f16_hi(hp));
+                const float x0 = vpre[2 * c][e], x1 = vpre[2 * c + 1][e];
+                const uint32_t hp = pack_f16x2(x0 * v_scale, x1 * v_scale);
+                const uint32_t mp = m_pair_f16(x0, x1, v_scale, hp);
                 const int dim = vd + 32 * c + e;
                 *reinterpret_cast<uint32_t *>(&Vp[0][dim][v_pos]) = hp;
                 *reinterpret_cast<uint32_t *>(&Vp[1][dim][v_pos]) = mp;

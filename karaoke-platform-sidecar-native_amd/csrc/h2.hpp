@@ -59,18 +59,51 @@ VH_DEVICE uint32_t pack_f16x2(float a, float b) {
     typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, halfx2));
 }
-VH_DEVICE float f16_lo(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p & 0xffffu)); }
-VH_DEVICE float f16_hi(uint32_t p) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(p >> 16)); }
+
+// The m pieces of two values x0 s, x1 s whose h pieces hp holds (as
+// pack_f16x2 made them): fp16(x s - h).  x s - h is formed exactly inside one
+// v_fma_mix_f32 per value (the fp16 h read in place, no conversion) and the
+// pair rounded by one v_cvt_pk_f16_f32: the bits of fp16(y - h), y = x s, in
+// 3 VALU per pair instead of 5.  s must not be a compile-time 1 (the
+// multiply-add would fold back into a conversion and a subtraction): pass
+// opaque_one() for unscaled values.
+VH_DEVICE uint32_t m_pair_f16(float x0, float x1, float s, uint32_t hp) {
+    typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+    const halfx2 h = __builtin_bit_cast(halfx2, hp);
+    return pack_f16x2(__builtin_fmaf(x0, s, -(float)h[0]), __builtin_fmaf(x1, s, -(float)h[1]));
+}
+
+// 1.0f that the compiler does not constant-fold (see m_pair_f16).
+VH_DEVICE float opaque_one() {
+    float one = 1.0f;
+    asm("" : "+v"(one));
+    return one;
+}
 
 // Eight fp32 values times s -> their h and m fp16 pieces, packed as the MFMA
-// operand wants them (a lane's eight k-values): 4 VALU per value.
+// operand wants them (a lane's eight k-values): 2.5 VALU per value.
 VH_DEVICE void split8_h2(floatx4 lo, floatx4 hi, float s, halfx8 &h, halfx8 &m) {
-    const float x[8] = {lo[0] * s, lo[1] * s, lo[2] * s, lo[3] * s, hi[0] * s, hi[1] * s, hi[2] * s, hi[3] * s};
+    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    uint32_t ph[4], pm[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        ph[e] = pack_f16x2(x[2 * e] * s, x[2 * e + 1] * s);
+        pm[e] = m_pair_f16(x[2 * e], x[2 * e + 1], s, ph[e]);
+    }
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    h = __builtin_bit_cast(halfx8, (u32x4){ph[0], ph[1], ph[2], ph[3]});
+    m = __builtin_bit_cast(halfx8, (u32x4){pm[0], pm[1], pm[2], pm[3]});
+}
+
+// The same for unscaled values (s = 1): 2 VALU per value.
+VH_DEVICE void split8_h2_unit(floatx4 lo, floatx4 hi, halfx8 &h, halfx8 &m) {
+    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const float one = opaque_one();
     uint32_t ph[4], pm[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         ph[e] = pack_f16x2(x[2 * e], x[2 * e + 1]);
-        pm[e] = pack_f16x2(x[2 * e] - f16_lo(ph[e]), x[2 * e + 1] - f16_hi(ph[e]));
+        pm[e] = m_pair_f16(x[2 * e], x[2 * e + 1], one, ph[e]);
     }
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     h = __builtin_bit_cast(halfx8, (u32x4){ph[0], ph[1], ph[2], ph[3]});
@@ -85,10 +118,8 @@ VH_HOST_DEVICE inline int h2_row_offset(int j) { return 16 * (j & 1) + 8 * (j >>
 // Four consecutive values (k 4j..4j+3 of the chunk at `chunk`) times s into
 // an h2 row: 8 bytes of h and 8 of m.
 VH_DEVICE void store4_h2(unsigned char *chunk, int j, floatx4 v, float s) {
-    const float y0 = v[0] * s, y1 = v[1] * s, y2 = v[2] * s, y3 = v[3] * s;
-    const uint32_t h01 = pack_f16x2(y0, y1), h23 = pack_f16x2(y2, y3);
-    const uint32_t m01 = pack_f16x2(y0 - f16_lo(h01), y1 - f16_hi(h01));
-    const uint32_t m23 = pack_f16x2(y2 - f16_lo(h23), y3 - f16_hi(h23));
+    const uint32_t h01 = pack_f16x2(v[0] * s, v[1] * s), h23 = pack_f16x2(v[2] * s, v[3] * s);
+    const uint32_t m01 = m_pair_f16(v[0], v[1], s, h01), m23 = m_pair_f16(v[2], v[3], s, h23);
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     const int o = h2_row_offset(j);
     *reinterpret_cast<u32x2 *>(chunk + o) = u32x2{h01, h23};
@@ -100,10 +131,8 @@ VH_DEVICE void store4_h2(unsigned char *chunk, int j, floatx4 v, float s) {
 // lane writes a whole 16-byte slot -- lanes 0, 1 the h slots, lanes 2, 3 the
 // m slots -- instead of two 8-byte halves.  Every lane of the quad takes part.
 VH_DEVICE void store4_h2_quad(unsigned char *chunk, int j, floatx4 v, float s) {
-    const float y0 = v[0] * s, y1 = v[1] * s, y2 = v[2] * s, y3 = v[3] * s;
-    const uint32_t h01 = pack_f16x2(y0, y1), h23 = pack_f16x2(y2, y3);
-    const uint32_t m01 = pack_f16x2(y0 - f16_lo(h01), y1 - f16_hi(h01));
-    const uint32_t m23 = pack_f16x2(y2 - f16_lo(h23), y3 - f16_hi(h23));
+    const uint32_t h01 = pack_f16x2(v[0] * s, v[1] * s), h23 = pack_f16x2(v[2] * s, v[3] * s);
+    const uint32_t m01 = m_pair_f16(v[0], v[1], s, h01), m23 = m_pair_f16(v[2], v[3], s, h23);
     const bool h_slot = j < 2;
     const uint32_t r0 = (uint32_t)__shfl_xor((int)(h_slot ? m01 : h01), 2, 64);
     const uint32_t r1 = (uint32_t)__shfl_xor((int)(h_slot ? m23 : h23), 2, 64);

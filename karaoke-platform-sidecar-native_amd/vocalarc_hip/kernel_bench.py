@@ -244,9 +244,10 @@ def main() -> int:
 
     if "bf16" in groups:
         # the same four GEMMs on bf16 matrix-core operands, with the operand
-        # types of the bf16 pipeline: bf16 activations in, bf16 FFN hidden out
+        # types of the bf16 pipeline: bf16 activations in, bf16 projections and
+        # FFN hidden layer out, fp32 residual stream
         M = 8 * 801 * 62
-        for name, K, N, epi, ocols, c16 in (("gemm_bf16_qkv_gates", 384, 1568, native.EPI_STORE, 1568, False),
+        for name, K, N, epi, ocols, c16 in (("gemm_bf16_qkv_gates", 384, 1568, native.EPI_STORE, 1568, True),
                                             ("gemm_bf16_out_residual", 512, 384, native.EPI_RESIDUAL, 384, False),
                                             ("gemm_bf16_ff1_geglu", 384, 3072, native.EPI_GEGLU, 1536, True),
                                             ("gemm_bf16_ff2_residual", 1536, 384, native.EPI_RESIDUAL, 384, False)):
