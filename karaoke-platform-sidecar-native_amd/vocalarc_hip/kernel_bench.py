@@ -95,9 +95,11 @@ def _emit(name: str, ms, *, gbytes: float | None = None, gflop: float | None = N
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--only", default="", help="comma list of groups: copy,c1,c2,c3,gemm,ff1,h2,split,attn,bf16")
+    ap.add_argument("--only", default="",
+                    help="comma list of groups: copy,c1,c2,c3,gemm,ff1,h2,split,attn,bf16,vendor")
     args = ap.parse_args()
-    groups = set(args.only.split(",")) if args.only else {"copy", "c1", "c2", "c3", "gemm", "h2", "split", "attn", "bf16"}
+    groups = (set(args.only.split(",")) if args.only else
+              {"copy", "c1", "c2", "c3", "gemm", "h2", "split", "attn", "bf16", "vendor"})
 
     import torch
 
@@ -263,6 +265,23 @@ def main() -> int:
                   gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=BF16_TFLOPS,
                   device=r"gemm_bf16_(dma_)?kernel", reps=r)
             del a, w, wh, b, c
+
+    if "vendor" in groups:
+        # reference point, not part of the library: the vendor GEMM (torch.matmul
+        # on hipBLASLt) on the same four shapes with a plain store -- no bias,
+        # no epilogue, C as wide as N (the fused kernels above add the bias,
+        # the GELU-GLU or the residual read-modify-write)
+        M = 8 * 801 * 62
+        for dt, tag, peak in ((torch.bfloat16, "bf16", BF16_TFLOPS), (torch.float32, "fp32", FP32_TFLOPS)):
+            for name, K, N in (("qkv_gates", 384, 1568), ("out", 512, 384), ("ff1", 384, 3072), ("ff2", 1536, 384)):
+                a = torch.randn(M, K, device=dev, generator=g).to(dt)
+                w = (0.05 * torch.randn(N, K, device=dev, generator=g)).to(dt)
+                c = torch.empty(M, N, device=dev, dtype=dt)
+                r = max(3, reps // 4)
+                _emit(f"vendor_{tag}_{name}", _event_time(lambda: torch.matmul(a, w.t(), out=c), r),
+                      gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=peak,
+                      device=r"^Cijk_", reps=r)
+                del a, w, c
 
     if "attn" in groups:
         # the two attention shapes of one 8-window pass; the fp16 two-piece

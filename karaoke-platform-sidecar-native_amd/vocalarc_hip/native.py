@@ -19,20 +19,6 @@ PKG = Path(__file__).resolve().parent.parent
 # VOCALARC_HIP_LIB names another build of the library (e.g. to compare two)
 LIB_PATH = Path(os.environ.get("VOCALARC_HIP_LIB", PKG / "lib" / "libvocalarc_hip.so"))
 
-# Every entry point declared in include/vocalarc_hip.h and include/native_gpu.h.
-HARNESS_SYMBOLS = [
-    "vh_create", "vh_destroy", "vh_set_stream", "vh_synchronize", "vh_last_error", "vh_device_name",
-    "vh_rmsnorm", "vh_rmsnorm_bf16", "vh_rmsnorm_h2", "vh_softmax_rows", "vh_rope_bhld", "vh_geglu", "vh_residual_add", "vh_gemm", "vh_gemm_bf16",
-    "vh_gemm_split", "vh_split_bytes", "vh_split_weights", "vh_gemm_h2", "vh_h2_bytes", "vh_split_weights_h2", "vh_operand_bounds", "vh_to_bf16", "vh_attention", "vh_attention_noalloc", "vh_model_load", "vh_model_free", "vh_model_set_precision", "vh_transformer", "vh_stft", "vh_istft", "vh_band_split",
-    "vh_mask_estimate", "vh_forward", "vh_separate", "vh_timing_enable", "vh_timing_reset", "vh_timing_get",
-]
-ABI_SYMBOLS = [
-    "native_gpu_create", "native_gpu_destroy", "native_gpu_matmul", "native_gpu_backend", "native_gpu_device",
-    "native_gpu_uses_full_batches", "native_gpu_can_use_full_batches", "native_gpu_transformer",
-    "native_gpu_resident_begin", "native_gpu_resident_transformer", "native_gpu_resident_transpose",
-    "native_gpu_resident_end", "native_gpu_resident_mask",
-]
-
 EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16, PRECISION_FP32_MFMA = 0, 1, 2
 BF16_A, BF16_C, BF16_STAGED = 1, 2, 4  # vh_gemm_bf16 operand flags; STAGED forces the register-staged kernel
@@ -44,6 +30,54 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
 _lib = None
+
+# Signatures (result, arguments) of every entry point declared in
+# include/vocalarc_hip.h (vh_*) and include/native_gpu.h (native_gpu_*).
+SIGNATURES = {
+    "vh_create": (_P, []), "vh_destroy": (None, [_P]), "vh_set_stream": (_I, [_P, _P]),
+    "vh_synchronize": (_I, [_P]), "vh_last_error": (ctypes.c_char_p, []), "vh_device_name": (ctypes.c_char_p, [_P]),
+    "vh_rmsnorm": (_I, [_P, _I64, _I, _P, _P, _P]), "vh_rmsnorm_bf16": (_I, [_P, _I64, _I, _P, _P, _P]),
+    "vh_rmsnorm_h2": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
+    "vh_softmax_rows": (_I, [_P, _I64, _I, _P, _P]),
+    "vh_rope_bhld": (_I, [_P, _I64, _I, _I, _P]),
+    "vh_geglu": (_I, [_P, _I64, _I, _P, _P]),
+    "vh_residual_add": (_I, [_P, _I64, _P, _P]),
+    "vh_gemm": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
+    "vh_gemm_bf16": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I, _I]),
+    "vh_gemm_split": (_I, [_P, _I64, _I, _I, _P, _I, _P, _P, _P, _I, _I]),
+    "vh_split_bytes": (ctypes.c_size_t, [_I, _I]),
+    "vh_split_weights": (_I, [_P, _I, _I, _P, _I, _P]),
+    "vh_gemm_h2": (_I, [_P, _I64, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _I, _I, _I]),
+    "vh_h2_bytes": (ctypes.c_size_t, [_I, _I]),
+    "vh_split_weights_h2": (_I, [_P, _I, _I, _P, _I, _P]),
+    "vh_operand_bounds": (_I, [_P, _P, _I, _P, _I, _P, _I, _P]),
+    "vh_to_bf16": (_I, [_P, _I64, _I, _P, _P, _I]),
+    "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
+    "vh_attention_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
+    "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
+    "vh_model_free": (None, [_P]), "vh_model_set_precision": (_I, [_P, _I]),
+    "vh_transformer": (_I, [_P, _P, _I, _I, _P, _I, _I]),
+    "vh_stft": (_I, [_P, _P, _P, _I, _P, _I]),
+    "vh_istft": (_I, [_P, _P, _P, _P, _I, _P, _I]),
+    "vh_band_split": (_I, [_P, _P, _P, _I, _P, _I]),
+    "vh_mask_estimate": (_I, [_P, _P, _P, _I, _P, _I]),
+    "vh_forward": (_I, [_P, _P, _P, _I, _P, _P]),
+    "vh_separate": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "vh_timing_enable": (_I, [_P, ctypes.c_char_p]), "vh_timing_reset": (_I, [_P]),
+    "vh_timing_get": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
+    "native_gpu_create": (_P, []), "native_gpu_destroy": (None, [_P]),
+    "native_gpu_matmul": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
+    "native_gpu_backend": (ctypes.c_char_p, [_P]), "native_gpu_device": (ctypes.c_char_p, [_P]),
+    "native_gpu_uses_full_batches": (_I, [_P]), "native_gpu_can_use_full_batches": (_I, [_P, _I]),
+    "native_gpu_transformer": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "native_gpu_resident_begin": (_I, [_P, _I, _I, _P]),
+    "native_gpu_resident_transformer": (_I, [_P, _I, _I, _P]),
+    "native_gpu_resident_transpose": (_I, [_P, _I, _I]),
+    "native_gpu_resident_end": (_I, [_P, _P]),
+    "native_gpu_resident_mask": (_I, [_P, _I, _P, _P, _P, _I]),
+}
+HARNESS_SYMBOLS = [n for n in SIGNATURES if n.startswith("vh_")]
+ABI_SYMBOLS = [n for n in SIGNATURES if n.startswith("native_gpu_")]
 
 
 class NativeError(RuntimeError):
@@ -58,50 +92,7 @@ def lib():
     if not LIB_PATH.exists():
         raise NativeError(f"{LIB_PATH} is missing: build it with `make -C {PKG}`")
     L = ctypes.CDLL(str(LIB_PATH))
-    sig = {
-        "vh_create": (_P, []), "vh_destroy": (None, [_P]), "vh_set_stream": (_I, [_P, _P]),
-        "vh_synchronize": (_I, [_P]), "vh_last_error": (ctypes.c_char_p, []), "vh_device_name": (ctypes.c_char_p, [_P]),
-        "vh_rmsnorm": (_I, [_P, _I64, _I, _P, _P, _P]), "vh_rmsnorm_bf16": (_I, [_P, _I64, _I, _P, _P, _P]),
-        "vh_rmsnorm_h2": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
-        "vh_softmax_rows": (_I, [_P, _I64, _I, _P, _P]),
-        "vh_rope_bhld": (_I, [_P, _I64, _I, _I, _P]),
-        "vh_geglu": (_I, [_P, _I64, _I, _P, _P]),
-        "vh_residual_add": (_I, [_P, _I64, _P, _P]),
-        "vh_gemm": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I]),
-        "vh_gemm_bf16": (_I, [_P, _I64, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I, _I]),
-        "vh_gemm_split": (_I, [_P, _I64, _I, _I, _P, _I, _P, _P, _P, _I, _I]),
-        "vh_split_bytes": (ctypes.c_size_t, [_I, _I]),
-        "vh_split_weights": (_I, [_P, _I, _I, _P, _I, _P]),
-        "vh_gemm_h2": (_I, [_P, _I64, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _I, _I, _I]),
-        "vh_h2_bytes": (ctypes.c_size_t, [_I, _I]),
-        "vh_split_weights_h2": (_I, [_P, _I, _I, _P, _I, _P]),
-        "vh_operand_bounds": (_I, [_P, _P, _I, _P, _I, _P, _I, _P]),
-        "vh_to_bf16": (_I, [_P, _I64, _I, _P, _P, _I]),
-        "vh_attention": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
-        "vh_attention_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _I, _I]),
-        "vh_model_load": (_P, [_P, ctypes.POINTER(CDims), _P, ctypes.c_size_t]),
-        "vh_model_free": (None, [_P]), "vh_model_set_precision": (_I, [_P, _I]),
-        "vh_transformer": (_I, [_P, _P, _I, _I, _P, _I, _I]),
-        "vh_stft": (_I, [_P, _P, _P, _I, _P, _I]),
-        "vh_istft": (_I, [_P, _P, _P, _P, _I, _P, _I]),
-        "vh_band_split": (_I, [_P, _P, _P, _I, _P, _I]),
-        "vh_mask_estimate": (_I, [_P, _P, _P, _I, _P, _I]),
-        "vh_forward": (_I, [_P, _P, _P, _I, _P, _P]),
-        "vh_separate": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P]),
-        "vh_timing_enable": (_I, [_P, ctypes.c_char_p]), "vh_timing_reset": (_I, [_P]),
-        "vh_timing_get": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
-        "native_gpu_create": (_P, []), "native_gpu_destroy": (None, [_P]),
-        "native_gpu_matmul": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
-        "native_gpu_backend": (ctypes.c_char_p, [_P]), "native_gpu_device": (ctypes.c_char_p, [_P]),
-        "native_gpu_uses_full_batches": (_I, [_P]), "native_gpu_can_use_full_batches": (_I, [_P, _I]),
-        "native_gpu_transformer": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
-        "native_gpu_resident_begin": (_I, [_P, _I, _I, _P]),
-        "native_gpu_resident_transformer": (_I, [_P, _I, _I, _P]),
-        "native_gpu_resident_transpose": (_I, [_P, _I, _I]),
-        "native_gpu_resident_end": (_I, [_P, _P]),
-        "native_gpu_resident_mask": (_I, [_P, _I, _P, _P, _P, _I]),
-    }
-    for name, (res, args) in sig.items():
+    for name, (res, args) in SIGNATURES.items():
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args
@@ -124,6 +115,21 @@ def ptr(t) -> int:
     if hasattr(t, "data_ptr"):
         return t.data_ptr()
     return t.ctypes.data
+
+
+def _opt(t):
+    """ptr(t), or a null pointer for None."""
+    return ptr(t) if t is not None else None
+
+
+def _out_cols(N: int, epilogue: int) -> int:
+    """Output columns of a linear with N weight rows (GELU-GLU halves them)."""
+    return N // 2 if epilogue == EPI_GEGLU else N
+
+
+def _att_flags(out_bf16: bool, bf16: bool, split: bool, h2: bool) -> int:
+    return ((ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0) | (ATT_SPLIT if split else 0) |
+            (ATT_H2 if h2 else 0))
 
 
 class Context:
@@ -188,15 +194,15 @@ class Context:
     def gemm(self, A, W, C, M: int, N: int, K: int, bias=None, epilogue: int = EPI_STORE,
              lda: int | None = None, ldw: int | None = None, ldc: int | None = None):
         _ok(lib().vh_gemm(self.h, M, N, K, ptr(A), lda or K, ptr(W), ldw or K,
-                          ptr(bias) if bias is not None else None, ptr(C),
-                          ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm")
+                          _opt(bias), ptr(C),
+                          ldc or _out_cols(N, epilogue), epilogue), "vh_gemm")
 
     def gemm_bf16(self, A, Wh, C, M: int, N: int, K: int, ldw: int, bias=None, epilogue: int = EPI_STORE,
                   lda: int | None = None, ldc: int | None = None, flags: int = 0):
         """Wh: bf16 weight copy [N][ldw] (see to_bf16); flags: BF16_A / BF16_C operand types, BF16_STAGED."""
         _ok(lib().vh_gemm_bf16(self.h, M, N, K, ptr(A), lda or K, ptr(Wh), ldw,
-                               ptr(bias) if bias is not None else None, ptr(C),
-                               ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue, flags), "vh_gemm_bf16")
+                               _opt(bias), ptr(C),
+                               ldc or _out_cols(N, epilogue), epilogue, flags), "vh_gemm_bf16")
 
     @staticmethod
     def split_bytes(N: int, K: int) -> int:
@@ -211,8 +217,8 @@ class Context:
                    lda: int | None = None, ldc: int | None = None):
         """fp32-accurate linear on bf16 matrix cores; Ws from split_weights."""
         _ok(lib().vh_gemm_split(self.h, M, N, K, ptr(A), lda or K, ptr(Ws),
-                                ptr(bias) if bias is not None else None, ptr(C),
-                                ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue), "vh_gemm_split")
+                                _opt(bias), ptr(C),
+                                ldc or _out_cols(N, epilogue), epilogue), "vh_gemm_split")
 
     @staticmethod
     def h2_bytes(N: int, K: int) -> int:
@@ -228,14 +234,14 @@ class Context:
         """fp32-accurate linear on fp16 matrix cores; Wp from split_weights_h2; a_bound bounds |A| (0: max|A|);
         a_rows: A is given as h2 rows split with a_bound (rmsnorm_h2)."""
         _ok(lib().vh_gemm_h2(self.h, M, N, K, ptr(A), lda or K, float(a_bound), ptr(Wp),
-                             ptr(bias) if bias is not None else None, ptr(C),
-                             ldc or (N // 2 if epilogue == EPI_GEGLU else N), epilogue, 1 if a_rows else 0),
+                             _opt(bias), ptr(C),
+                             ldc or _out_cols(N, epilogue), epilogue, 1 if a_rows else 0),
             "vh_gemm_h2")
 
     def operand_bounds(self, gamma, D: int, out, W=None, N: int = 0, bias=None, square: bool = False):
         """Device bounds out[0..1] of the A operands after an RMSNorm with gain gamma (see vh_operand_bounds)."""
-        _ok(lib().vh_operand_bounds(self.h, ptr(gamma), D, ptr(W) if W is not None else None, N,
-                                    ptr(bias) if bias is not None else None, 1 if square else 0, ptr(out)),
+        _ok(lib().vh_operand_bounds(self.h, ptr(gamma), D, _opt(W), N,
+                                    _opt(bias), 1 if square else 0, ptr(out)),
             "vh_operand_bounds")
 
     def to_bf16(self, src, dst, rows: int, cols: int, ld: int):
@@ -246,17 +252,14 @@ class Context:
         """bf16: qkv is bf16 and the bf16-MFMA kernel runs; out_bf16: out is bf16; split: fp32 accuracy on the
         bf16 matrix cores (three-piece splits, length > 64); h2: fp32 accuracy on the fp16 matrix cores (two-piece
         splits, scales from max|qkv|, any length)."""
-        flags = ((ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0) | (ATT_SPLIT if split else 0) |
-                 (ATT_H2 if h2 else 0))
-        _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), flags),
-            "vh_attention")
+        _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary),
+                               _att_flags(out_bf16, bf16, split, h2)), "vh_attention")
 
     def attention_noalloc(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True,
                           out_bf16: bool = False, bf16: bool = False, split: bool = False, h2: bool = False) -> int:
         """vh_attention_noalloc (no device allocation; length <= NOALLOC_MAX_LENGTH); returns its status."""
-        flags = ((ATT_OUT_BF16 if out_bf16 else 0) | (ATT_BF16 if bf16 else 0) | (ATT_SPLIT if split else 0) |
-                 (ATT_H2 if h2 else 0))
-        return lib().vh_attention_noalloc(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary), flags)
+        return lib().vh_attention_noalloc(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary),
+                                          _att_flags(out_bf16, bf16, split, h2))
 
     # -- timing --
     def timing(self, classes: str | None = "*"):
@@ -317,8 +320,8 @@ class Model:
 
     def forward(self, audio, length: int, vocals, instrumental=None):
         _ok(lib().vh_forward(self.ctx.h, self.h, ptr(audio), length, ptr(vocals),
-                             ptr(instrumental) if instrumental is not None else None), "vh_forward")
+                             _opt(instrumental)), "vh_forward")
 
     def separate(self, audio, length: int, chunk: int, step: int, batch: int, vocals, instrumental=None):
         _ok(lib().vh_separate(self.ctx.h, self.h, ptr(audio), length, chunk, step, batch, ptr(vocals),
-                              ptr(instrumental) if instrumental is not None else None), "vh_separate")
+                              _opt(instrumental)), "vh_separate")
