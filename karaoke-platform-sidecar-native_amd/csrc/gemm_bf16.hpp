@@ -249,6 +249,84 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_batched_kernel(Ge
     gemm_bf16_body<EPI, TA, TC, BK, WM, WN, FM, FN>(b.d[blockIdx.z], (int)blockIdx.x);
 }
 
+// bf16-output epilogue of a wave's 64 x 64 block through LDS, for MFMAs that
+// take the B tile as their first operand: the accumulators then hold C
+// transposed -- lane (li, lh), register r of acc[i][j] is row 32 i + li,
+// column 32 j + 8 (r / 4) + 4 lh + r % 4 of the block -- so each lane has
+// four consecutive columns per register quad.  The lane writes each quad,
+// finished (bias, activation or GELU-GLU) and rounded, as 8 bytes into the
+// wave's own LDS block of 64 rows (`stage`, 64 x (OC + 8) bf16, OC the
+// block's output columns), then every lane stores 16 bytes of a row, so a
+// store instruction covers whole 64- or 128-byte row segments instead of
+// 2-byte scatters (bf16 QKV -7%, FFN up -9% against the per-element store).
+template <int EPI>
+VH_DEVICE void gemm_bf16_epilogue_staged(const GemmDescBF16 &d, const floatx16 (&acc)[2][2], bf16 *stage, int row0,
+                                         int col0, int lane) {
+    constexpr int OC = EPI == EPI_GEGLU ? 32 : 64;
+    constexpr int PITCH = OC + 8;  // 16-byte aligned rows
+    const int li = lane & 31, lh = lane >> 5;
+    auto quad = [](const floatx16 &v, int q) { return floatx4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}; };
+    auto bias4 = [&](int c) {  // columns c .. c+3, clamped to N (columns past N are never stored)
+        floatx4 b = {0.f, 0.f, 0.f, 0.f};
+        if (d.bias)
+            for (int e = 0; e < 4; e++) b[e] = d.bias[min(c + e, d.N - 1)];
+        return b;
+    };
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if constexpr (EPI == EPI_GEGLU) {
+            // value columns 8q + 4lh .. +3 of the 64-wide group, gates 32 further
+            const int nv = col0 + 8 * q + 4 * lh;
+            const floatx4 bv = bias4(nv), bg = bias4(nv + 32);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const floatx4 v = quad(acc[i][0], q), g = quad(acc[i][1], q);
+                floatx4 o;
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = (v[e] + bv[e]) * gelu_dev(g[e] + bg[e]);
+                *reinterpret_cast<bf16x4 *>(&stage[(32 * i + li) * PITCH + 8 * q + 4 * lh]) = to_bf16x4(o);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int c = 32 * j + 8 * q + 4 * lh;
+                const floatx4 b = bias4(col0 + c);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const floatx4 v = quad(acc[i][j], q);
+                    floatx4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        o[e] = v[e] + b[e];
+                        if constexpr (EPI == EPI_GELU) o[e] = gelu_dev(o[e]);
+                        else if constexpr (EPI == EPI_TANH) o[e] = tanhf(o[e]);
+                    }
+                    *reinterpret_cast<bf16x4 *>(&stage[(32 * i + li) * PITCH + c]) = to_bf16x4(o);
+                }
+            }
+        }
+    }
+    constexpr int LPR = OC / 8;  // lanes per row, 16 bytes each
+    constexpr int RPI = 64 / LPR;  // rows per store instruction
+    const int oc0 = EPI == EPI_GEGLU ? col0 / 2 : col0;
+    const int ncols = EPI == EPI_GEGLU ? d.N / 2 : d.N;
+    bf16 *C = static_cast<bf16 *>(d.C);
+#pragma unroll
+    for (int t = 0; t < 64 / RPI; t++) {
+        const int rr = RPI * t + lane / LPR, c8 = 8 * (lane % LPR);
+        const bf16x8 v = *reinterpret_cast<const bf16x8 *>(&stage[rr * PITCH + c8]);
+        const int row = row0 + rr, col = oc0 + c8;
+        if (row < d.M) {
+            bf16 *dst = C + (size_t)row * d.ldc + col;
+            if (col + 8 <= ncols) {
+                *reinterpret_cast<bf16x8 *>(dst) = v;
+            } else {
+                for (int e = 0; e < 8 && col + e < ncols; e++) dst[e] = v[e];
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Pipelined variant for bf16 A with K % 32 == 0 (every bf16-variant GEMM but
 // the band split): the same 256x128 block of 8 waves x (64x64), but operands
@@ -259,7 +337,10 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_batched_kernel(Ge
 // of 64 B, lane l carrying row l/4, 16-byte position l%4.  Position p of row
 // r holds K-chunk p ^ ((r / 4) % 4), so the 16-byte operand reads (32 rows,
 // one chunk) fall on distinct banks.  Identical operands and MFMA order to
-// the register-staged kernel, so results are bit-identical.
+// the register-staged kernel, so results are bit-identical (for bf16 outputs
+// each MFMA takes its two operands the other way round, which gives the
+// transposed block with the same bits: checked against the register-staged
+// kernel by the boundary tests).
 //
 // The loads are issued from inline assembly and waited for with explicit
 // s_waitcnt vmcnt(N) + barrier: the compiler's own wait insertion treats any
@@ -284,6 +365,9 @@ constexpr int GBD_BM = 256, GBD_BN = 128, GBD_BK = 32, GBD_STAGES = 3, GBD_THREA
 
 template <int EPI, typename TC>
 __device__ __forceinline__ void gemm_bf16_dma_body(const GemmDescBF16 &d, int tile) {
+    // bf16 outputs leave through LDS in row order (gemm_bf16_epilogue_staged):
+    // their MFMAs take the B tile first
+    constexpr bool ROWS = std::is_same<TC, bf16>::value;
     constexpr int BM = GBD_BM, BN = GBD_BN, BK = GBD_BK, STAGES = GBD_STAGES, W = GBD_THREADS / 64;
     constexpr int A_BYTES = BM * BK * 2, STAGE_BYTES = A_BYTES + BN * BK * 2;
     constexpr int NA = BM / 16 / W, NB = BN / 16 / W;  // load instructions per wave per chunk
@@ -373,13 +457,22 @@ __device__ __forceinline__ void gemm_bf16_dma_body(const GemmDescBF16 &d, int ti
             for (int i = 0; i < 2; i++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = ROWS ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a[i], acc[i][j], 0, 0, 0)
+                                     : __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         if (kt + 2 < nk) wait_vmcnt<NA + NB>();  // chunk kt+1 has landed; kt+2 may still fly
         else wait_vmcnt<0>();
         __syncthreads();
     }
-    gemm_bf16_epilogue<EPI, TC, 2, 2>(d, acc, m0 + wm * 64, n0 + wn * 64, li, lh);
+    if constexpr (ROWS) {
+        // the ring is free: every wave finished its reads before the last
+        // barrier and no load is in flight; wave w stages in its own ninth
+        static_assert(GBD_THREADS / 64 * 64 * (64 + 8) * 2 <= STAGES * STAGE_BYTES, "staging fits the ring");
+        gemm_bf16_epilogue_staged<EPI>(d, acc, reinterpret_cast<bf16 *>(ring) + wave * 64 * (64 + 8), m0 + wm * 64,
+                                       n0 + wn * 64, lane);
+    } else {
+        gemm_bf16_epilogue<EPI, TC, 2, 2>(d, acc, m0 + wm * 64, n0 + wn * 64, li, lh);
+    }
 }
 
 template <int EPI, typename TC>
