@@ -37,9 +37,12 @@ struct GemmBatchBF16 {
     GemmDescBF16 d[GB_MAX_BATCH];
 };
 
+// One output element; fp32 outputs are written non-temporally (no kernel
+// reads them back, and they would only displace the operands' lines in L2:
+// -1.5 to -3% on the fp16 two-piece GEMMs).
 template <typename T>
 VH_DEVICE void store_out(T *p, float v) {
-    if constexpr (std::is_same<T, float>::value) *p = v;
+    if constexpr (std::is_same<T, float>::value) __builtin_nontemporal_store(v, p);
     else *p = (bf16)v;
 }
 
@@ -96,7 +99,7 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
 #pragma unroll
                         for (int r = 0; r < 16; r++) old[r] = C[(size_t)row_of(i, r) * d.ldc + col];
 #pragma unroll
-                        for (int r = 0; r < 16; r++) C[(size_t)row_of(i, r) * d.ldc + col] = old[r] + value(r);
+                        for (int r = 0; r < 16; r++) store_out(C + (size_t)row_of(i, r) * d.ldc + col, old[r] + value(r));
                     } else {
 #pragma unroll
                         for (int r = 0; r < 16; r++) store_out(C + (size_t)row_of(i, r) * d.ldc + col, value(r));
@@ -107,8 +110,7 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
                         const int row = row_of(i, r);
                         if (row >= d.M) continue;
                         TC *p = C + (size_t)row * d.ldc + col;
-                        if constexpr (EPI == EPI_RESIDUAL) *p = *p + value(r);
-                        else store_out(p, value(r));
+                        store_out(p, EPI == EPI_RESIDUAL ? *p + value(r) : value(r));
                     }
                 }
             }
