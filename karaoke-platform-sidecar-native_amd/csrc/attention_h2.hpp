@@ -288,6 +288,18 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
             }
             store(st, kb + 2, kb + 1, true);
             load(st, kb + 3, kb + 2);
+            if constexpr (ACTIVE) {
+                // interleave the iteration's 24 MFMAs with its VALU work (block
+                // kb's exponentials and splits, the staging's rotation and
+                // splits): five VALU instructions after each MFMA, so the wave
+                // issues them while the matrix core runs instead of after a
+                // burst of MFMAs (-2.2%; four: -0.5%, six spills)
+#pragma unroll
+                for (int i = 0; i < 24; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
+                }
+            }
             __syncthreads();
             if constexpr (ACTIVE) {
                 if (kb + 1 < nkb) soft_max(sn, kb + 1);
