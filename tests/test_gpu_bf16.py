@@ -167,6 +167,8 @@ DMA_CASES = [
     (77, 384, 1536, 2, False),
     (4097, 768, 384, 0, True),
     (1, 8, 32, 0, False),
+    (300, 200, 96, 2, True),   # bf16 output leaving through LDS: tanh, ragged last 8-column store
+    (70, 5, 32, 0, True),      # fewer columns than one 16-byte store
 ]
 
 
