@@ -120,6 +120,19 @@ int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, 
 #define VH_H2_A_ROWS 1 /* flags of vh_gemm_h2: A given as h2 rows (vh_rmsnorm_h2), scaled from a_bound */
 int vh_gemm_h2(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, float a_bound, const void *Wp,
                const float *bias, float *C, int ldc, int epilogue, int flags);
+/* vh_gemm_h2 as the fused transformer block runs it: the bound is the device
+   float a_bound_dev; with VH_H2_ROW_NORM (fp32 A, epilogue VH_EPI_STORE, GELU
+   or GELU_GLU, K the row length) the GEMM of an RMSNorm of A's rows -- each
+   output row is multiplied by sqrt(K) / sqrt(sum_k A^2 + 1e-12) before bias
+   and activation, Wp holding the norm's gain folded in (the pieces of
+   W[n][k] gamma[k]) -- so the normalised rows are never written; zero_slot
+   (may be null) is set to 0 by the kernel; amax (epilogue VH_EPI_RESIDUAL,
+   may be null) is raised to max |C| over the elements written, the bound of
+   the next row-norm GEMM's A. */
+#define VH_H2_ROW_NORM 2 /* flags of vh_gemm_h2_ex */
+int vh_gemm_h2_ex(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const float *a_bound_dev,
+                  const void *Wp, const float *bias, float *C, int ldc, int epilogue, int flags, float *zero_slot,
+                  float *amax);
 /* Bytes of the fp16 pieces of an N x K weight: a 256-byte header, then two
    planes (N rounded up to 128 rows). */
 size_t vh_h2_bytes(int N, int K);

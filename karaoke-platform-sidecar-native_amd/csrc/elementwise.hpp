@@ -244,6 +244,17 @@ static __global__ __launch_bounds__(256) void interleave_glu_bias_kernel(const f
     dst[(c / 32) * 64 + 32 * g + (c % 32)] = src[o];
 }
 
+// W [N][ldw] with column k multiplied by g[k] -> out [N][K]: an RMSNorm's gain
+// folded into the matrix that consumes its output (gemm_h2 row_norm).
+static __global__ __launch_bounds__(256) void scale_columns_kernel(const float *__restrict__ W, int N, int K, int ldw,
+                                                                  const float *__restrict__ g,
+                                                                  float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)N * K) return;
+    const int n = (int)(i / K), k = (int)(i % K);
+    out[i] = W[(size_t)n * ldw + k] * g[k];
+}
+
 // ------------------------------------------------- token-row transposes
 // [outer][a][b][D] -> [outer][b][a][D]: whole D-float rows move, so reads and
 // writes are both contiguous 16-byte streams.

@@ -51,10 +51,11 @@ VH_DEVICE void store_out(T *p, float v) {
 // lh), register r holds row 8*(r/4) + 4*lh + r%4, column li.  Tiles whose
 // rows all lie inside M (all but the last row of tiles) take a path without
 // per-element row checks, so the residual epilogue issues its 16 loads of C
-// together instead of one load-wait-store per element.
+// together instead of one load-wait-store per element.  mx_out (residual
+// epilogue only; null for none): raised to the largest |C| this lane wrote.
 template <int EPI, typename TC, int FM, int FN>
 VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[FM][FN], int row0, int col0, int li,
-                                  int lh) {
+                                  int lh, float *mx_out = nullptr) {
     TC *C = static_cast<TC *>(d.C);
     const bool rows_full = row0 + 32 * FM <= d.M;
     auto row_of = [&](int i, int r) { return row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3); };
@@ -80,6 +81,7 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
         }
     } else {
         static_assert(EPI != EPI_RESIDUAL || std::is_same<TC, float>::value, "residual output is fp32");
+        float mx = 0.0f;  // largest |C| written (residual epilogue)
 #pragma unroll
         for (int j = 0; j < FN; j++) {
             const int col = col0 + j * 32 + li;
@@ -99,7 +101,11 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
 #pragma unroll
                         for (int r = 0; r < 16; r++) old[r] = C[(size_t)row_of(i, r) * d.ldc + col];
 #pragma unroll
-                        for (int r = 0; r < 16; r++) store_out(C + (size_t)row_of(i, r) * d.ldc + col, old[r] + value(r));
+                        for (int r = 0; r < 16; r++) {
+                            const float v = old[r] + value(r);
+                            mx = fmaxf(mx, fabsf(v));
+                            store_out(C + (size_t)row_of(i, r) * d.ldc + col, v);
+                        }
                     } else {
 #pragma unroll
                         for (int r = 0; r < 16; r++) store_out(C + (size_t)row_of(i, r) * d.ldc + col, value(r));
@@ -110,10 +116,15 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
                         const int row = row_of(i, r);
                         if (row >= d.M) continue;
                         TC *p = C + (size_t)row * d.ldc + col;
-                        store_out(p, EPI == EPI_RESIDUAL ? *p + value(r) : value(r));
+                        const float v = EPI == EPI_RESIDUAL ? *p + value(r) : value(r);
+                        if constexpr (EPI == EPI_RESIDUAL) mx = fmaxf(mx, fabsf(v));
+                        store_out(p, v);
                     }
                 }
             }
+        }
+        if constexpr (EPI == EPI_RESIDUAL) {
+            if (mx_out) *mx_out = fmaxf(*mx_out, mx);
         }
     }
 }

@@ -54,6 +54,11 @@ struct GemmDescH2 {
     float *C;
     int M, N, K;
     int lda, ldc;
+    // Null for none.  zero_slot: a device float the kernel sets to 0 (the bound
+    // slot a later residual GEMM raises); amax: raised to max |C| by the
+    // residual epilogue (gemm_bf16_epilogue).
+    float *zero_slot;
+    float *amax;
 };
 // Bound on |A|: *ptr when ptr is set (a device float), else value.
 struct H2Bound {
@@ -67,8 +72,16 @@ constexpr int H2_WBLOCK = 2 * GS_BN * GS_BK;  // fp16 per (row tile, K chunk) bl
 // A_H2: A arrives as h2 rows (h2.hpp) scaled by 2^h2_exponent(a_bound) -- its
 // producer split it -- and the K loop only reads the pieces.
 // RING: K chunks held in LDS, RING - 1 of them in flight while one is multiplied.
-template <int EPI, bool A_H2, int RING = 3>
+// NORM (fp32 A): the GEMM of an RMSNorm of A's rows, W holding the norm's gain
+// folded in (W[n][k] gamma[k]): each accumulator row is multiplied by its row's
+// sqrt(K) / sqrt(sum_k A^2 + 1e-12) (the RMSNorm kernels' expression), the
+// sum taken from the fp32 values the K loop splits anyway, before bias and
+// activation.  So the normalised rows are never written: the RMSNorm pass and
+// its 2 x 4 bytes per element of traffic go, and A is the residual stream
+// itself, bounded by the max |x| its producer's epilogue recorded.
+template <int EPI, bool A_H2, int RING = 3, bool NORM = false>
 __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound, int tile) {
+    static_assert(!(NORM && A_H2), "the row norm needs the fp32 rows");
     constexpr int A_BYTES = GS_BM * GS_BK * 4;  // 16 KB: fp32 rows of 64 B
     constexpr int P_BYTES = GS_BN * GS_BK * 2;  // 4 KB per W plane: fp16 rows of 32 B
     constexpr int STAGE_BYTES = A_BYTES + 2 * P_BYTES;
@@ -76,6 +89,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
 
     const int tiles_n = (d.N + GS_BN - 1) / GS_BN;
     const int tiles_m = (d.M + GS_BM - 1) / GS_BM;
+    if (d.zero_slot && tile == 0 && threadIdx.x == 0) *d.zero_slot = 0.0f;
     if (tile >= tiles_m * tiles_n) return;
     // column-fastest order within groups of row tiles (see gemm.hpp)
     // groups of 4 row tiles for the wide GEMMs (measured against 1, 2, 8, 16:
@@ -127,6 +141,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
         for (int r = 0; r < 16; r++) acc[0][j][r] = 0.0f;
 
     const int nk = d.K / GS_BK;
+    float ss = 0.0f;  // NORM: sum of squares of this lane's half of row wave*32 + li
 #pragma unroll
     for (int i = 0; i < RING - 1; i++)
         if (i < nk) issue(i);
@@ -156,6 +171,10 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
                 const floatx4 lo = *reinterpret_cast<const floatx4 *>(ar + 16 * (lh ^ swz_a(r)));
                 const floatx4 hi = *reinterpret_cast<const floatx4 *>(ar + 16 * ((2 + lh) ^ swz_a(r)));
                 split8_h2(lo, hi, a_scale, ah, am);
+                if constexpr (NORM) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) ss = fmaf(hi[e], hi[e], fmaf(lo[e], lo[e], ss));
+                }
             }
             // W column tiles two at a time: their pieces, then (m,h) (h,m) (h,h)
 #pragma unroll
@@ -195,14 +214,47 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     else k_loop(std::integral_constant<int, 1>());
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[0][j] = (acc[0][j] * a_unscale) * w_unscale;  // exact: powers of two
+    if constexpr (NORM) {
+        // lanes li and li + 32 summed the two halves of row wave*32 + li;
+        // register 4q + e of a lane holds row 8q + 4lh + e of the wave's 32
+        __shared__ float rscale[GS_THREADS / 64][32];
+        const float tot = ss + __shfl_xor(ss, 32, 64);
+        if (lh == 0) rscale[wave][li] = sqrtf((float)d.K) / sqrtf(tot + 1.0e-12f);
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const floatx4 r4 = *reinterpret_cast<const floatx4 *>(&rscale[wave][8 * q + 4 * lh]);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[0][j][4 * q + e] *= r4[e];
+        }
+    }
     GemmDescBF16 e{};
     e.bias = d.bias; e.C = d.C; e.M = d.M; e.N = d.N; e.K = d.K; e.ldc = d.ldc;
-    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh);
+    float mx = 0.0f;
+    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh, &mx);
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (d.amax) {
+            // one atomic per workgroup (one per wave, all on one address,
+            // cost 17 us per launch of 4656 tiles); non-negative floats
+            // order as their bit patterns
+            __shared__ float wmax[GS_THREADS / 64];
+            mx = wave_max(mx);
+            if (lane == 0) wmax[wave] = mx;
+            __syncthreads();
+            if (tid == 0) {
+#pragma unroll
+                for (int w = 1; w < GS_THREADS / 64; w++) mx = fmaxf(mx, wmax[w]);
+                atomicMax(reinterpret_cast<unsigned int *>(d.amax), __float_as_uint(mx));
+            }
+        }
+    }
 }
 
-template <int EPI, bool A_H2>
+template <int EPI, bool A_H2, bool NORM = false>
 __global__ __launch_bounds__(GS_THREADS, 2) void gemm_h2_kernel(GemmDescH2 d, H2Bound b) {
-    gemm_h2_body<EPI, A_H2>(d, b.ptr ? *b.ptr : b.value, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+    gemm_h2_body<EPI, A_H2, 3, NORM>(d, b.ptr ? *b.ptr : b.value, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
 // Ragged batch (the mask estimator's per-band linears): problem blockIdx.z,

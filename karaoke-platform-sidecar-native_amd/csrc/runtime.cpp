@@ -419,6 +419,9 @@ static bool gemm_h2_ok(const GemmArgsH2 &g, int epilogue) {
     if (g.K % GS_BK || g.lda % 4 || g.lda < g.K || g.lda > (1 << 21)) return false;  // lane load offsets are 32-bit
     if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return false;
+    if (g.row_norm && (g.a_h2 || !(epilogue == EPI_STORE || epilogue == EPI_GELU || epilogue == EPI_GEGLU)))
+        return false;
+    if (g.amax && epilogue != EPI_RESIDUAL) return false;
     return true;
 }
 
@@ -427,19 +430,27 @@ static GemmDescH2 to_desc_h2(const GemmArgsH2 &g) {
     d.A = g.A; d.W = g.W; d.bias = g.bias; d.C = g.C;
     d.M = (int)g.M; d.N = g.N; d.K = g.K;
     d.lda = g.lda; d.ldc = g.ldc;
+    d.zero_slot = g.zero_slot; d.amax = g.amax;
     return d;
 }
 
 template <int EPI>
-static void launch_h2(hipStream_t s, const GemmDescH2 &d, const H2Bound &b, unsigned tiles, bool a_h2) {
-    if (a_h2) hipLaunchKernelGGL((gemm_h2_kernel<EPI, true>), dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
+static void launch_h2(hipStream_t s, const GemmDescH2 &d, const H2Bound &b, unsigned tiles, const GemmArgsH2 &g) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_GELU || EPI == EPI_GEGLU) {
+        if (g.row_norm) {  // gemm_h2_ok: fp32 A
+            hipLaunchKernelGGL((gemm_h2_kernel<EPI, false, true>), dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
+            return;
+        }
+    }
+    if (g.a_h2) hipLaunchKernelGGL((gemm_h2_kernel<EPI, true>), dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
     else hipLaunchKernelGGL((gemm_h2_kernel<EPI, false>), dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
 }
 
 bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int epilogue, KernelTimer *t,
              const char *name) {
     if (!gemm_h2_ok(g, epilogue)) {
-        set_error("gemm_h2: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K, g.lda);
+        set_error("gemm_h2: unsupported shape or mode M=%lld N=%d K=%d lda=%d epilogue %d%s%s", (long long)g.M, g.N,
+                  g.K, g.lda, epilogue, g.row_norm ? " row norm" : "", g.amax ? " amax" : "");
         return false;
     }
     const GemmDescH2 d = to_desc_h2(g);
@@ -447,11 +458,11 @@ bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int 
     const unsigned tiles = (unsigned)(((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
     Scope sc(t, s, name);
     switch (epilogue) {
-        case EPI_STORE: launch_h2<EPI_STORE>(s, d, b, tiles, g.a_h2); break;
-        case EPI_GELU: launch_h2<EPI_GELU>(s, d, b, tiles, g.a_h2); break;
-        case EPI_TANH: launch_h2<EPI_TANH>(s, d, b, tiles, g.a_h2); break;
-        case EPI_RESIDUAL: launch_h2<EPI_RESIDUAL>(s, d, b, tiles, g.a_h2); break;
-        case EPI_GEGLU: launch_h2<EPI_GEGLU>(s, d, b, tiles, g.a_h2); break;
+        case EPI_STORE: launch_h2<EPI_STORE>(s, d, b, tiles, g); break;
+        case EPI_GELU: launch_h2<EPI_GELU>(s, d, b, tiles, g); break;
+        case EPI_TANH: launch_h2<EPI_TANH>(s, d, b, tiles, g); break;
+        case EPI_RESIDUAL: launch_h2<EPI_RESIDUAL>(s, d, b, tiles, g); break;
+        case EPI_GEGLU: launch_h2<EPI_GEGLU>(s, d, b, tiles, g); break;
         default: set_error("unknown GEMM epilogue %d", epilogue); return false;
     }
     return sync_debug(s, "gemm_h2_kernel");
@@ -656,6 +667,18 @@ bool unpack_weight(hipStream_t s, const float *packed_dev, int in, int out, floa
     return sync_debug(s, "unpack_weight_kernel");
 }
 
+bool fold_gain_split_h2(hipStream_t s, const float *W, int N, int K, int ldw, const float *gamma, float *tmp,
+                        void *pieces) {
+    if (!W || !gamma || !tmp || N <= 0 || K <= 0 || ldw < K) {
+        set_error("fold_gain_split_h2: bad arguments N=%d K=%d ldw=%d", N, K, ldw);
+        return false;
+    }
+    const int64_t n = (int64_t)N * K;
+    hipLaunchKernelGGL(scale_columns_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, W, N, K, ldw, gamma, tmp);
+    if (!sync_debug(s, "scale_columns_kernel")) return false;
+    return split_weights_h2(s, tmp, N, K, K, pieces);
+}
+
 bool interleave_glu_bias(hipStream_t s, const float *src, float *dst, int out) {
     hipLaunchKernelGGL(interleave_glu_bias_kernel, dim3(blocks_for(out, 256)), dim3(256), 0, s, src, dst, out);
     return sync_debug(s, "interleave_glu_bias_kernel");
@@ -846,7 +869,8 @@ bool BlockScratch::ensure(const Dims &d, int64_t tokens) {
 }
 
 bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, float *x, int64_t tokens,
-                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t, int precision) {
+                       const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t, int precision,
+                       XBound *xb) {
     if (!scr.ensure(d, tokens)) return false;
     const float *rt = nullptr;
     if (!rope.get_interleaved(lay.L, d.dim_head, s, &rt)) return false;
@@ -891,9 +915,43 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
         }
         return gemm(s, {A, lda, W, K, bias, C, ldc, tokens, N, K}, epi, t, name);
     };
+    const bool qkv_h2 = use_h2(w.wqkvg_p, D);
+    const bool ff1_h2 = use_h2(w.w1_p, D);
+    const bool att_h2 = precision == PREC_FP32 && w.bounds && w.att_h2;
+    if (xb && xb->dev && xb->scratch && qkv_h2 && ff1_h2 && w.wqkvg_pg && use_h2(w.wout_p, inner) &&
+        use_h2(w.w2_p, d.ff_dim)) {
+        // The attention's pre-norm inside the QKV GEMM (row_norm, the gain in
+        // its pieces), A = x bounded by max |x| in xb->dev: found by an
+        // absmax pass or raised by the previous block's FFN down-projection
+        // epilogue.  The FFN-up GEMM (after the QKV GEMM's last read of the
+        // slot) zeroes it for this block's FFN down-projection to raise.  The
+        // FFN's pre-norm stays a pass of its own: inside the FFN-up GEMM the
+        // split of A, repeated in each of its 24 column tiles, cost more
+        // (+9%) than the pass it saves.
+        if (!xb->valid && !absmax(s, x, tokens * D, xb->scratch, xb->dev)) return false;
+        xb->valid = false;  // until the FFN down-projection has raised the slot
+        GemmArgsH2 gq{x, D, w.wqkvg_pg, w.bqkvg, qkvg, nq, tokens, nq, D};
+        gq.row_norm = true;
+        if (!gemm_h2(s, gq, OperandBound{xb->dev, 0.0f}, EPI_STORE, t, "gemm_qkv")) return false;
+        if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, true,
+                       att_h2 ? w.bounds + 1 : nullptr))
+            return false;
+        if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out"))
+            return false;
+        if (!rmsnorm_h2(s, x, D, w.ff_gamma, normed, D, tokens, D, w.bounds + 2, t)) return false;
+        GemmArgsH2 g1{normed, D, w.w1_p, w.b1, hid, d.ff_dim, tokens, d.ff1_out(), D};
+        g1.a_h2 = true;
+        g1.zero_slot = xb->dev;
+        if (!gemm_h2(s, g1, OperandBound{w.bounds + 2, 0.0f}, ff1_epi, t, "gemm_ff1")) return false;
+        GemmArgsH2 g2{hid, d.ff_dim, w.w2_p, w.b2, x, D, tokens, D, d.ff_dim};
+        g2.amax = xb->dev;
+        if (!gemm_h2(s, g2, OperandBound{w.bounds + 3, 0.0f}, EPI_RESIDUAL, t, "gemm_ff2")) return false;
+        xb->valid = true;
+        return true;
+    }
+    if (xb) xb->valid = false;
     // pre-norm (split into fp16 pieces for the two-piece GEMM) -> fused QKV
     // (+gate logits with their bias)
-    const bool qkv_h2 = use_h2(w.wqkvg_p, D);
     if (!(qkv_h2 ? rmsnorm_h2(s, x, D, w.gamma, normed, D, tokens, D, w.bounds, t)
                  : rmsnorm(s, x, D, w.gamma, normed, D, tokens, D, t)))
         return false;
@@ -901,12 +959,11 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     // rotary + attention + gates (products as fp16 two-piece splits on the
     // default fp32 path)
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32,
-                   precision == PREC_FP32 && w.bounds && w.att_h2 ? w.bounds + 1 : nullptr))
+                   att_h2 ? w.bounds + 1 : nullptr))
         return false;
     // out projection added to the residual stream
     if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;
     // FFN
-    const bool ff1_h2 = use_h2(w.w1_p, D);
     if (!(ff1_h2 ? rmsnorm_h2(s, x, D, w.ff_gamma, normed, D, tokens, D, w.bounds + 2, t)
                  : rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)))
         return false;

@@ -139,6 +139,12 @@ struct GemmArgsH2 {
     float *C; int ldc;
     int64_t M; int N, K;
     bool a_h2 = false;  // A given as h2 rows (h2.hpp) scaled from the same bound
+    // fp32 A rows RMSNorm-ed inside the GEMM, W holding the gain (gemm_h2_body
+    // NORM): each output row times sqrt(K) / sqrt(sum_k A^2 + 1e-12) before
+    // bias and activation (EPI_STORE, EPI_GELU, EPI_GEGLU)
+    bool row_norm = false;
+    float *zero_slot = nullptr;  // a device float the kernel sets to 0
+    float *amax = nullptr;       // EPI_RESIDUAL: raised to max |C| written
 };
 struct OperandBound {
     const float *dev = nullptr;
@@ -155,6 +161,10 @@ inline size_t h2_bytes(int N, int K) { return 256 + (size_t)(N + 127) / 128 * 12
 // fp32 W [N][ldw] -> max|W| and the h, m fp16 pieces of W * 2^e
 // (h2_bytes(N, K) bytes, 256-byte aligned).
 bool split_weights_h2(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces);
+// The same for W with column k multiplied by gamma[k] (an RMSNorm gain folded
+// into the matrix after it, for gemm_h2 row_norm); tmp: N*K device floats.
+bool fold_gain_split_h2(hipStream_t s, const float *W, int N, int K, int ldw, const float *gamma, float *tmp,
+                        void *pieces);
 // Device bounds for the fp16 two-piece GEMM's A operands downstream of an
 // RMSNorm with gain gamma[D] (operand_bounds_kernel in gemm_h2.hpp):
 // out[0] bounds the normalised activations, out[1] (when W [N][D] is given)
@@ -234,6 +244,10 @@ struct LayerWeights {
     // matrix cores, and the device bounds of their A operands {QKV, out,
     // FFN up, FFN down} (layer_bounds); null: the fp32 MFMA GEMM runs instead
     void *wqkvg_p = nullptr, *wout_p = nullptr, *w1_p = nullptr, *w2_p = nullptr;
+    // the same pieces of the QKV matrix with its RMSNorm gain folded in
+    // (fold_gain_split_h2), for blocks whose attention pre-norm runs inside
+    // that GEMM (XBound); null: the RMSNorm kernel runs
+    void *wqkvg_pg = nullptr;
     float *bounds = nullptr;
     // the fused projection's bound (bounds[1], which also bounds q, k and v)
     // lies in the fp16 two-piece attention's range (h2_attention_bound_ok);
@@ -289,9 +303,23 @@ struct BlockScratch {
 // One axial transformer block on device-resident activations x
 // (native/vocalarc_separation.c:836-873).  Rows of x are tokens; `lay` maps
 // (sequence, position) to rows.
+// Bound slot of the residual stream x for blocks whose attention pre-norm runs
+// inside the QKV GEMM (gemm_h2 row_norm; its fp32 A is x itself, split by the
+// bound of |x|): *dev bounds x entering a block -- raised by the previous
+// block's FFN-down epilogue, which `valid` records, else found by an absmax
+// pass.  scratch: ABSMAX_PARTIALS device floats.
+struct XBound {
+    float *dev = nullptr;
+    float *scratch = nullptr;
+    bool valid = false;
+};
+// One pre-norm transformer block on x in place.  With xb (and the gain-folded
+// QKV pieces in w, every linear on the fp16 pieces) the attention's pre-norm
+// is fused into the QKV GEMM; otherwise the RMSNorm kernel writes the
+// normalised rows for both.
 bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, float *x, int64_t tokens,
                        const AttnLayout &lay, BlockScratch &scr, RopeCache &rope, KernelTimer *t = nullptr,
-                       int precision = PREC_FP32);
+                       int precision = PREC_FP32, XBound *xb = nullptr);
 
 // Host packed weight (reference layout) -> device [out][in] rows, through a
 // staging buffer.  mode as unpack_weight.

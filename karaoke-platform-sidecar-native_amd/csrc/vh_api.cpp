@@ -37,7 +37,9 @@ struct vh_context {
     RopeCache rope;
     BlockScratch scratch;
     DeviceBuffer staging;
-    DeviceBuffer bounds;  // vh_gemm_h2's computed A bound and its absmax scratch
+    // vh_gemm_h2's computed A bound (float 0), vh_transformer's stream bound
+    // (float 8) and the absmax scratch (from float 64)
+    DeviceBuffer bounds;
 };
 
 struct vh_model {
@@ -241,6 +243,20 @@ extern "C" int vh_gemm_h2(vh_context *ctx, int64_t M, int N, int K, const float 
         b.dev = ctx->bounds.f();
     }
     return gemm_h2(ctx->stream, g, b, epilogue, &ctx->timer, "gemm_h2") ? 1 : 0;
+}
+
+extern "C" int vh_gemm_h2_ex(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda,
+                             const float *a_bound_dev, const void *Wp, const float *bias, float *C, int ldc,
+                             int epilogue, int flags, float *zero_slot, float *amax) {
+    if (!ctx || !a_bound_dev || (flags & ~VH_H2_ROW_NORM)) {
+        set_error("vh_gemm_h2_ex: null context or bound, or unknown flags %d", flags);
+        return 0;
+    }
+    GemmArgsH2 g{A, lda, Wp, bias, C, ldc, M, N, K};
+    g.row_norm = (flags & VH_H2_ROW_NORM) != 0;
+    g.zero_slot = zero_slot;
+    g.amax = amax;
+    return gemm_h2(ctx->stream, g, OperandBound{a_bound_dev, 0.0f}, epilogue, &ctx->timer, "gemm_h2") ? 1 : 0;
 }
 
 extern "C" size_t vh_h2_bytes(int N, int K) { return N > 0 && K > 0 ? h2_bytes(N, K) : 0; }
@@ -565,6 +581,8 @@ bool prepare_bf16(vh_model *m) {
 // the bounds of their A operands.
 static float *mask_feature_bound(vh_model *m) { return m->bounds.f() + 4 * m->layers.size(); }
 static float *absmax_scratch(vh_model *m) { return m->bounds.f() + 4 * m->layers.size() + 64; }
+// the residual stream's bound slot (XBound) of the layer stack
+static float *stream_bound(vh_model *m) { return m->bounds.f() + 4 * m->layers.size() + 8; }
 
 bool prepare_split(vh_model *m) {
     if (m->weights_s.ptr) return true;
@@ -572,7 +590,10 @@ bool prepare_split(vh_model *m) {
     hipStream_t s = m->ctx->stream;
     const int D = d.dim, Hm = d.mask_hidden;
     auto bytes = [](int N, int K) { return K % SPLIT_K_MULTIPLE ? 0 : (h2_bytes(N, K) + 255) & ~(size_t)255; };
-    const size_t per_layer = bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) + bytes(D, d.ff_dim);
+    // per layer: the four matrices, and the QKV one again with its RMSNorm
+    // gain folded in (the attention's pre-norm fused into the QKV GEMM)
+    const size_t per_layer =
+        2 * bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) + bytes(D, d.ff_dim);
     size_t total = per_layer * m->layers.size();
     for (int b = 0; b < d.bands; b++) total += bytes(Hm, D) + bytes(2 * d.in_dim(b), Hm);
     m->mask_w1_s.assign(d.bands, nullptr);
@@ -591,6 +612,14 @@ bool prepare_split(vh_model *m) {
         cur += bytes(N, K);
         return split_weights_h2(s, src, N, K, K, *dst);
     };
+    DeviceBuffer fold_tmp;  // a gain-folded fp32 matrix on its way to its pieces
+    auto split_folded = [&](const float *src, int N, const float *gamma, void **dst) {
+        if (D % SPLIT_K_MULTIPLE) return true;
+        if (!fold_tmp.ensure((size_t)N * D * sizeof(float), "hipMalloc(folded weight)")) return false;
+        *dst = cur;
+        cur += bytes(N, D);
+        return fold_gain_split_h2(s, src, N, D, D, gamma, fold_tmp.f(), *dst);
+    };
     for (size_t i = 0; i < m->layers.size(); i++) {
         LayerWeights &w = m->layers[i];
         if (!split(w.wqkvg, d.qkvg_dim(), D, &w.wqkvg_p) || !split(w.wout, D, d.inner(), &w.wout_p) ||
@@ -603,6 +632,7 @@ bool prepare_split(vh_model *m) {
         if (ok < 0) return false;
         if (ok == 0) w.bounds = nullptr;  // weights beyond the scale range: this layer's linears on fp32 MFMA
         w.att_h2 = w.bounds && h2_attention_bound_ok(hb[1]);
+        if (w.bounds && !split_folded(w.wqkvg, d.qkvg_dim(), w.gamma, &w.wqkvg_pg)) return false;
     }
     for (int b = 0; b < d.bands && mask_ok; b++)  // no pieces: the mask estimator stays on fp32 MFMA
         if (!split(m->mask_w1[b], Hm, D, &m->mask_w1_s[b]) || !split(m->mask_w2[b], 2 * d.in_dim(b), Hm, &m->mask_w2_s[b]))
@@ -793,12 +823,17 @@ bool stage_stack(vh_model *m, float *x, int chunks, int T) {
     const Dims &d = m->d;
     const int64_t tokens = (int64_t)chunks * T * d.bands;
     vh_context *ctx = m->ctx;
+    // attention pre-norms fused into the QKV GEMMs: the stream's bound is
+    // found once, then carried from block to block by the FFN-down epilogues
+    XBound xb;
+    xb.dev = stream_bound(m);
+    xb.scratch = absmax_scratch(m);
     for (int l = 0; l < d.depth; l++) {
         if (!transformer_block(ctx->stream, d, m->layers[2 * l], x, tokens, time_axis_layout(chunks, T, d.bands),
-                               ctx->scratch, ctx->rope, &ctx->timer, m->precision))
+                               ctx->scratch, ctx->rope, &ctx->timer, m->precision, &xb))
             return false;
         if (!transformer_block(ctx->stream, d, m->layers[2 * l + 1], x, tokens, band_axis_layout(chunks, T, d.bands),
-                               ctx->scratch, ctx->rope, &ctx->timer, m->precision))
+                               ctx->scratch, ctx->rope, &ctx->timer, m->precision, &xb))
             return false;
     }
     return true;
@@ -876,8 +911,14 @@ extern "C" void vh_model_free(vh_model *m) {
 
 extern "C" int vh_transformer(vh_context *ctx, vh_model *m, int layer, int axis, float *x, int S, int L) {
     if (!ctx || !m || layer < 0 || layer >= m->d.depth || axis < 0 || axis > 1 || S <= 0 || L <= 0) return 0;
+    // the attention's pre-norm fused into the QKV GEMM as in the layer stack,
+    // the stream's bound found by an absmax pass (float 8 of the context's bounds)
+    if (!ctx->bounds.ensure((64 + ABSMAX_PARTIALS) * sizeof(float), "hipMalloc(operand bounds)")) return 0;
+    XBound xb;
+    xb.dev = ctx->bounds.f() + 8;
+    xb.scratch = ctx->bounds.f() + 64;
     return transformer_block(ctx->stream, m->d, m->layers[2 * layer + axis], x, (int64_t)S * L, contiguous_layout(S, L),
-                             ctx->scratch, ctx->rope, &ctx->timer, m->precision)
+                             ctx->scratch, ctx->rope, &ctx->timer, m->precision, &xb)
                ? 1
                : 0;
 }

@@ -211,8 +211,11 @@ def main() -> int:
 
     if "h2" in groups or "ff1" in groups:
         # the same four GEMMs as the default fp32 path runs them: fp16 two-piece
-        # splits (three products); QKV and FFN up read A as RMSNorm h2 rows,
-        # the others split fp32 A bounded by its maximum
+        # splits (three products); QKV takes the residual stream itself with
+        # its pre-norm inside the GEMM (row norm, the gain folded into the
+        # weight's pieces, bound max|x|), FFN up reads A as RMSNorm h2 rows,
+        # the others split fp32 A bounded by its maximum, FFN down also
+        # raising the stream's bound for the next QKV GEMM
         M = 8 * 801 * 62
         shapes = (("gemm_h2_qkv_gates", 384, 1568, native.EPI_STORE, 1568),
                   ("gemm_h2_out_residual", 512, 384, native.EPI_RESIDUAL, 384),
@@ -224,22 +227,30 @@ def main() -> int:
             a = torch.randn(M, K, device=dev, generator=g)
             w = 0.05 * torch.randn(N, K, device=dev, generator=g)
             wp = torch.empty(ctx.h2_bytes(N, K) // 2, dtype=torch.float16, device=dev)
-            ctx.split_weights_h2(w, wp, N, K)
+            gamma = 1.0 + 0.02 * torch.randn(K, device=dev, generator=g)
             b = torch.randn(N, device=dev, generator=g)
             c = torch.zeros(M, ocols, device=dev)
-            rows = K == 384  # QKV and FFN up take their A as RMSNorm h2 rows, as in the model
-            if rows:
-                gamma = 1.0 + 0.02 * torch.randn(K, device=dev, generator=g)
+            dbound = a.abs().max().reshape(1)
+            if name == "gemm_h2_qkv_gates":
+                ctx.split_weights_h2((w * gamma).contiguous(), wp, N, K)
+                call = lambda: ctx.gemm_h2_ex(a, wp, c, M, N, K, dbound, bias=b, epilogue=epi, row_norm=True)
+            elif name == "gemm_h2_ff1_geglu":
+                ctx.split_weights_h2(w, wp, N, K)
                 bnd = torch.zeros(2, device=dev)
                 ctx.operand_bounds(gamma, K, bnd)
                 ah = torch.empty_like(a)
                 ctx.rmsnorm_h2(a, gamma, bnd, ah, M, K)
                 bound = float(bnd[0])
-                a = ah
+                call = lambda: ctx.gemm_h2(ah, wp, c, M, N, K, bias=b, epilogue=epi, a_bound=bound, a_rows=True)
+            elif name == "gemm_h2_ff2_residual":
+                ctx.split_weights_h2(w, wp, N, K)
+                amax = torch.zeros(1, device=dev)
+                call = lambda: ctx.gemm_h2_ex(a, wp, c, M, N, K, dbound, bias=b, epilogue=epi, amax=amax)
             else:
-                bound = float(a.abs().max())
+                ctx.split_weights_h2(w, wp, N, K)
+                call = lambda: ctx.gemm_h2_ex(a, wp, c, M, N, K, dbound, bias=b, epilogue=epi)
             r = max(3, reps // 4)
-            t = _event_time(lambda: ctx.gemm_h2(a, wp, c, M, N, K, bias=b, epilogue=epi, a_bound=bound, a_rows=rows), r)
+            t = _event_time(call, r)
             _emit(name, t, gflop=2.0 * M * K * N / 1e9, shape=f"M={M} K={K} N={N}", peak_tflops=FP16_TFLOPS,
                   mc_products=3, device=r"gemm_h2_kernel", reps=r)
             del a, w, wp, b, c

@@ -48,6 +48,7 @@ SIGNATURES = {
     "vh_split_bytes": (ctypes.c_size_t, [_I, _I]),
     "vh_split_weights": (_I, [_P, _I, _I, _P, _I, _P]),
     "vh_gemm_h2": (_I, [_P, _I64, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _I, _I, _I]),
+    "vh_gemm_h2_ex": (_I, [_P, _I64, _I, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "vh_h2_bytes": (ctypes.c_size_t, [_I, _I]),
     "vh_split_weights_h2": (_I, [_P, _I, _I, _P, _I, _P]),
     "vh_operand_bounds": (_I, [_P, _P, _I, _P, _I, _P, _I, _P]),
@@ -237,6 +238,16 @@ class Context:
                              _opt(bias), ptr(C),
                              ldc or _out_cols(N, epilogue), epilogue, 1 if a_rows else 0),
             "vh_gemm_h2")
+
+    def gemm_h2_ex(self, A, Wp, C, M: int, N: int, K: int, a_bound, bias=None, epilogue: int = EPI_STORE,
+                   lda: int | None = None, ldc: int | None = None, row_norm: bool = False, zero_slot=None,
+                   amax=None):
+        """gemm_h2 with a device bound a_bound; row_norm: C = op(rms(A) (A Wp^T) + bias) with the RMSNorm gain folded
+        into Wp; zero_slot set to 0; amax (residual epilogue) raised to max|C| (see vh_gemm_h2_ex)."""
+        _ok(lib().vh_gemm_h2_ex(self.h, M, N, K, ptr(A), lda or K, ptr(a_bound), ptr(Wp), _opt(bias), ptr(C),
+                                ldc or _out_cols(N, epilogue), epilogue, 2 if row_norm else 0, _opt(zero_slot),
+                                _opt(amax)),
+            "vh_gemm_h2_ex")
 
     def operand_bounds(self, gamma, D: int, out, W=None, N: int = 0, bias=None, square: bool = False):
         """Device bounds out[0..1] of the A operands after an RMSNorm with gain gamma (see vh_operand_bounds)."""

@@ -196,6 +196,112 @@ def test_gemm_h2_geglu(ctx, rng):
     assert err.max() <= 2e-5, err.max()
 
 
+def _geglu_perm(F: int) -> np.ndarray:
+    """Row order of a GELU-GLU weight in the library: 32 value rows, then their 32 gate rows."""
+    perm = np.empty(2 * F, dtype=np.int64)
+    for c in range(F):
+        perm[(c // 32) * 64 + (c % 32)] = c
+        perm[(c // 32) * 64 + 32 + (c % 32)] = F + c
+    return perm
+
+
+@pytest.mark.parametrize("epi", ["store", "geglu", "gelu"])
+def test_gemm_h2_row_norm(ctx, rng, epi):
+    """The GEMM of an RMSNorm of x's rows (VH_H2_ROW_NORM): x raw, the gain
+    folded into the weight's pieces, each output row scaled by
+    sqrt(D) / sqrt(sum x^2 + 1e-12) inside the GEMM.  Against a float64
+    RMSNorm and linear of the same fp32 inputs, with the bound max|x| (what
+    the model passes), its error is as small as that of the unfused pair
+    (fp32 RMSNorm kernel, then the two-piece GEMM) and within 2^-18
+    sum|y||w|; a dropped or misplaced row scale would be off by the rows'
+    norms (the rows' scales span e^+-3).  With a bound 2^10 times looser the
+    pieces of x are exact only to 2^-25 / 2^e absolute (e from the bound), so
+    a row's error grows with its scale factor: held to that analytic bound.
+    Rows are ragged against the 256-row tile."""
+    rows, D = 1000, 384
+    N = {"store": 1568, "geglu": 2 * 192, "gelu": 256}[epi]
+    code = {"store": native.EPI_STORE, "geglu": native.EPI_GEGLU, "gelu": native.EPI_GELU}[epi]
+    x = (rng.standard_normal((rows, D)) * np.exp(rng.standard_normal((rows, 1)))).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    w = (0.05 * rng.standard_normal((N, D))).astype(np.float32)
+    b = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    if epi == "geglu":
+        perm = _geglu_perm(N // 2)
+        w, b = np.ascontiguousarray(w[perm]), np.ascontiguousarray(b[perm])
+    x64 = x.astype(np.float64)
+    y64 = x64 * (np.sqrt(D) / np.sqrt(np.sum(x64 * x64, axis=1, keepdims=True) + 1e-12)) * gamma
+    pre = y64 @ w.astype(np.float64).T + b
+    if epi == "store":
+        ref = pre
+    elif epi == "gelu":
+        ref = O.gelu(pre.astype(np.float32)).astype(np.float64)
+    else:
+        inv = np.argsort(perm)
+        ref = O.geglu(pre[:, inv].astype(np.float32)).astype(np.float64)
+    folded = _pieces(ctx, (w * gamma[None, :]).astype(np.float32))
+    dx, db = to_dev(x), to_dev(b)
+    cols = N // 2 if epi == "geglu" else N
+    amax = float(np.abs(x).max())
+    outs = {}
+    loose = amax * 2.0 ** 10
+    for kind, bound in (("fused", amax), ("fused_loose", loose)):
+        dbound = torch.tensor([bound], dtype=torch.float32, device="cuda:0")
+        zero = torch.tensor([5.0], device="cuda:0")
+        dc = empty_dev((rows, cols))
+        ctx.gemm_h2_ex(dx, folded, dc, rows, N, D, dbound, bias=db, epilogue=code, row_norm=True, zero_slot=zero)
+        torch.cuda.synchronize()
+        assert float(zero.cpu()[0]) == 0.0
+        outs[kind] = from_dev(dc).astype(np.float64)
+    # the unfused pair on the same inputs
+    dy = empty_dev((rows, D))
+    ctx.rmsnorm(dx, to_dev(gamma), dy, rows, D)
+    dc = empty_dev((rows, cols))
+    ctx.gemm_h2(dy, _pieces(ctx, w), dc, rows, N, D, bias=db, epilogue=code)
+    outs["unfused"] = from_dev(dc).astype(np.float64)
+    err = {k: np.abs(o - ref) for k, o in outs.items()}
+    print(f"row norm {epi}: fused max|d| {err['fused'].max():.3e} rms {np.sqrt(np.mean(err['fused'] ** 2)):.3e}"
+          f" | loose {err['fused_loose'].max():.3e} | unfused max|d| {err['unfused'].max():.3e}"
+          f" rms {np.sqrt(np.mean(err['unfused'] ** 2)):.3e}")
+    assert err["fused"].max() <= 1.5 * err["unfused"].max() + 1e-7
+    assert np.sqrt(np.mean(err["fused"] ** 2)) <= 1.25 * np.sqrt(np.mean(err["unfused"] ** 2)) + 1e-8
+    if epi == "store":
+        aw = np.abs(w.astype(np.float64))
+        scale = np.abs(y64) @ aw.T
+        assert np.all(err["fused"] <= 2.0 ** -18 * scale + 2.0 ** -22 * np.abs(ref))
+        # loose bound: each x element carries up to 2^-24 / 2^e absolute more,
+        # times the row's scale factor and |gamma_k w_nk| summed over k
+        r = np.sqrt(D) / np.sqrt(np.sum(x64 * x64, axis=1, keepdims=True) + 1e-12)
+        extra = r * 2.0 ** (-24 - _exponent(loose)) * (np.abs(gamma.astype(np.float64)) @ aw.T)[None, :]
+        assert np.all(err["fused_loose"] <= 2.0 ** -18 * scale + 2.0 ** -22 * np.abs(ref) + extra)
+    # the fp32 bar against the oracle's RMSNorm and linear
+    assert err["fused"].max() <= 2e-5 * max(1.0, float(np.abs(ref).max()))
+
+
+def test_gemm_h2_residual_amax(ctx, rng):
+    """The residual epilogue's amax: raised to exactly max |C| over the
+    elements written (the fp32 values stored), from below and not lowered
+    from above; the bound the next row-norm GEMM splits the residual stream
+    with.  Rows ragged against the tile, N = 384 (three column tiles)."""
+    M, N, K = 1000, 384, 512
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    c0 = (3.0 * rng.standard_normal((M, N))).astype(np.float32)
+    planes = _pieces(ctx, w)
+    dbound = torch.tensor([float(np.abs(x).max())], device="cuda:0")
+    for start in (0.0, 1.0e6):
+        amax = torch.tensor([start], device="cuda:0")
+        dc = to_dev(c0)
+        ctx.gemm_h2_ex(to_dev(x), planes, dc, M, N, K, dbound, epilogue=native.EPI_RESIDUAL, amax=amax)
+        torch.cuda.synchronize()
+        want = max(start, float(dc.abs().max().cpu()))
+        assert float(amax.cpu()[0]) == want, (start, float(amax.cpu()[0]), want)
+    with pytest.raises(native.NativeError):
+        ctx.gemm_h2_ex(to_dev(x), planes, empty_dev((M, N)), M, N, K, dbound, epilogue=native.EPI_STORE, amax=amax)
+    with pytest.raises(native.NativeError):
+        ctx.gemm_h2_ex(to_dev(x), planes, empty_dev((M, N)), M, N, K, dbound, epilogue=native.EPI_RESIDUAL,
+                       row_norm=True)
+
+
 def test_gemm_h2_rejects_bad_shapes(ctx):
     x = torch.zeros(8, 24, device="cuda:0")
     pieces = torch.zeros(ctx.h2_bytes(8, 32) // 2, dtype=torch.float16, device="cuda:0")
