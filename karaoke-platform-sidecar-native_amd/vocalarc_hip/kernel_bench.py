@@ -38,24 +38,38 @@ FP16_TFLOPS = 2500.0
 
 
 def _event_time(fn, reps: int) -> tuple[float, int]:
-    """(mean ms per call, calls made) of `fn` after one untimed call."""
+    """(mean ms per call, calls made) of `fn` after untimed calls (see _event_time_sets)."""
     return _event_time_sets([fn], reps)
+
+
+WARM_MS = 25.0  # untimed work before each record's timed calls
 
 
 def _event_time_sets(fns, reps: int) -> tuple[float, int]:
     """Mean ms per call over `reps` calls cycling through `fns` (one per
-    buffer set), after one untimed call of each; returns (ms, calls made)."""
+    buffer set), after untimed rounds over all of them: one (which also
+    builds per-length tables), then as many as fill WARM_MS -- the clock dips
+    for some 10-20 ms when matrix work resumes after a pause (host-side
+    set-up), and a record of 5 timed 1.5 ms calls would measure the dip.
+    Returns (ms, calls made)."""
     import torch
-    for fn in fns:  # warm-up (also builds per-length tables)
-        fn()
-    torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for fn in fns:
+        fn()
+    b.record()
+    b.synchronize()
+    rounds = 1 + min(200, int(WARM_MS / max(a.elapsed_time(b), 1e-3)))
+    for _ in range(rounds - 1):
+        for fn in fns:
+            fn()
+    torch.cuda.synchronize()
     a.record()
     for i in range(reps):
         fns[i % len(fns)]()
     b.record()
     b.synchronize()
-    return a.elapsed_time(b) / reps, len(fns) + reps
+    return a.elapsed_time(b) / reps, rounds * len(fns) + reps
 
 
 def _sets_for(footprint_bytes: float) -> int:

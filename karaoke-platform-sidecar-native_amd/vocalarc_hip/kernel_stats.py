@@ -36,15 +36,20 @@ from pathlib import Path
 ROLES = [
     (r"gemm_h2_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via two-piece fp16)"),
+    (r"gemm_h2_kernel(<0, false, true>|ILi0ELb0ELb1E)",
+     "fused QKV + gate projection with the attention's pre-norm inside (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via two-piece fp16)"),
     (r"gemm_h2_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32 via two-piece fp16)"),
     (r"gemm_h2_batched_kernel(<|ILi)0", "mask estimator layer 2, batched over bands (fp32 via two-piece fp16)"),
     (r"split_weight_h2_kernel", "weight split into fp16 pieces (model load)"),
-    (r"absmax_kernel", "weight maximum for the fp16 pieces (model load)"),
+    (r"scale_columns_kernel", "RMSNorm gain folded into the QKV weight (model load)"),
+    (r"interleave_glu_bias_kernel", "GELU-GLU bias interleave (model load)"),
+    (r"absmax_kernel", "maxima: of a weight for its fp16 pieces (model load), of the residual stream (once per pass)"),
+    (r"absmax_partial_kernel", "residual stream maximum, partial (once per pass)"),
     (r"operand_bounds_kernel", "operand bounds of the fp16 two-piece GEMMs (model load)"),
     (r"attention_h2_kernel", "time-axis attention, L = 801 (fp32 via two-piece fp16)"),
     (r"attention_short_h2_kernel", "band-axis attention, L = 62 (fp32 via two-piece fp16)"),
-    (r"rmsnorm_h2_kernel", "pre-norms, written as fp16 pieces for the QKV / FFN-up GEMMs"),
+    (r"rmsnorm_h2_kernel", "FFN pre-norm, written as fp16 pieces for the FFN-up GEMM"),
     (r"gemm_split_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via split bf16)"),
