@@ -236,9 +236,8 @@ int vh_mask_estimate(vh_context *ctx, vh_model *model, const float *features, in
 int vh_forward(vh_context *ctx, vh_model *model, const float *audio, int length, float *vocals,
                float *instrumental);
 /* Chunked separation of a long device audio[C][length]: windows of `chunk`
-   samples every `step` samples (zero-padded at the end), at most `batch`
-   windows per device pass (as few passes as that allows, their sizes
-   balanced), linear cross-fade over the overlap normalised by the summed
+   samples every `step` samples (zero-padded at the end), `batch` windows per
+   device pass, linear cross-fade over the overlap normalised by the summed
    fade weights; `instrumental` (nullable) as for vh_forward.  No reference counterpart (the reference host runs the whole
    file as one window, native/vocalarc_separation.c:1344). */
 int vh_separate(vh_context *ctx, vh_model *model, const float *audio, int length, int chunk, int step, int batch,

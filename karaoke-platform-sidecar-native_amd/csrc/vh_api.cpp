@@ -997,16 +997,11 @@ extern "C" int vh_separate(vh_context *ctx, vh_model *m, const float *audio, int
                "hipMemcpy(chunk starts)") ||
         !check(hipStreamSynchronize(s), "hipStreamSynchronize(starts)"))
         return 0;
-    // as few passes as `batch` allows, their sizes balanced (50 windows by 8:
-    // one pass of 8 and six of 7, not six of 8 and one of 2, whose grids
-    // fill the device in fewer, more ragged rounds)
-    const int passes = (count + batch - 1) / batch;
-    for (int p = 0, k0 = 0; p < passes; p++) {
-        const int n = count / passes + (p < count % passes ? 1 : 0);
+    for (int k0 = 0; k0 < count; k0 += batch) {
+        const int n = std::min(batch, count - k0);
         if (!run_windows(m, audio, length, static_cast<const int64_t *>(m->starts.ptr) + k0, chunk, n,
                          m->chunk_out.f() + (size_t)k0 * d.channels * chunk, chunk))
             return 0;
-        k0 += n;
     }
     FadeArgs a;
     a.chunks = m->chunk_out.f(); a.count = count; a.chunk = chunk; a.step = step; a.C = d.channels; a.length = length;
