@@ -513,8 +513,11 @@ bool split_weights_h2(hipStream_t s, const float *W, int N, int K, int ldw, void
                   ldw);
         return false;
     }
-    hipLaunchKernelGGL(absmax_kernel, dim3(1), dim3(1024), 0, s, W, N, K, ldw, static_cast<float *>(pieces));
-    if (!sync_debug(s, "absmax_kernel")) return false;
+    hipLaunchKernelGGL(zero_float_kernel, dim3(1), dim3(1), 0, s, static_cast<float *>(pieces));
+    const int64_t nw = (int64_t)N * K;
+    hipLaunchKernelGGL(absmax_rows_kernel, dim3((unsigned)std::min<int64_t>(512, (nw + 4095) / 4096)), dim3(256), 0, s,
+                       W, N, K, ldw, static_cast<float *>(pieces));
+    if (!sync_debug(s, "absmax_rows_kernel")) return false;
     const int64_t n = (int64_t)(N + GS_BN - 1) / GS_BN * GS_BN * K;
     hipLaunchKernelGGL(split_weight_h2_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, W, N, K, ldw, pieces);
     return sync_debug(s, "split_weight_h2_kernel");

@@ -16,6 +16,13 @@ algorithmic work:
 
     python -m vocalarc_hip.kernel_stats kernels RUN_DIR BENCH_JSONL OUT.md "<command>"
 
+The reference host linked against the HIP provider under `rocprofv3
+--kernel-trace --memory-copy-trace`: splits the trace into the host's
+requests at idle gaps of the device (> 20 ms), and reports per request the
+kernel and copy time beside the host's own `inferenceMs` from its responses:
+
+    python -m vocalarc_hip.kernel_stats host RUN_DIR RESPONSES_JSONL OUT.md "<commands>"
+
 `rocprofv3 --pmc` passes (one directory each): the per-dispatch average of
 every counter over the dispatches whose kernel name matches a regular
 expression (optionally only those with a given grid size):
@@ -167,6 +174,48 @@ def counters(regex: str, out: str, command: str, *dirs: str) -> int:
     return 0
 
 
+def host(run_dir: str, responses: str, out: str, command: str) -> int:
+    ktrace = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+              for r in csv.DictReader(open(next(Path(run_dir).rglob("*kernel_trace.csv"))))]
+    ctrace = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r.get("Direction", r.get("Operation", "")))
+              for r in csv.DictReader(open(next(Path(run_dir).rglob("*memory_copy_trace.csv"))))]
+    events = sorted([(a, b, "k", n) for a, b, n in ktrace] + [(a, b, "c", n) for a, b, n in ctrace])
+    groups, cur, last = [], [], None
+    for e in events:
+        if last is not None and e[0] - last > 20_000_000:
+            groups.append(cur)
+            cur = []
+        cur.append(e)
+        last = e[1] if last is None else max(last, e[1])
+    if cur:
+        groups.append(cur)
+    sep = [json.loads(x) for x in Path(responses).read_text().splitlines() if x.strip()]
+    sep = [r for r in sep if r.get("type") == "separated"]
+    lines = ["# The reference host with the HIP provider: device time per request (command below)", "",
+             "Commands (repository root, MI355X box):", "", "```", command.strip(), "```", "",
+             "Source: the rocprofv3 kernel and memory-copy traces, split into requests at idle gaps of the device "
+             "(> 20 ms); `inferenceMs` is the host's own timing of the request (STFT to iSTFT, "
+             "native/vocalarc_separation.c:1584-1586) from its responses, in order. The first request also uploads, "
+             "splits and bounds the weights (first use of the cached tensors).", "",
+             "| request | inferenceMs | device span ms | kernels ms | copies ms (count) | kernel classes (ms) |",
+             "|---:|---:|---:|---:|---:|---|"]
+    for i, g in enumerate(groups):
+        kern = sum(b - a for a, b, t, _ in g if t == "k") / 1e6
+        cop = [b - a for a, b, t, _ in g if t == "c"]
+        span = (max(b for _, b, _, _ in g) - min(a for a, _, _, _ in g)) / 1e6
+        by: dict[str, float] = {}
+        for a, b, t, n in g:
+            if t == "k":
+                key = re.sub(r"\(.*", "", n).replace("void ", "")
+                by[key] = by.get(key, 0.0) + (b - a) / 1e6
+        top = "; ".join(f"{k} {v:.1f}" for k, v in sorted(by.items(), key=lambda kv: -kv[1])[:5])
+        inf = f"{float(sep[i]['inferenceMs']):.1f}" if i < len(sep) and "inferenceMs" in sep[i] else ""
+        lines.append(f"| {i + 1} | {inf} | {span:.1f} | {kern:.1f} | {sum(cop) / 1e6:.1f} ({len(cop)}) | {top} |")
+    Path(out).write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+    return 0
+
+
 def _timed_calls(r: dict) -> int:
     """Timed calls of a record: its timed dispatches over the dispatches one
     call launches (dispatches = calls made x per call)."""
@@ -177,6 +226,8 @@ def _timed_calls(r: dict) -> int:
 def main() -> int:
     if sys.argv[1] == "kernels":
         return kernels(*sys.argv[2:6])
+    if sys.argv[1] == "host":
+        return host(*sys.argv[2:6])
     if sys.argv[1] == "counters":
         return counters(sys.argv[2], sys.argv[3], sys.argv[4], *sys.argv[5:])
     run_dir, bench_json, out, command = sys.argv[1:5]
