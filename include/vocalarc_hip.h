@@ -162,11 +162,16 @@ int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *src, void *
    any length) runs them in fp32 accuracy as two-piece fp16 splits of
    power-of-two-scaled operands, the scales from max|qkv| computed on the
    device (the default fp32 path's attention on both axes, which takes its
-   bound from the projection's weights instead). */
+   bound from the projection's weights instead); with VH_ATT_H2,
+   VH_ATT_OUT_H2 writes out as h2 rows (vh_rmsnorm_h2's layout) scaled from
+   that same bound, max|qkv| -- the A operand of a vh_gemm_h2 with
+   VH_H2_A_ROWS and a_bound = max|qkv|, as the model's out projection takes
+   it (vh_attention_noalloc does not take it). */
 #define VH_ATT_OUT_BF16 1
 #define VH_ATT_BF16 2
 #define VH_ATT_SPLIT 4
 #define VH_ATT_H2 8
+#define VH_ATT_OUT_H2 16
 int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                  int apply_rotary, int flags);
 /* vh_attention without any device allocation, for callers that cannot

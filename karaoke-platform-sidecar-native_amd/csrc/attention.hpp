@@ -40,6 +40,10 @@ struct AttnArgs {
     int gate_col;   // < 0: no gates
     float scale;    // 1/sqrt(64)
     const float *bound;  // device bound on |q|, |k|, |v| (attention_h2_kernel only)
+    // fp32 out written as h2 rows (h2.hpp) scaled by 2^h2_exponent(*bound):
+    // the out projection's A operand, split here once instead of in each of
+    // its column tiles (the fp16 two-piece kernels only)
+    int out_h2;
 };
 
 constexpr int ATT_DH = 64;

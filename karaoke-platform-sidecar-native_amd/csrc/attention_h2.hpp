@@ -324,6 +324,26 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
     // the gate logit, loaded here rather than held through the key loop
     const float gate = a.gate_col >= 0 ? sigmoid_dev(qkv[(size_t)row * a.ld + a.gate_col + h]) : 1.0f;
     TO *op = static_cast<TO *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
+    if constexpr (std::is_same<TO, float>::value) {
+        if (a.out_h2) {
+            // chunk c of the head's 64 dims: this lane holds dims 4lh..4lh+3
+            // and 8+4lh..8+4lh+3 of it (o[c/2] quads 2(c%2), 2(c%2)+1), the
+            // chunk's MFMA operand half lh: h slot lh, m slot 2+lh
+            const float so = ldexpf(1.0f, h2_exponent(bnd));
+            unsigned char *rowp = reinterpret_cast<unsigned char *>(op);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                floatx4 lo, hi;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    lo[r] = (o[c >> 1][8 * (c & 1) + r] * inv) * gate;
+                    hi[r] = (o[c >> 1][8 * (c & 1) + 4 + r] * inv) * gate;
+                }
+                store8_h2_half(rowp + 64 * c, lh, lo, hi, so);
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -504,8 +524,22 @@ __global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) 
         if (q < a.L) {
             const float f = (1.0f / l) * (a.gate_col >= 0 ? sigmoid_dev(gate_logit) : 1.0f) * o_unscale;
             TO *op = static_cast<TO *>(a.out) + (size_t)attn_row(a, s, q) * a.ld_out + h * ATT_DH + 4 * g;
+            bool done = false;
+            if constexpr (std::is_same<TO, float>::value) {
+                if (a.out_h2) {
+                    // dims 16dt + 4g .. +3: group g of chunk dt, whose groups
+                    // g^2 lies in lane ^ 32 (the same query)
+                    const float so = ldexpf(1.0f, h2_exponent(bnd));
+                    unsigned char *rowp = reinterpret_cast<unsigned char *>(op - 4 * g);
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) st4(op + 16 * dt, o[dt] * f);
+                    for (int dt = 0; dt < 4; dt++) store4_h2_swap<32>(rowp + 64 * dt, g, o[dt] * f, so);
+                    done = true;
+                }
+            }
+            if (!done) {
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++) st4(op + 16 * dt, o[dt] * f);
+            }
         }
         __syncthreads();  // LDS is refilled for the next task
     }

@@ -126,20 +126,34 @@ VH_DEVICE void store4_h2(unsigned char *chunk, int j, floatx4 v, float s) {
     *reinterpret_cast<u32x2 *>(chunk + 32 + o) = u32x2{m01, m23};
 }
 
-// The same for a quad of lanes holding the four groups 4j..4j+3 (lane j of the
-// quad, j = lane % 4) of one chunk: lanes j and j^2 swap one piece, so each
-// lane writes a whole 16-byte slot -- lanes 0, 1 the h slots, lanes 2, 3 the
-// m slots -- instead of two 8-byte halves.  Every lane of the quad takes part.
-VH_DEVICE void store4_h2_quad(unsigned char *chunk, int j, floatx4 v, float s) {
+// The same for four lanes holding the four groups 4j..4j+3 of one chunk, the
+// lanes of groups j and j^2 being XOR apart (lane j of a quad: XOR = 2; the
+// band-axis attention's lane groups: XOR = 32): they swap one piece, so each
+// lane writes a whole 16-byte slot -- groups 0, 1 the h slots, groups 2, 3 the
+// m slots -- instead of two 8-byte halves.  Every one of the four lanes takes
+// part.
+template <int XOR>
+VH_DEVICE void store4_h2_swap(unsigned char *chunk, int j, floatx4 v, float s) {
     const uint32_t h01 = pack_f16x2(v[0] * s, v[1] * s), h23 = pack_f16x2(v[2] * s, v[3] * s);
     const uint32_t m01 = m_pair_f16(v[0], v[1], s, h01), m23 = m_pair_f16(v[2], v[3], s, h23);
     const bool h_slot = j < 2;
-    const uint32_t r0 = (uint32_t)__shfl_xor((int)(h_slot ? m01 : h01), 2, 64);
-    const uint32_t r1 = (uint32_t)__shfl_xor((int)(h_slot ? m23 : h23), 2, 64);
+    const uint32_t r0 = (uint32_t)__shfl_xor((int)(h_slot ? m01 : h01), XOR, 64);
+    const uint32_t r1 = (uint32_t)__shfl_xor((int)(h_slot ? m23 : h23), XOR, 64);
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     // slot j = h of groups j, j+2; slot 2 + (j-2) = m of groups j-2, j
     if (h_slot) *reinterpret_cast<u32x4 *>(chunk + 16 * j) = u32x4{h01, h23, r0, r1};
     else *reinterpret_cast<u32x4 *>(chunk + 32 + 16 * (j - 2)) = u32x4{r0, r1, m01, m23};
+}
+VH_DEVICE void store4_h2_quad(unsigned char *chunk, int j, floatx4 v, float s) { store4_h2_swap<2>(chunk, j, v, s); }
+
+// Eight values of one chunk -- k 0-3 and 8-11 (half 0) or k 4-7 and 12-15
+// (half 1), the pieces of one MFMA operand half -- times s into an h2 row: h
+// to slot `half`, m to slot 2 + `half`, 16 bytes each.
+VH_DEVICE void store8_h2_half(unsigned char *chunk, int half, floatx4 lo, floatx4 hi, float s) {
+    halfx8 h, m;
+    split8_h2(lo, hi, s, h, m);
+    *reinterpret_cast<halfx8 *>(chunk + 16 * half) = h;
+    *reinterpret_cast<halfx8 *>(chunk + 32 + 16 * half) = m;
 }
 
 }  // namespace vh

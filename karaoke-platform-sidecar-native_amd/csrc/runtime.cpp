@@ -750,9 +750,14 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
 }
 
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
-               int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split, const float *bound) {
+               int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split, const float *bound,
+               bool out_h2) {
     if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
+        return false;
+    }
+    if (out_h2 && (out_bf16 || qkv_bf16 || !split || !bound || ((uintptr_t)out & 15))) {
+        set_error("attention: h2 rows out need the fp16 two-piece kernels (fp32 qkv, a bound) and a 16-byte aligned out");
         return false;
     }
     AttnArgs a;
@@ -762,6 +767,7 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     a.group = lay.group; a.group_stride = lay.group_stride; a.seq_stride = lay.seq_stride; a.pos_stride = lay.pos_stride;
     a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
     a.bound = split && !qkv_bf16 ? bound : nullptr;
+    a.out_h2 = out_h2 ? 1 : 0;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
     if (lay.L <= 64 && !qkv_bf16) {
         // persistent: four workgroups per CU loop over the (sequence, head) tasks
@@ -937,9 +943,9 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
         gq.row_norm = true;
         if (!gemm_h2(s, gq, OperandBound{xb->dev, 0.0f}, EPI_STORE, t, "gemm_qkv")) return false;
         if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, true,
-                       att_h2 ? w.bounds + 1 : nullptr))
+                       att_h2 ? w.bounds + 1 : nullptr, att_h2))
             return false;
-        if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out"))
+        if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, att_h2, "gemm_out"))
             return false;
         if (!rmsnorm_h2(s, x, D, w.ff_gamma, normed, D, tokens, D, w.bounds + 2, t)) return false;
         GemmArgsH2 g1{normed, D, w.w1_p, w.b1, hid, d.ff_dim, tokens, d.ff1_out(), D};
@@ -961,11 +967,15 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
     if (!lin(normed, D, w.wqkvg, w.wqkvg_p, 0, w.bqkvg, qkvg, nq, nq, D, EPI_STORE, qkv_h2, "gemm_qkv")) return false;
     // rotary + attention + gates (products as fp16 two-piece splits on the
     // default fp32 path)
+    // the two-piece attention writes its output as the out projection's
+    // pieces when that GEMM runs on them (same bound: the value bound)
+    const bool attn_rows = att_h2 && use_h2(w.wout_p, inner);
     if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, precision == PREC_FP32,
-                   att_h2 ? w.bounds + 1 : nullptr))
+                   att_h2 ? w.bounds + 1 : nullptr, attn_rows))
         return false;
     // out projection added to the residual stream
-    if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, false, "gemm_out")) return false;
+    if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, attn_rows, "gemm_out"))
+        return false;
     // FFN
     if (!(ff1_h2 ? rmsnorm_h2(s, x, D, w.ff_gamma, normed, D, tokens, D, w.bounds + 2, t)
                  : rmsnorm(s, x, D, w.ff_gamma, normed, D, tokens, D, t)))

@@ -210,10 +210,11 @@ struct AttnLayout {
 // bounding |q|, |k|, |v|) is given (attention_h2.hpp, any L), else, for
 // L > 64, as exact three-piece bf16 splits (attention_split.hpp; L <= 64
 // keeps the fp32 MFMA kernel).  rope: interleaved rotary
-// table of length lay.L (or null).
+// table of length lay.L (or null).  out_h2 (with `bound`): out written as h2
+// rows scaled by 2^h2_exponent(*bound), for a gemm_h2 with a_h2 and that bound.
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false,
-               bool split = false, const float *bound = nullptr);
+               bool split = false, const float *bound = nullptr, bool out_h2 = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {

@@ -282,7 +282,7 @@ extern "C" int vh_to_bf16(vh_context *ctx, int64_t rows, int cols, const float *
 
 extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                             int apply_rotary, int flags) {
-    if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16 | VH_ATT_SPLIT | VH_ATT_H2))) return 0;
+    if (!ctx || (flags & ~(VH_ATT_OUT_BF16 | VH_ATT_BF16 | VH_ATT_SPLIT | VH_ATT_H2 | VH_ATT_OUT_H2))) return 0;
     const float *rt = nullptr;
     if (apply_rotary && !ctx->rope.get_interleaved(length, 64, ctx->stream, &rt)) return 0;
     const int inner = heads * 64;
@@ -300,9 +300,14 @@ extern "C" int vh_attention(vh_context *ctx, int sequences, int length, int head
         if (bounds_usable(ctx->stream, ctx->bounds.f(), 1, &b) < 0) return 0;
         h2_ok = h2_attention_bound_ok(b);
     }
+    const bool out_h2 = (flags & VH_ATT_OUT_H2) != 0;
+    if (out_h2 && !h2_ok) {
+        set_error("vh_attention: VH_ATT_OUT_H2 needs the two-piece kernel (VH_ATT_H2, fp32, max|qkv| in its range)");
+        return 0;
+    }
     return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
                      &ctx->timer, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0,
-                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2_ok ? ctx->bounds.f() : nullptr)
+                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2_ok ? ctx->bounds.f() : nullptr, out_h2)
                ? 1
                : 0;
 }

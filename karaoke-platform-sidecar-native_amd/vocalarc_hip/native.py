@@ -22,7 +22,7 @@ LIB_PATH = Path(os.environ.get("VOCALARC_HIP_LIB", PKG / "lib" / "libvocalarc_hi
 EPI_STORE, EPI_GELU, EPI_TANH, EPI_RESIDUAL, EPI_GEGLU = range(5)
 PRECISION_FP32, PRECISION_BF16, PRECISION_FP32_MFMA = 0, 1, 2
 BF16_A, BF16_C, BF16_STAGED = 1, 2, 4  # vh_gemm_bf16 operand flags; STAGED forces the register-staged kernel
-ATT_OUT_BF16, ATT_BF16, ATT_SPLIT, ATT_H2 = 1, 2, 4, 8  # vh_attention flags
+ATT_OUT_BF16, ATT_BF16, ATT_SPLIT, ATT_H2, ATT_OUT_H2 = 1, 2, 4, 8, 16  # vh_attention flags
 NOALLOC_MAX_LENGTH = 4096  # VH_NOALLOC_MAX_LENGTH
 SPEC_REFERENCE, SPEC_FRAME_MAJOR = 0, 1  # spectrum layouts: [F][C][T][2] / [C][T][F][2]
 
@@ -259,12 +259,12 @@ class Context:
         _ok(lib().vh_to_bf16(self.h, rows, cols, ptr(src), ptr(dst), ld), "vh_to_bf16")
 
     def attention(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True, out_bf16: bool = False,
-                  bf16: bool = False, split: bool = False, h2: bool = False):
+                  bf16: bool = False, split: bool = False, h2: bool = False, out_h2: bool = False):
         """bf16: qkv is bf16 and the bf16-MFMA kernel runs; out_bf16: out is bf16; split: fp32 accuracy on the
         bf16 matrix cores (three-piece splits, length > 64); h2: fp32 accuracy on the fp16 matrix cores (two-piece
-        splits, scales from max|qkv|, any length)."""
+        splits, scales from max|qkv|, any length); out_h2 (with h2): out as h2 rows scaled from max|qkv|."""
         _ok(lib().vh_attention(self.h, sequences, length, heads, ptr(qkv), ptr(out), int(rotary),
-                               _att_flags(out_bf16, bf16, split, h2)), "vh_attention")
+                               _att_flags(out_bf16, bf16, split, h2) | (ATT_OUT_H2 if out_h2 else 0)), "vh_attention")
 
     def attention_noalloc(self, qkv, out, sequences: int, length: int, heads: int, rotary: bool = True,
                           out_bf16: bool = False, bf16: bool = False, split: bool = False, h2: bool = False) -> int:

@@ -196,6 +196,45 @@ def test_gemm_h2_geglu(ctx, rng):
     assert err.max() <= 2e-5, err.max()
 
 
+@pytest.mark.parametrize("S,L", [(3, 801), (2, 97), (40, 62), (30, 17)])
+def test_attention_h2_rows_out(ctx, rng, S, L):
+    """VH_ATT_OUT_H2: the two-piece attention (time-axis kernel for L > 64,
+    band-axis kernel otherwise) writes its output as h2 rows scaled from
+    max|qkv|: the pieces are those of its fp32 output times 2^e, bit for bit,
+    at the documented positions, and the out projection fed them gives the
+    same bits as the GEMM splitting that fp32 output itself with the same
+    bound.  Ragged lengths leave rows of the last query wave partly empty."""
+    H, N = 8, 384
+    K = H * 64
+    qkv = rng.standard_normal((S * L, 3 * K)).astype(np.float32)
+    dq = to_dev(qkv)
+    bound = float(np.abs(qkv).max())
+    out32 = empty_dev((S * L, K))
+    outh = torch.full((S * L, K), 7.0, device="cuda:0")
+    ctx.attention(dq, out32, S, L, H, rotary=True, h2=True)
+    ctx.attention(dq, outh, S, L, H, rotary=True, h2=True, out_h2=True)
+    torch.cuda.synchronize()
+    y = from_dev(out32)
+    e = _exponent(bound)
+    h, m = _decode_h2_rows(outh.cpu().numpy().view(np.float16).ravel(), S * L, K)
+    ys = y * np.float32(2.0 ** e)
+    h_ref = ys.astype(np.float16).astype(np.float32)
+    m_ref = (ys - h_ref).astype(np.float16).astype(np.float32)
+    for got, want in ((h, h_ref), (m, m_ref)):
+        nz = want != 0
+        assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32))
+        assert np.all(got[~nz] == 0.0)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    planes = _pieces(ctx, w)
+    c_rows, c_fp32 = to_dev(np.ones((S * L, N), np.float32)), to_dev(np.ones((S * L, N), np.float32))
+    ctx.gemm_h2(outh, planes, c_rows, S * L, N, K, epilogue=native.EPI_RESIDUAL, a_bound=bound, a_rows=True)
+    ctx.gemm_h2(out32, planes, c_fp32, S * L, N, K, epilogue=native.EPI_RESIDUAL, a_bound=bound)
+    torch.cuda.synchronize()
+    assert torch.equal(c_rows, c_fp32)
+    with pytest.raises(native.NativeError):
+        ctx.attention(dq, outh, S, L, H, rotary=True, out_h2=True)  # h2 rows need the two-piece kernel
+
+
 def _geglu_perm(F: int) -> np.ndarray:
     """Row order of a GELU-GLU weight in the library: 32 value rows, then their 32 gate rows."""
     perm = np.empty(2 * F, dtype=np.int64)
