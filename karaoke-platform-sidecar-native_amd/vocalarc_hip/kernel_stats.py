@@ -42,6 +42,10 @@ from pathlib import Path
 # the separation pass
 ROLES = [
     (r"gemm_h2_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via two-piece fp16)"),
+    (r"gemm_h2_kernel(<3, true|ILi3ELb1E)",
+     "out projection + residual, A as the attentions' h2 rows (fp32 via two-piece fp16)"),
+    (r"gemm_h2_kernel(<3, false|ILi3ELb0E)",
+     "FFN down-projection + residual, raising the stream's bound (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<0, false, true>|ILi0ELb0ELb1E)",
      "fused QKV + gate projection with the attention's pre-norm inside (fp32 via two-piece fp16)"),
