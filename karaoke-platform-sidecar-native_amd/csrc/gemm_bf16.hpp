@@ -53,10 +53,14 @@ VH_DEVICE void store_out(T *p, float v) {
 // per-element row checks, so the residual epilogue issues its 16 loads of C
 // together instead of one load-wait-store per element.  mx_out (residual
 // epilogue only; null for none): raised to the largest |C| this lane wrote.
+// bpre (null for none): the bias of the lane's column in each of the FN
+// column tiles (0 past N), loaded by the caller before its K loop so that
+// the load's latency is not spent here.
 template <int EPI, typename TC, int FM, int FN>
 VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[FM][FN], int row0, int col0, int li,
-                                  int lh, float *mx_out = nullptr) {
+                                  int lh, float *mx_out = nullptr, const float *bpre = nullptr) {
     TC *C = static_cast<TC *>(d.C);
+    auto bias_of = [&](int j, int col) { return bpre ? bpre[j] : (d.bias ? d.bias[col] : 0.0f); };
     const bool rows_full = row0 + 32 * FM <= d.M;
     auto row_of = [&](int i, int r) { return row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3); };
     if constexpr (EPI == EPI_GEGLU) {
@@ -67,8 +71,8 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
             const int ng = nv + 32;
             const int oc = (col0 + 64 * p) / 2 + li;
             if (ng >= d.N) continue;
-            const float bv = d.bias ? d.bias[nv] : 0.0f;
-            const float bg = d.bias ? d.bias[ng] : 0.0f;
+            const float bv = bias_of(2 * p, nv);
+            const float bg = bias_of(2 * p + 1, ng);
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -86,7 +90,7 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
         for (int j = 0; j < FN; j++) {
             const int col = col0 + j * 32 + li;
             if (col >= d.N) continue;
-            const float bc = d.bias ? d.bias[col] : 0.0f;
+            const float bc = bias_of(j, col);
 #pragma unroll
             for (int i = 0; i < FM; i++) {
                 auto value = [&](int r) {

@@ -103,7 +103,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
 
     const int ea = h2_exponent(a_bound);
     const int ew = h2_exponent(*static_cast<const float *>(d.W));
-    const float a_scale = ldexpf(1.0f, ea), a_unscale = ldexpf(1.0f, -ea), w_unscale = ldexpf(1.0f, -ew);
+    const float a_scale = ldexpf(1.0f, ea);
 
     const int tid = (int)threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -111,6 +111,16 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     const uint32_t ring_base = (uint32_t)(uintptr_t)ring;
     auto swz_a = [](int r) { return (r >> 2) & 3; };
     auto swz_w = [](int r) { return (r >> 3) & 1; };
+
+    // the bias of the lane's column in each 32-column tile (0 past N), loaded
+    // before the K loop so that its latency is spent there, not in the
+    // epilogue
+    float bpre[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int col = n0 + 32 * j + li;
+        bpre[j] = d.bias && col < d.N ? d.bias[col] : 0.0f;
+    }
 
     // A: 16 loads of 1 KB (16 rows each), wave w loads blocks w and w+8 from
     // the tile's first row (scalar base) plus its lane offset (below 2^32:
@@ -212,8 +222,14 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     if (live > 64) k_loop(std::integral_constant<int, 4>());
     else if (live > 32) k_loop(std::integral_constant<int, 2>());
     else k_loop(std::integral_constant<int, 1>());
+    // both scales undone at once: acc 2^-(ea+ew) by one v_ldexp_f32 (exact, as
+    // the two power-of-two multiplies it replaces were where their product
+    // is a normal float, and correctly rounded where it is not)
+    const int eu = -(ea + ew);
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[0][j] = (acc[0][j] * a_unscale) * w_unscale;  // exact: powers of two
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[0][j][r] = ldexpf(acc[0][j][r], eu);
     if constexpr (NORM) {
         // lanes li and li + 32 summed the two halves of row wave*32 + li;
         // register 4q + e of a lane holds row 8q + 4lh + e of the wave's 32
@@ -233,7 +249,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     GemmDescBF16 e{};
     e.bias = d.bias; e.C = d.C; e.M = d.M; e.N = d.N; e.K = d.K; e.ldc = d.ldc;
     float mx = 0.0f;
-    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh, &mx);
+    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh, &mx, bpre);
     if constexpr (EPI == EPI_RESIDUAL) {
         if (d.amax) {
             // one atomic per workgroup (one per wave, all on one address,
