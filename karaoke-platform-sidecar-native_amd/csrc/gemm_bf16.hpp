@@ -45,6 +45,13 @@ VH_DEVICE void store_out(T *p, float v) {
     if constexpr (std::is_same<T, float>::value) __builtin_nontemporal_store(v, p);
     else *p = (bf16)v;
 }
+// The same through a global-address-space pointer (the saddr-form stores
+// of gemm_bf16_epilogue).
+template <typename T>
+VH_DEVICE void store_out(__attribute__((address_space(1))) T *p, float v) {
+    if constexpr (std::is_same<T, float>::value) __builtin_nontemporal_store(v, p);
+    else *p = (bf16)v;
+}
 
 // Fused epilogue of a wave's FM x FN accumulators whose tile starts at
 // (row0, col0).  Accumulator layout as for the fp32 32x32 MFMA: lane (li,
@@ -55,14 +62,35 @@ VH_DEVICE void store_out(T *p, float v) {
 // epilogue only; null for none): raised to the largest |C| this lane wrote.
 // bpre (null for none): the bias of the lane's column in each of the FN
 // column tiles (0 past N), loaded by the caller before its K loop so that
-// the load's latency is not spent here.
+// the load's latency is not spent here.  rs (null for none): a scale per
+// accumulator row (rs[16 i + r] for register r of acc[i][.]), applied with
+// the bias in one fused multiply-add (the row norm of the fp16 two-piece
+// GEMM).
 template <int EPI, typename TC, int FM, int FN>
 VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[FM][FN], int row0, int col0, int li,
-                                  int lh, float *mx_out = nullptr, const float *bpre = nullptr) {
+                                  int lh, float *mx_out = nullptr, const float *bpre = nullptr,
+                                  const float *rs = nullptr) {
     TC *C = static_cast<TC *>(d.C);
     auto bias_of = [&](int j, int col) { return bpre ? bpre[j] : (d.bias ? d.bias[col] : 0.0f); };
+    auto pre = [&](int i, int j, int r, float b) { return rs ? fmaf(acc[i][j][r], rs[16 * i + r], b) : acc[i][j][r] + b; };
     const bool rows_full = row0 + 32 * FM <= d.M;
     auto row_of = [&](int i, int r) { return row0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3); };
+    // Full tiles address element (i, r) as a row pointer that is the same for
+    // the whole wave (row0 is wave-uniform in every caller, so it lives in
+    // SGPRs) plus the lane's 32-bit byte offset: the loads and stores take
+    // the saddr form, with no 64-bit address arithmetic per element.
+    // (ldc * sizeof(TC) < 2^26 by the callers' checks, so row offsets within a
+    // wave's 32 * FM rows fit 32 bits)
+    typedef __attribute__((address_space(1))) char gchar;
+    typedef __attribute__((address_space(1))) TC gTC;
+    const uint32_t pitch = (uint32_t)d.ldc * (uint32_t)sizeof(TC);
+    const uint32_t lh_off = (uint32_t)(4 * lh) * pitch;
+    const gchar *const rbase = (const gchar *)(reinterpret_cast<char *>(C) + (size_t)row0 * (size_t)pitch);
+    auto at = [&](int i, int r, uint32_t off) {
+        const gchar *rp = rbase + (uint32_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * pitch;
+        asm("" : "+s"(rp));  // opaque: the lane offset is not folded into it
+        return (gTC *)(rp + off);
+    };
     if constexpr (EPI == EPI_GEGLU) {
         // accumulator pair (2p, 2p+1) = value and gate columns of one 64-wide group
 #pragma unroll
@@ -73,15 +101,21 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
             if (ng >= d.N) continue;
             const float bv = bias_of(2 * p, nv);
             const float bg = bias_of(2 * p + 1, ng);
+            const uint32_t off = lh_off + (uint32_t)oc * (uint32_t)sizeof(TC);
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+            for (int i = 0; i < FM; i++) {
+                auto value = [&](int r) { return pre(i, 2 * p, r, bv) * gelu_dev(pre(i, 2 * p + 1, r, bg)); };
+                if (rows_full) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = row_of(i, r);
-                    if (rows_full || row < d.M)
-                        store_out(C + (size_t)row * d.ldc + oc,
-                                  (acc[i][2 * p][r] + bv) * gelu_dev(acc[i][2 * p + 1][r] + bg));
+                    for (int r = 0; r < 16; r++) store_out(at(i, r, off), value(r));
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = row_of(i, r);
+                        if (row < d.M) store_out(C + (size_t)row * d.ldc + oc, value(r));
+                    }
                 }
+            }
         }
     } else {
         static_assert(EPI != EPI_RESIDUAL || std::is_same<TC, float>::value, "residual output is fp32");
@@ -91,10 +125,11 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
             const int col = col0 + j * 32 + li;
             if (col >= d.N) continue;
             const float bc = bias_of(j, col);
+            const uint32_t off = lh_off + (uint32_t)col * (uint32_t)sizeof(TC);
 #pragma unroll
             for (int i = 0; i < FM; i++) {
                 auto value = [&](int r) {
-                    const float v = acc[i][j][r] + bc;
+                    const float v = pre(i, j, r, bc);
                     if constexpr (EPI == EPI_GELU) return gelu_dev(v);
                     else if constexpr (EPI == EPI_TANH) return tanhf(v);
                     else return v;
@@ -103,16 +138,16 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
                     if constexpr (EPI == EPI_RESIDUAL) {
                         float old[16];
 #pragma unroll
-                        for (int r = 0; r < 16; r++) old[r] = C[(size_t)row_of(i, r) * d.ldc + col];
+                        for (int r = 0; r < 16; r++) old[r] = *at(i, r, off);
 #pragma unroll
                         for (int r = 0; r < 16; r++) {
                             const float v = old[r] + value(r);
                             mx = fmaxf(mx, fabsf(v));
-                            store_out(C + (size_t)row_of(i, r) * d.ldc + col, v);
+                            store_out(at(i, r, off), v);
                         }
                     } else {
 #pragma unroll
-                        for (int r = 0; r < 16; r++) store_out(C + (size_t)row_of(i, r) * d.ldc + col, value(r));
+                        for (int r = 0; r < 16; r++) store_out(at(i, r, off), value(r));
                     }
                 } else {
 #pragma unroll
@@ -168,7 +203,7 @@ __device__ __forceinline__ void gemm_bf16_body(const GemmDescBF16 &d, int tile) 
     const int n0 = (in_group / group_rows) * GB_BN;
 
     const int tid = (int)threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int wm = wave / WN, wn = wave % WN;
     const int li = lane & 31, lh = lane >> 5;
 

@@ -230,6 +230,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     for (int j = 0; j < 4; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[0][j][r] = ldexpf(acc[0][j][r], eu);
+    float rs[16];  // NORM: the scale of each accumulator row, applied with the bias
     if constexpr (NORM) {
         // lanes li and li + 32 summed the two halves of row wave*32 + li;
         // register 4q + e of a lane holds row 8q + 4lh + e of the wave's 32
@@ -241,15 +242,13 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
         for (int q = 0; q < 4; q++) {
             const floatx4 r4 = *reinterpret_cast<const floatx4 *>(&rscale[wave][8 * q + 4 * lh]);
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc[0][j][4 * q + e] *= r4[e];
+            for (int e = 0; e < 4; e++) rs[4 * q + e] = r4[e];
         }
     }
     GemmDescBF16 e{};
     e.bias = d.bias; e.C = d.C; e.M = d.M; e.N = d.N; e.K = d.K; e.ldc = d.ldc;
     float mx = 0.0f;
-    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh, &mx, bpre);
+    gemm_bf16_epilogue<EPI, float, 1, 4>(e, acc, m0 + wave * 32, n0, li, lh, &mx, bpre, NORM ? rs : nullptr);
     if constexpr (EPI == EPI_RESIDUAL) {
         if (d.amax) {
             // one atomic per workgroup (one per wave, all on one address,
