@@ -82,7 +82,7 @@ int vh_gemm(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, c
    A is fp32, rounded to bf16 (nearest even) as it is staged, or bf16 with
    VH_BF16_A (then K and lda multiples of 8); C is fp32, or bf16 with
    VH_BF16_C (not with the residual epilogue).  K and lda multiples of 4,
-   A and Wh 16-byte aligned.  bf16 A with K a multiple of 32 runs the
+   ldc at most 2^21, A and Wh 16-byte aligned.  bf16 A with K a multiple of 32 runs the
    pipelined kernel (direct global->LDS loads); VH_BF16_STAGED forces the
    register-staged kernel instead (same results, bit for bit). */
 #define VH_BF16_A 1
@@ -94,8 +94,8 @@ int vh_gemm_bf16(vh_context *ctx, int64_t M, int N, int K, const void *A, int ld
    exact sum of three bf16 pieces (h = bf16(x), m = bf16(x - h),
    l = x - h - m) and the six piece products that reach 2^-24 of a product
    are accumulated in fp32.  Ws: the weight's pieces from vh_split_weights.
-   K a multiple of 16, lda a multiple of 4 and at most 2^21, A and Ws
-   16-byte aligned.  The token-wise linear of
+   K a multiple of 16, lda a multiple of 4 and at most 2^21, ldc at most
+   2^21, A and Ws 16-byte aligned.  The token-wise linear of
    native/vocalarc_separation.c:631-636, as vh_gemm. */
 int vh_gemm_split(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, const void *Ws,
                   const float *bias, float *C, int ldc, int epilogue);
@@ -114,8 +114,8 @@ int vh_split_weights(vh_context *ctx, int N, int K, const float *W, int ldw_in, 
    and every scaled value is split into two fp16 pieces (h = fp16(y),
    m = fp16(y - h)); the products hh, hm, mh are accumulated in fp32 and the
    result scaled back.  Wp: the weight's pieces from vh_split_weights_h2.
-   K a multiple of 16, lda a multiple of 4 and at most 2^21, A 16-byte
-   aligned.  The token-wise linear of native/vocalarc_separation.c:631-636,
+   K a multiple of 16, lda a multiple of 4 and at most 2^21, ldc at most
+   2^21, A 16-byte aligned.  The token-wise linear of native/vocalarc_separation.c:631-636,
    as vh_gemm; the default fp32 path's linears. */
 #define VH_H2_A_ROWS 1 /* flags of vh_gemm_h2: A given as h2 rows (vh_rmsnorm_h2), scaled from a_bound */
 int vh_gemm_h2(vh_context *ctx, int64_t M, int N, int K, const float *A, int lda, float a_bound, const void *Wp,

@@ -79,8 +79,8 @@ VH_DEVICE void gemm_bf16_epilogue(const GemmDescBF16 &d, const floatx16 (&acc)[F
     // the whole wave (row0 is wave-uniform in every caller, so it lives in
     // SGPRs) plus the lane's 32-bit byte offset: the loads and stores take
     // the saddr form, with no 64-bit address arithmetic per element.
-    // (ldc * sizeof(TC) < 2^26 by the callers' checks, so row offsets within a
-    // wave's 32 * FM rows fit 32 bits)
+    // (ldc <= 2^21 by the callers' checks, so row offsets within a wave's
+    // 32 * FM rows fit 32 bits)
     typedef __attribute__((address_space(1))) char gchar;
     typedef __attribute__((address_space(1))) TC gTC;
     const uint32_t pitch = (uint32_t)d.ldc * (uint32_t)sizeof(TC);

@@ -200,7 +200,8 @@ static bool gemm_bf16_ok(const GemmArgsBF16 &g, int epilogue) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2) return false;
     if (g.K % 4 || g.lda % 4 || g.lda < g.K || g.ldb % 8 || g.ldb < bf16_pitch(g.K)) return false;
     if (g.a_bf16 && (g.K % 8 || g.lda % 8)) return false;
-    if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
+    // the epilogue's row offsets within a wave's rows are 32-bit
+    if (g.ldc < out_cols(g.N, epilogue) || g.ldc > (1 << 21) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
     if (g.c_bf16 && epilogue == EPI_RESIDUAL) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.B) & 15) return false;
     return true;
@@ -328,7 +329,8 @@ static_assert(GS_BK == SPLIT_K_MULTIPLE, "split GEMM K chunk");
 static bool gemm_split_ok(const GemmArgsSplit &g, int epilogue) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2) return false;
     if (g.K % GS_BK || g.lda % 4 || g.lda < g.K || g.lda > (1 << 21)) return false;  // lane load offsets are 32-bit
-    if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
+    // the epilogue's row offsets within a wave's rows are 32-bit
+    if (g.ldc < out_cols(g.N, epilogue) || g.ldc > (1 << 21) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return false;
     return true;
 }
@@ -417,7 +419,8 @@ bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *p
 static bool gemm_h2_ok(const GemmArgsH2 &g, int epilogue) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M > INT32_MAX / 2 || !g.W) return false;
     if (g.K % GS_BK || g.lda % 4 || g.lda < g.K || g.lda > (1 << 21)) return false;  // lane load offsets are 32-bit
-    if (g.ldc < out_cols(g.N, epilogue) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
+    // the epilogue's row offsets within a wave's rows are 32-bit
+    if (g.ldc < out_cols(g.N, epilogue) || g.ldc > (1 << 21) || (epilogue == EPI_GEGLU && g.N % 64)) return false;
     if (((uintptr_t)g.A | (uintptr_t)g.W) & 15) return false;
     if (g.row_norm && (g.a_h2 || !(epilogue == EPI_STORE || epilogue == EPI_GELU || epilogue == EPI_GEGLU)))
         return false;
