@@ -205,6 +205,9 @@ def test_gemm_bf16_operand_alignment_checks(ctx):
     c = torch.zeros(8, 64, device="cuda:0")
     with pytest.raises(native.NativeError, match="unsupported shape"):
         ctx.gemm_bf16(xh, wh, c, 8, 64, 20, 24, flags=native.BF16_A)  # bf16 A needs K % 8 == 0
+    with pytest.raises(native.NativeError, match="unsupported shape"):
+        ctx.gemm_bf16(torch.zeros(8, 24, device="cuda:0"), wh, c, 8, 64, 24, 24,
+                      ldc=(1 << 21) + 64)  # ldc <= 2^21 (32-bit row offsets)
 
 
 def test_rmsnorm_bf16_is_rounded_fp32(ctx, rng):

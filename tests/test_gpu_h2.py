@@ -349,6 +349,8 @@ def test_gemm_h2_rejects_bad_shapes(ctx):
         ctx.gemm_h2(x, pieces, c, 8, 8, 24, a_bound=1.0)  # K must be a multiple of 16
     with pytest.raises(native.NativeError, match="unsupported shape"):
         ctx.gemm_h2(x, pieces, c, 8, 8, 16, lda=14, a_bound=1.0)  # lda must be a multiple of 4 and >= K
+    with pytest.raises(native.NativeError, match="unsupported shape"):
+        ctx.gemm_h2(x, pieces, c, 8, 8, 16, ldc=(1 << 21) + 8, a_bound=1.0)  # ldc <= 2^21 (32-bit row offsets)
     with pytest.raises(native.NativeError, match="bad shape"):
         ctx.split_weights_h2(torch.zeros(8, 24, device="cuda:0"), pieces, 8, 24)  # K % 16
 

@@ -181,6 +181,8 @@ def test_gemm_split_rejects_bad_shapes(ctx):
         ctx.gemm_split(x, pieces, c, 8, 8, 24)  # K must be a multiple of 16
     with pytest.raises(native.NativeError, match="unsupported shape"):
         ctx.gemm_split(x, pieces, c, 8, 8, 16, lda=14)  # lda must be a multiple of 4 and >= K
+    with pytest.raises(native.NativeError, match="unsupported shape"):
+        ctx.gemm_split(x, pieces, c, 8, 8, 16, ldc=(1 << 21) + 8)  # ldc <= 2^21 (32-bit row offsets)
     with pytest.raises(native.NativeError, match="bad shape"):
         ctx.split_weights(torch.zeros(8, 24, device="cuda:0"), pieces, 8, 24)  # K % 16
 
