@@ -44,6 +44,10 @@ struct AttnArgs {
     // the out projection's A operand, split here once instead of in each of
     // its column tiles (the fp16 two-piece kernels only)
     int out_h2;
+    // the k and v columns of qkv arrive multiplied by 2^ek and 2^ev
+    // (att_h2_exponents of *bound), as the fused projection writes them: the
+    // staging splits them without scaling (the fp16 two-piece kernels only)
+    int kv_scaled;
 };
 
 constexpr int ATT_DH = 64;

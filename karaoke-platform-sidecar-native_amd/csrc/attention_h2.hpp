@@ -28,8 +28,10 @@
 
 namespace vh {
 
-// OFF32 as attention_split_kernel.
-template <int WAVES, typename TO, bool ROPE, bool OFF32>
+// OFF32 as attention_split_kernel.  KVS: k and v arrive already scaled
+// (AttnArgs::kv_scaled); rotation commutes with the power of two, so the
+// pieces are the same bits.
+template <int WAVES, typename TO, bool ROPE, bool OFF32, bool KVS = false>
 __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a) {
     constexpr int NT = 64 * WAVES;
     constexpr int CHUNKS = ATT_KB * ATT_DH / 8;  // 8-element chunks per K (or V) tile: 256
@@ -134,14 +136,19 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
                 k1 = rope_pairs(k1, st.kr[i][1]);
             }
             halfx8 p[2];
-            split8_h2(k0, k1, k_scale, p[0], p[1]);
+            if constexpr (KVS) split8_h2_unit(k0, k1, p[0], p[1]);
+            else split8_h2(k0, k1, k_scale, p[0], p[1]);
 #pragma unroll
             for (int k = 0; k < 2; k++) *reinterpret_cast<halfx8 *>(&Ks[kbk & 1][k][c >> 3][8 * (c & 7)]) = p[k];
             if (with_v) {
                 // the two keys' values interleaved, so dword e of each piece is
                 // the (key vk, key vk+1) pair of dim vd+e: one 32-bit write each
                 const floatx4 &v0 = st.v[i][0], &v1 = st.v[i][1];
-                split8_h2(floatx4{v0[0], v1[0], v0[1], v1[1]}, floatx4{v0[2], v1[2], v0[3], v1[3]}, v_scale, p[0], p[1]);
+                if constexpr (KVS)
+                    split8_h2_unit(floatx4{v0[0], v1[0], v0[1], v1[1]}, floatx4{v0[2], v1[2], v0[3], v1[3]}, p[0], p[1]);
+                else
+                    split8_h2(floatx4{v0[0], v1[0], v0[1], v1[1]}, floatx4{v0[2], v1[2], v0[3], v1[3]}, v_scale, p[0],
+                              p[1]);
                 const int vk = 2 * (c & 15), vd = 4 * (c >> 4);
                 const int pos = (vk & 16) | split_k_slot(vk & 15);  // even: the pair stays adjacent
                 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -381,8 +388,16 @@ VH_DEVICE void split4_h2(floatx4 v, float s, uint32_t &h01, uint32_t &h23, uint3
     m01 = m_pair_f16(v[0], v[1], s, h01);
     m23 = m_pair_f16(v[2], v[3], s, h23);
 }
+// The same for values already scaled (one: opaque_one()).
+VH_DEVICE void split4_h2_unit(floatx4 v, float one, uint32_t &h01, uint32_t &h23, uint32_t &m01, uint32_t &m23) {
+    h01 = pack_f16x2(v[0], v[1]);
+    h23 = pack_f16x2(v[2], v[3]);
+    m01 = m_pair_f16(v[0], v[1], one, h01);
+    m23 = m_pair_f16(v[2], v[3], one, h23);
+}
 
-template <typename TO>
+// KVS as attention_h2_kernel.
+template <typename TO, bool KVS = false>
 __global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) {
     constexpr int KEYS = 64;
     constexpr int PITCH = ATT_DH + 8;
@@ -413,6 +428,7 @@ __global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) 
     constexpr int EP = 13;  // probabilities <= 1: 2^13 < 2^14
     const float k_scale = ldexpf(1.0f, ek), v_scale = ldexpf(1.0f, ev), q_scale = qs * ldexpf(1.0f, eq);
     const float s_unscale = ldexpf(1.0f, -(ek + eq)), o_unscale = ldexpf(1.0f, -(ev + EP)), p_scale = ldexpf(1.0f, EP);
+    const float one = opaque_one();  // KVS: the unit scale of the m pieces
 
     floatx4 kpre[4], vpre[4], qpre[4];
     float gpre = 0.0f;
@@ -445,7 +461,8 @@ __global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) 
         for (int i = 0; i < 4; i++) {
             const int key = (tid >> 4) + 16 * i;
             uint32_t h01, h23, m01, m23;
-            split4_h2(rope4(kpre[i], a.rope, min(key, a.L - 1), d_st), k_scale, h01, h23, m01, m23);
+            if constexpr (KVS) split4_h2_unit(rope4(kpre[i], a.rope, min(key, a.L - 1), d_st), one, h01, h23, m01, m23);
+            else split4_h2(rope4(kpre[i], a.rope, min(key, a.L - 1), d_st), k_scale, h01, h23, m01, m23);
             *reinterpret_cast<u32x2 *>(&Kp[0][key][k_pos]) = u32x2{h01, h23};
             *reinterpret_cast<u32x2 *>(&Kp[1][key][k_pos]) = u32x2{m01, m23};
         }
@@ -454,8 +471,8 @@ __global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) 
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float x0 = vpre[2 * c][e], x1 = vpre[2 * c + 1][e];
-                const uint32_t hp = pack_f16x2(x0 * v_scale, x1 * v_scale);
-                const uint32_t mp = m_pair_f16(x0, x1, v_scale, hp);
+                const uint32_t hp = KVS ? pack_f16x2(x0, x1) : pack_f16x2(x0 * v_scale, x1 * v_scale);
+                const uint32_t mp = m_pair_f16(x0, x1, KVS ? one : v_scale, hp);
                 const int dim = vd + 32 * c + e;
                 *reinterpret_cast<uint32_t *>(&Vp[0][dim][v_pos]) = hp;
                 *reinterpret_cast<uint32_t *>(&Vp[1][dim][v_pos]) = mp;

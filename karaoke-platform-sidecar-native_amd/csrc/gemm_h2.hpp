@@ -59,6 +59,12 @@ struct GemmDescH2 {
     // residual epilogue (gemm_bf16_epilogue).
     float *zero_slot;
     float *amax;
+    // kv_inner > 0: C holds a fused q|k|v|gates projection with k in columns
+    // [kv_inner, 2 kv_inner) and v in [2 kv_inner, 3 kv_inner); those are
+    // written times 2^ek and 2^ev (att_h2_exponents of *kv_bound), the scales
+    // the fp16 two-piece attention would otherwise apply as it stages them
+    const float *kv_bound;
+    int kv_inner;
 };
 // Bound on |A|: *ptr when ptr is set (a device float), else value.
 struct H2Bound {
@@ -120,6 +126,18 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     for (int j = 0; j < 4; j++) {
         const int col = n0 + 32 * j + li;
         bpre[j] = d.bias && col < d.N ? d.bias[col] : 0.0f;
+    }
+    // each 32-column tile's extra power of two: ek for k columns, ev for v
+    // (kv_inner is a multiple of 32, so a tile is all q, k, v or gates)
+    int ekv[4] = {0, 0, 0, 0};
+    if (d.kv_inner > 0) {
+        int ek, eq, ev;
+        att_h2_exponents(*d.kv_bound, 1.0f, ek, eq, ev);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = n0 + 32 * j;
+            ekv[j] = c < d.kv_inner ? 0 : c < 2 * d.kv_inner ? ek : c < 3 * d.kv_inner ? ev : 0;
+        }
     }
 
     // A: 16 loads of 1 KB (16 rows each), wave w loads blocks w and w+8 from
@@ -227,9 +245,11 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     // is a normal float, and correctly rounded where it is not)
     const int eu = -(ea + ew);
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < 4; j++) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) acc[0][j][r] = ldexpf(acc[0][j][r], eu);
+        for (int r = 0; r < 16; r++) acc[0][j][r] = ldexpf(acc[0][j][r], eu + ekv[j]);
+        bpre[j] = ldexpf(bpre[j], ekv[j]);  // (acc + b) 2^e exactly, with the row norm too
+    }
     float rs[16];  // NORM: the scale of each accumulator row, applied with the bias
     if constexpr (NORM) {
         // lanes li and li + 32 summed the two halves of row wave*32 + li;

@@ -425,6 +425,7 @@ static bool gemm_h2_ok(const GemmArgsH2 &g, int epilogue) {
     if (g.row_norm && (g.a_h2 || !(epilogue == EPI_STORE || epilogue == EPI_GELU || epilogue == EPI_GEGLU)))
         return false;
     if (g.amax && epilogue != EPI_RESIDUAL) return false;
+    if (g.kv_inner && (g.kv_inner < 0 || g.kv_inner % 32 || !g.kv_bound || epilogue != EPI_STORE)) return false;
     return true;
 }
 
@@ -434,6 +435,7 @@ static GemmDescH2 to_desc_h2(const GemmArgsH2 &g) {
     d.M = (int)g.M; d.N = g.N; d.K = g.K;
     d.lda = g.lda; d.ldc = g.ldc;
     d.zero_slot = g.zero_slot; d.amax = g.amax;
+    d.kv_bound = g.kv_bound; d.kv_inner = g.kv_inner;
     return d;
 }
 
@@ -715,6 +717,13 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
                                (last_row + 1) * a.ld * 4 <= (int64_t)UINT32_MAX &&
                                (int64_t)a.pos_stride * a.ld * 4 < (1 << 24);
             auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, dim3(grid), block, 0, s, a); };
+            if (a.bound && a.kv_scaled) {  // fp16 two-piece products, k and v prescaled (fp32 out)
+                if (a.rope) off32 ? go(attention_h2_kernel<WAVES, float, true, true, true>)
+                                  : go(attention_h2_kernel<WAVES, float, true, false, true>);
+                else off32 ? go(attention_h2_kernel<WAVES, float, false, true, true>)
+                           : go(attention_h2_kernel<WAVES, float, false, false, true>);
+                return;
+            }
             if (a.bound) {  // fp16 two-piece products
                 if (a.rope) {
                     if (out_bf16) off32 ? go(attention_h2_kernel<WAVES, bf16, true, true>)
@@ -754,13 +763,17 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
 
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split, const float *bound,
-               bool out_h2) {
+               bool out_h2, bool kv_scaled) {
     if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
     }
     if (out_h2 && (out_bf16 || qkv_bf16 || !split || !bound || ((uintptr_t)out & 15))) {
         set_error("attention: h2 rows out need the fp16 two-piece kernels (fp32 qkv, a bound) and a 16-byte aligned out");
+        return false;
+    }
+    if (kv_scaled && (out_bf16 || qkv_bf16 || !split || !bound)) {
+        set_error("attention: prescaled k and v need the fp16 two-piece kernels (fp32 qkv and out, a bound)");
         return false;
     }
     AttnArgs a;
@@ -771,6 +784,7 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     a.inner = heads * ATT_DH; a.gate_col = gate_col; a.scale = 0.125f;
     a.bound = split && !qkv_bf16 ? bound : nullptr;
     a.out_h2 = out_h2 ? 1 : 0;
+    a.kv_scaled = kv_scaled ? 1 : 0;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
     if (lay.L <= 64 && !qkv_bf16) {
         // persistent: four workgroups per CU loop over the (sequence, head) tasks
@@ -779,6 +793,7 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
         const unsigned grid = (unsigned)std::min<int64_t>((int64_t)lay.S * heads, 4 * (int64_t)cus);
         if (a.bound) {  // fp16 two-piece products
             if (out_bf16) hipLaunchKernelGGL((attention_short_h2_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
+            else if (kv_scaled) hipLaunchKernelGGL((attention_short_h2_kernel<float, true>), dim3(grid), dim3(256), 0, s, a);
             else hipLaunchKernelGGL((attention_short_h2_kernel<float>), dim3(grid), dim3(256), 0, s, a);
         } else if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
         else hipLaunchKernelGGL((attention_short_kernel<float>), dim3(grid), dim3(256), 0, s, a);
@@ -944,9 +959,18 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
         xb->valid = false;  // until the FFN down-projection has raised the slot
         GemmArgsH2 gq{x, D, w.wqkvg_pg, w.bqkvg, qkvg, nq, tokens, nq, D};
         gq.row_norm = true;
+        // k and v written times the attention's piece scales, so its staging
+        // splits them without a multiply (the same bits: VOCALARC_KV_PRESCALE=0
+        // keeps them unscaled, to check that)
+        const char *kv_env = getenv("VOCALARC_KV_PRESCALE");
+        const bool kv_pre = att_h2 && inner % 32 == 0 && !(kv_env && kv_env[0] == '0');
+        if (kv_pre) {
+            gq.kv_bound = w.bounds + 1;
+            gq.kv_inner = inner;
+        }
         if (!gemm_h2(s, gq, OperandBound{xb->dev, 0.0f}, EPI_STORE, t, "gemm_qkv")) return false;
         if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, true,
-                       att_h2 ? w.bounds + 1 : nullptr, att_h2))
+                       att_h2 ? w.bounds + 1 : nullptr, att_h2, kv_pre))
             return false;
         if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, att_h2, "gemm_out"))
             return false;

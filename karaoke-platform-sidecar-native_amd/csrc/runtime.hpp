@@ -145,6 +145,11 @@ struct GemmArgsH2 {
     bool row_norm = false;
     float *zero_slot = nullptr;  // a device float the kernel sets to 0
     float *amax = nullptr;       // EPI_RESIDUAL: raised to max |C| written
+    // kv_inner > 0 (a multiple of 32): C is a fused q|k|v|gates projection
+    // whose k and v columns are written times 2^ek and 2^ev of the attention
+    // bound *kv_bound (GemmDescH2::kv_inner)
+    const float *kv_bound = nullptr;
+    int kv_inner = 0;
 };
 struct OperandBound {
     const float *dev = nullptr;
@@ -212,9 +217,11 @@ struct AttnLayout {
 // keeps the fp32 MFMA kernel).  rope: interleaved rotary
 // table of length lay.L (or null).  out_h2 (with `bound`): out written as h2
 // rows scaled by 2^h2_exponent(*bound), for a gemm_h2 with a_h2 and that bound.
+// kv_scaled (with `bound`, fp32 qkv and out): the k and v columns arrive
+// times 2^ek and 2^ev, as a gemm_h2 with kv_inner and that bound writes them.
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false,
-               bool split = false, const float *bound = nullptr, bool out_h2 = false);
+               bool split = false, const float *bound = nullptr, bool out_h2 = false, bool kv_scaled = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {

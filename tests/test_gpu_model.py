@@ -56,6 +56,29 @@ def test_transformer_block_config(cfg2_models, rng, axis, S, L):
     assert_close(ref, out, rtol=1e-4, atol=1e-4, min_snr=100, what="transformer (config)")
 
 
+@pytest.mark.parametrize("axis,S,L", [(0, 4, 62), (1, 3, 801), (1, 2, 97)])
+def test_transformer_block_kv_prescale_bit_identical(cfg2_models, rng, monkeypatch, axis, S, L):
+    """The fused block's QKV GEMM writes k and v times the attention's piece
+    scales (2^ek, 2^ev: one ldexp exponent per 32-column tile) and the
+    attention stages them unscaled; VOCALARC_KV_PRESCALE=0 keeps the
+    unscaled projection and the scaling multiplies in the attention.  Both
+    must give the same bits (powers of two commute with the rotation and the
+    splits), on both axes and on a ragged length."""
+    om, dm = cfg2_models
+    x = rng.standard_normal((S, L, om.d.dim), dtype=np.float32)
+    outs = []
+    for env in (None, "0"):
+        if env is None:
+            monkeypatch.delenv("VOCALARC_KV_PRESCALE", raising=False)
+        else:
+            monkeypatch.setenv("VOCALARC_KV_PRESCALE", env)
+        dx = to_dev(x)
+        dm.transformer(1, axis, dx, S, L)
+        outs.append(from_dev(dx))
+    monkeypatch.delenv("VOCALARC_KV_PRESCALE", raising=False)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("axis,S,L", [(0, 90, 23), (1, 23, 90)])
 def test_transformer_block_reference_shape(ref_models, rng, axis, S, L):
     om, dm = ref_models
