@@ -85,7 +85,9 @@ constexpr int H2_WBLOCK = 2 * GS_BN * GS_BK;  // fp16 per (row tile, K chunk) bl
 // activation.  So the normalised rows are never written: the RMSNorm pass and
 // its 2 x 4 bytes per element of traffic go, and A is the residual stream
 // itself, bounded by the max |x| its producer's epilogue recorded.
-template <int EPI, bool A_H2, int RING = 3, bool NORM = false>
+// KVS: the k and v columns scaled (GemmDescH2::kv_inner), compiled only into
+// the fused projection's instantiation.
+template <int EPI, bool A_H2, int RING = 3, bool NORM = false, bool KVS = false>
 __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound, int tile) {
     static_assert(!(NORM && A_H2), "the row norm needs the fp32 rows");
     constexpr int A_BYTES = GS_BM * GS_BK * 4;  // 16 KB: fp32 rows of 64 B
@@ -130,7 +132,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     // each 32-column tile's extra power of two: ek for k columns, ev for v
     // (kv_inner is a multiple of 32, so a tile is all q, k, v or gates)
     int ekv[4] = {0, 0, 0, 0};
-    if (d.kv_inner > 0) {
+    if (KVS && d.kv_inner > 0) {
         int ek, eq, ev;
         att_h2_exponents(*d.kv_bound, 1.0f, ek, eq, ev);
 #pragma unroll
@@ -287,9 +289,9 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
     }
 }
 
-template <int EPI, bool A_H2, bool NORM = false>
+template <int EPI, bool A_H2, bool NORM = false, bool KVS = false>
 __global__ __launch_bounds__(GS_THREADS, 2) void gemm_h2_kernel(GemmDescH2 d, H2Bound b) {
-    gemm_h2_body<EPI, A_H2, 3, NORM>(d, b.ptr ? *b.ptr : b.value, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
+    gemm_h2_body<EPI, A_H2, 3, NORM, KVS>(d, b.ptr ? *b.ptr : b.value, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
 // Ragged batch (the mask estimator's per-band linears): problem blockIdx.z,

@@ -425,7 +425,8 @@ static bool gemm_h2_ok(const GemmArgsH2 &g, int epilogue) {
     if (g.row_norm && (g.a_h2 || !(epilogue == EPI_STORE || epilogue == EPI_GELU || epilogue == EPI_GEGLU)))
         return false;
     if (g.amax && epilogue != EPI_RESIDUAL) return false;
-    if (g.kv_inner && (g.kv_inner < 0 || g.kv_inner % 32 || !g.kv_bound || epilogue != EPI_STORE)) return false;
+    if (g.kv_inner && (g.kv_inner < 0 || g.kv_inner % 32 || !g.kv_bound || epilogue != EPI_STORE || !g.row_norm))
+        return false;
     return true;
 }
 
@@ -443,6 +444,13 @@ template <int EPI>
 static void launch_h2(hipStream_t s, const GemmDescH2 &d, const H2Bound &b, unsigned tiles, const GemmArgsH2 &g) {
     if constexpr (EPI == EPI_STORE || EPI == EPI_GELU || EPI == EPI_GEGLU) {
         if (g.row_norm) {  // gemm_h2_ok: fp32 A
+            if constexpr (EPI == EPI_STORE) {
+                if (g.kv_inner) {  // the fused projection with k and v scaled
+                    hipLaunchKernelGGL((gemm_h2_kernel<EPI, false, true, true>), dim3(tiles), dim3(GS_THREADS), 0, s,
+                                       d, b);
+                    return;
+                }
+            }
             hipLaunchKernelGGL((gemm_h2_kernel<EPI, false, true>), dim3(tiles), dim3(GS_THREADS), 0, s, d, b);
             return;
         }

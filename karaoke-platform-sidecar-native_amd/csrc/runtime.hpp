@@ -145,9 +145,9 @@ struct GemmArgsH2 {
     bool row_norm = false;
     float *zero_slot = nullptr;  // a device float the kernel sets to 0
     float *amax = nullptr;       // EPI_RESIDUAL: raised to max |C| written
-    // kv_inner > 0 (a multiple of 32): C is a fused q|k|v|gates projection
-    // whose k and v columns are written times 2^ek and 2^ev of the attention
-    // bound *kv_bound (GemmDescH2::kv_inner)
+    // kv_inner > 0 (a multiple of 32; EPI_STORE with row_norm): C is a fused
+    // q|k|v|gates projection whose k and v columns are written times 2^ek and
+    // 2^ev of the attention bound *kv_bound (GemmDescH2::kv_inner)
     const float *kv_bound = nullptr;
     int kv_inner = 0;
 };
