@@ -47,7 +47,7 @@ ROLES = [
     (r"gemm_h2_kernel(<3, false|ILi3ELb0E)",
      "FFN down-projection + residual, raising the stream's bound (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via two-piece fp16)"),
-    (r"gemm_h2_kernel(<0, false, true>|ILi0ELb0ELb1E)",
+    (r"gemm_h2_kernel(<0, false, true[,>]|ILi0ELb0ELb1E)",
      "fused QKV + gate projection with the attention's pre-norm inside (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via two-piece fp16)"),
     (r"gemm_h2_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32 via two-piece fp16)"),

@@ -18,7 +18,7 @@ import sys
 from pathlib import Path
 
 COPY_BYTES = 496 * 801 * 801 * 4          # read once and written once by the copy
-GEMM_KERNEL = "gemm_h2_kernel<4, true, false>"  # GELU-GLU epilogue, A as h2 rows: the FFN up-projection
+GEMM_KERNEL = "gemm_h2_kernel<4, true, false, false>"  # GELU-GLU epilogue, A as h2 rows: the FFN up-projection
 COPY_KERNEL = "__amd_rocclr_copyBuffer"  # torch copy_ of a contiguous tensor is a runtime blit
 # A as h2 rows (the bytes of fp32), W as two fp16 planes, bias fp32, output fp32
 FF1_ALGORITHMIC = 397296 * 384 * 4 + 2 * 3072 * 384 * 2 + 3072 * 4 + 397296 * 1536 * 4
