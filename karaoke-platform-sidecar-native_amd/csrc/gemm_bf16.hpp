@@ -301,16 +301,6 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void gemm_bf16_batched_kernel(Ge
     gemm_bf16_body<EPI, TA, TC, BK, WM, WN, FM, FN>(b.d[blockIdx.z], (int)blockIdx.x);
 }
 
-// bf16-output epilogue of a wave's 64 x 64 block through LDS, for MFMAs that
-// take the B tile as their first operand: the accumulators then hold C
-// transposed -- lane (li, lh), register r of acc[i][j] is row 32 i + li,
-// column 32 j + 8 (r / 4) + 4 lh + r % 4 of the block -- so each lane has
-// four consecutive columns per register quad.  The lane writes each quad,
-// finished (bias, activation or GELU-GLU) and rounded, as 8 bytes into the
-// wave's own LDS block of 64 rows (`stage`, 64 x (OC + 8) bf16, OC the
-// block's output columns), then every lane stores 16 bytes of a row, so a
-// store instruction covers whole 64- or 128-byte row segments instead of
-// 2-byte scatters (bf16 QKV -7%, FFN up -9% against the per-element store).
 // The bias of columns c .. c+3 (c a multiple of 4), clamped to N (columns
 // past N are never stored): one 16-byte load where all four lie inside N and
 // the bias is 16-byte aligned.
@@ -341,6 +331,16 @@ VH_DEVICE void bias_quads_staged(const GemmDescBF16 &d, int col0, int lh, floatx
     }
 }
 
+// bf16-output epilogue of a wave's 64 x 64 block through LDS, for MFMAs that
+// take the B tile as their first operand: the accumulators then hold C
+// transposed -- lane (li, lh), register r of acc[i][j] is row 32 i + li,
+// column 32 j + 8 (r / 4) + 4 lh + r % 4 of the block -- so each lane has
+// four consecutive columns per register quad.  The lane writes each quad,
+// finished (bias, activation or GELU-GLU) and rounded, as 8 bytes into the
+// wave's own LDS block of 64 rows (`stage`, 64 x (OC + 8) bf16, OC the
+// block's output columns), then every lane stores 16 bytes of a row, so a
+// store instruction covers whole 64- or 128-byte row segments instead of
+// 2-byte scatters (bf16 QKV -7%, FFN up -9% against the per-element store).
 template <int EPI>
 VH_DEVICE void gemm_bf16_epilogue_staged(const GemmDescBF16 &d, const floatx16 (&acc)[2][2], bf16 *stage, int row0,
                                          int col0, int lane, const floatx4 (&bq)[8]) {
