@@ -210,6 +210,33 @@ def test_gemm_bf16_operand_alignment_checks(ctx):
                       ldc=(1 << 21) + 64)  # ldc <= 2^21 (32-bit row offsets)
 
 
+@pytest.mark.parametrize("epi", [0, 4])
+def test_gemm_bf16_unaligned_bias(ctx, rng, epi):
+    """A bias that is only 4-byte aligned: the bf16-output kernel loads its
+    bias quads element by element instead of by 16-byte loads, with the same
+    bits as an aligned copy of the bias."""
+    M, N, K = 600, 384, 96
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    wh, ld = _dev_bf16(ctx, w)
+    xh = torch.empty(M, K, dtype=torch.bfloat16, device="cuda:0")
+    ctx.to_bf16(to_dev(x), xh, M, K, K)
+    aligned = to_dev(bias)
+    holder = torch.zeros(N + 1, device="cuda:0")
+    holder[1:] = aligned
+    unaligned = holder[1:]
+    assert unaligned.data_ptr() % 16 == 4
+    cols = N // 2 if epi == native.EPI_GEGLU else N
+    outs = []
+    for b in (aligned, unaligned):
+        c = torch.zeros(M, cols, dtype=torch.bfloat16, device="cuda:0")
+        ctx.gemm_bf16(xh, wh, c, M, N, K, ld, bias=b, epilogue=epi, flags=native.BF16_A | native.BF16_C)
+        outs.append(c)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 def test_rmsnorm_bf16_is_rounded_fp32(ctx, rng):
     rows, dim = 1234, 384
     x = to_dev(rng.standard_normal((rows, dim), dtype=np.float32))

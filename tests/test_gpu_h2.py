@@ -341,6 +341,29 @@ def test_gemm_h2_residual_amax(ctx, rng):
                        row_norm=True)
 
 
+@pytest.mark.parametrize("epi", [native.EPI_STORE, native.EPI_RESIDUAL, native.EPI_GEGLU])
+def test_gemm_h2_padded_c(ctx, rng, epi):
+    """C with a row pitch wider than its columns (ldc = out + 24): full row
+    tiles store through a wave-uniform row pointer plus a lane offset, the
+    last (ragged) row tile per element; both must give the compact result's
+    bits in the first columns and leave the padding as it was."""
+    M, N, K = 700, 384, 128
+    out = N // 2 if epi == native.EPI_GEGLU else N
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    b = to_dev((0.1 * rng.standard_normal(N)).astype(np.float32))
+    planes = _pieces(ctx, w)
+    c0 = rng.standard_normal((M, out + 24)).astype(np.float32)
+    compact = to_dev(np.ascontiguousarray(c0[:, :out]))
+    padded = to_dev(c0)
+    dx = to_dev(x)
+    ctx.gemm_h2(dx, planes, compact, M, N, K, bias=b, epilogue=epi, a_bound=float(np.abs(x).max()))
+    ctx.gemm_h2(dx, planes, padded, M, N, K, bias=b, epilogue=epi, ldc=out + 24, a_bound=float(np.abs(x).max()))
+    got = from_dev(padded)
+    assert np.array_equal(got[:, :out].view(np.uint32), from_dev(compact).view(np.uint32))
+    assert np.array_equal(got[:, out:].view(np.uint32), c0[:, out:].view(np.uint32)), "padding columns were written"
+
+
 def test_gemm_h2_rejects_bad_shapes(ctx):
     x = torch.zeros(8, 24, device="cuda:0")
     pieces = torch.zeros(ctx.h2_bytes(8, 32) // 2, dtype=torch.float16, device="cuda:0")
