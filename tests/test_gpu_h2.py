@@ -341,12 +341,13 @@ def test_gemm_h2_residual_amax(ctx, rng):
                        row_norm=True)
 
 
-@pytest.mark.parametrize("epi", [native.EPI_STORE, native.EPI_RESIDUAL, native.EPI_GEGLU])
-def test_gemm_h2_padded_c(ctx, rng, epi):
+@pytest.mark.parametrize("epi_name", ["store", "residual", "geglu"])
+def test_gemm_h2_padded_c(ctx, rng, epi_name):
     """C with a row pitch wider than its columns (ldc = out + 24): full row
     tiles store through a wave-uniform row pointer plus a lane offset, the
     last (ragged) row tile per element; both must give the compact result's
     bits in the first columns and leave the padding as it was."""
+    epi = {"store": native.EPI_STORE, "residual": native.EPI_RESIDUAL, "geglu": native.EPI_GEGLU}[epi_name]
     M, N, K = 700, 384, 128
     out = N // 2 if epi == native.EPI_GEGLU else N
     x = rng.standard_normal((M, K)).astype(np.float32)
