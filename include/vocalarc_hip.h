@@ -181,10 +181,14 @@ int vh_attention(vh_context *ctx, int sequences, int length, int heads, const vo
    rotary table, the operand bound and its absmax partials -- lives in one
    fixed device array per GPU (1.05 MB, held until the process ends), so
    length is at most VH_NOALLOC_MAX_LENGTH (a longer one fails with an
-   error).  Every call on a GPU shares that array: calls that overlap on one
-   GPU (other threads, or other streams before this one's work has finished)
-   race.  Synchronises the stream when the table is copied (apply_rotary) and
-   when VH_ATT_H2 reads the bound back. */
+   error).  The rotary table is written there once, by vh_create; with
+   VH_ATT_H2 the bound is computed into the array and the kernels themselves
+   choose, on the device, between the two-piece products and those without
+   piece scales (vh_attention reads the bound back to choose), so the call
+   issues kernels only: no copy, no synchronisation, no allocation, and it
+   can be captured in a HIP graph and replayed.  Every call on a GPU shares
+   that array: calls that overlap on one GPU (other threads, or other
+   streams before this one's work has finished) race. */
 #define VH_NOALLOC_MAX_LENGTH 4096
 int vh_attention_noalloc(vh_context *ctx, int sequences, int length, int heads, const void *qkv, void *out,
                          int apply_rotary, int flags);
@@ -200,8 +204,11 @@ void vh_model_free(vh_model *model);
    VH_PRECISION_FP32 (default, the parity path): fp32 accuracy.  The
      transformer and mask-estimator linears run on fp16 matrix cores by
      two-piece operand splitting (vh_gemm_h2; pieces and operand bounds made
-     at load), the time-axis attention on bf16 matrix cores by three-piece
-     splitting, every other product on the fp32 MFMA instruction.
+     at load), and so does the attention on both axes (the two-piece
+     kernels of VH_ATT_H2, scaled from the fused projection's weight bound;
+     a layer whose bound lies outside their scale range runs its attention
+     on the kernels without piece scales); the band split runs on the fp32
+     MFMA instruction.
    VH_PRECISION_FP32_MFMA: every product on the fp32 MFMA instruction.
    VH_PRECISION_BF16: activations rounded to bf16 as they enter the matrix
      cores, bf16 weight copies made on the first switch, fp32 accumulation,

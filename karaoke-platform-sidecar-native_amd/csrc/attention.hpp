@@ -25,6 +25,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "h2.hpp"
 
 namespace vh {
 
@@ -48,12 +49,24 @@ struct AttnArgs {
     // (att_h2_exponents of *bound), as the fused projection writes them: the
     // staging splits them without scaling (the fp16 two-piece kernels only)
     int kv_scaled;
+    // Range choice on the device (null: none).  The kernel runs only when
+    // h2_attention_bound_ok(*guard) equals guard_h2 and otherwise returns at
+    // once: the two-piece kernel launched with guard_h2 = 1 and the kernel
+    // without piece scales with guard_h2 = 0 on the same bound compute the
+    // attention once between them, with no read-back of the bound.
+    const float *guard;
+    int guard_h2;
 };
 
 constexpr int ATT_DH = 64;
 constexpr int ATT_KB = 32;             // keys per iteration
 constexpr int ATT_KPITCH = ATT_DH + 4; // K tile row pitch (floats)
 constexpr int ATT_VPITCH = ATT_KB + 4; // V^T tile row pitch (floats)
+
+// Whether a guarded launch (AttnArgs::guard) has nothing to do.
+VH_DEVICE bool attn_guard_skip(const AttnArgs &a) {
+    return a.guard && h2_attention_bound_ok(*a.guard) != (a.guard_h2 != 0);
+}
 
 VH_DEVICE int attn_row(const AttnArgs &a, int s, int p) {
     return (s / a.group) * a.group_stride + (s % a.group) * a.seq_stride + p * a.pos_stride;
@@ -282,6 +295,7 @@ VH_DEVICE int short_sigma(int m) { return 4 * (m & 3) + (m >> 2); }
 
 template <typename TO>
 __global__ __launch_bounds__(256, 4) void attention_short_kernel(AttnArgs a) {
+    if (attn_guard_skip(a)) return;
     constexpr int PITCH = ATT_DH + 4;
     constexpr int KEYS = 64;
     __shared__ __attribute__((aligned(16))) float Ks[KEYS][PITCH];

@@ -33,6 +33,7 @@ namespace vh {
 // pieces are the same bits.
 template <int WAVES, typename TO, bool ROPE, bool OFF32, bool KVS = false>
 __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a) {
+    if (attn_guard_skip(a)) return;
     constexpr int NT = 64 * WAVES;
     constexpr int CHUNKS = ATT_KB * ATT_DH / 8;  // 8-element chunks per K (or V) tile: 256
     constexpr int PER_T = CHUNKS / NT;
@@ -399,6 +400,7 @@ VH_DEVICE void split4_h2_unit(floatx4 v, float one, uint32_t &h01, uint32_t &h23
 // KVS as attention_h2_kernel.
 template <typename TO, bool KVS = false>
 __global__ __launch_bounds__(256, 4) void attention_short_h2_kernel(AttnArgs a) {
+    if (attn_guard_skip(a)) return;
     constexpr int KEYS = 64;
     constexpr int PITCH = ATT_DH + 8;
     __shared__ __attribute__((aligned(16))) _Float16 Kp[2][KEYS][PITCH];

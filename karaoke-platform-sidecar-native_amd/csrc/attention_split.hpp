@@ -29,6 +29,7 @@ namespace vh {
 // 24-bit multiply-add from a per-lane byte offset and the SGPR base.
 template <int WAVES, typename TO, bool ROPE, bool OFF32>
 __global__ __launch_bounds__(64 * WAVES, 2) void attention_split_kernel(AttnArgs a) {
+    if (attn_guard_skip(a)) return;
     constexpr int NT = 64 * WAVES;
     constexpr int CHUNKS = ATT_KB * ATT_DH / 8;  // 8-element chunks per K (or V) tile: 256
     constexpr int PER_T = CHUNKS / NT;

@@ -220,17 +220,10 @@ __global__ __launch_bounds__(GS_THREADS, 2) void gemm_split_kernel(GemmDescSplit
     gemm_split_body<EPI>(d, xcd_swizzle((int)blockIdx.x, (int)gridDim.x));
 }
 
-// Ragged batch (the mask estimator's per-band linears): problem blockIdx.z,
-// descriptors in the kernel arguments; blocks past a problem's tiles return.
+// Problems per launch of the ragged batched GEMMs (the mask estimator's
+// per-band linears): descriptors in the kernel arguments, problem blockIdx.z,
+// blocks past a problem's tiles return.
 constexpr int GS_MAX_BATCH = 64;
-struct GemmBatchSplit {
-    GemmDescSplit d[GS_MAX_BATCH];
-};
-
-template <int EPI>
-__global__ __launch_bounds__(GS_THREADS, 2) void gemm_split_batched_kernel(GemmBatchSplit b) {
-    gemm_split_body<EPI>(b.d[blockIdx.z], (int)blockIdx.x);
-}
 
 // fp32 W [N][ldw_in] (K a multiple of 16) -> its h, m, l pieces, tile-major:
 // element (n, k) of piece p at

@@ -40,7 +40,7 @@ VH_HOST_DEVICE inline int h2_exponent(float bound) {
 // split for long sequences, the fp32 MFMA kernel for short ones).
 constexpr float H2_ATT_BOUND_MIN = 0x1p-40f;
 constexpr float H2_ATT_BOUND_MAX = 0x1p60f;
-inline bool h2_attention_bound_ok(float b) { return b >= H2_ATT_BOUND_MIN && b <= H2_ATT_BOUND_MAX; }
+VH_HOST_DEVICE inline bool h2_attention_bound_ok(float b) { return b >= H2_ATT_BOUND_MIN && b <= H2_ATT_BOUND_MAX; }
 
 // The fp16 two-piece attention's exponents for a bound B on |q|, |k|, |v|
 // (before rotation): k and q (times the softmax scale and log2 e, qs) from
@@ -61,12 +61,16 @@ VH_DEVICE uint32_t pack_f16x2(float a, float b) {
 }
 
 // The m pieces of two values x0 s, x1 s whose h pieces hp holds (as
-// pack_f16x2 made them): fp16(x s - h).  x s - h is formed exactly inside one
-// v_fma_mix_f32 per value (the fp16 h read in place, no conversion) and the
-// pair rounded by one v_cvt_pk_f16_f32: the bits of fp16(y - h), y = x s, in
-// 3 VALU per pair instead of 5.  s must not be a compile-time 1 (the
-// multiply-add would fold back into a conversion and a subtraction): pass
-// opaque_one() for unscaled values.
+// pack_f16x2 made them): x s - h formed inside one v_fma_mix_f32 per value
+// (the fp16 h read in place, no conversion, one rounding) and the pair
+// rounded to fp16 by one v_cvt_pk_f16_f32, 3 VALU per pair instead of 5.
+// For a power-of-two s, x s is exact, so these are the bits of fp16(y - h),
+// y = x s (the weights, the GEMM's A, k and v).  For any other s (the
+// attention's q times its softmax scale) h + m is the split of the exact
+// product x s, which can differ in m's last bits from splitting the rounded
+// fp32 product (and is at least as accurate).  s must not be a compile-time
+// 1 (the multiply-add would fold back into a conversion and a subtraction):
+// pass opaque_one() for unscaled values.
 VH_DEVICE uint32_t m_pair_f16(float x0, float x1, float s, uint32_t hp) {
     typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
     const halfx2 h = __builtin_bit_cast(halfx2, hp);

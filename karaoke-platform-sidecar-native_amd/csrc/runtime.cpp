@@ -367,43 +367,6 @@ bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer
     return sync_debug(s, "gemm_split_kernel");
 }
 
-template <int EPI>
-static void launch_split_batched(hipStream_t s, const GemmBatchSplit &b, unsigned tiles, unsigned n) {
-    hipLaunchKernelGGL(gemm_split_batched_kernel<EPI>, dim3(tiles, 1, n), dim3(GS_THREADS), 0, s, b);
-}
-
-bool gemm_split_batched(hipStream_t s, const std::vector<GemmArgsSplit> &gs, int epilogue, KernelTimer *t,
-                        const char *name) {
-    Scope sc(t, s, name);
-    for (size_t first = 0; first < gs.size(); first += GS_MAX_BATCH) {
-        const size_t count = std::min(gs.size() - first, (size_t)GS_MAX_BATCH);
-        GemmBatchSplit b;
-        memset(&b, 0, sizeof(b));
-        int64_t max_tiles = 0;
-        for (size_t i = 0; i < count; i++) {
-            const GemmArgsSplit &g = gs[first + i];
-            if (!gemm_split_ok(g, epilogue)) {
-                set_error("gemm_split_batched: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K,
-                          g.lda);
-                return false;
-            }
-            b.d[i] = to_desc_split(g);
-            max_tiles = std::max(max_tiles, ((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
-        }
-        const unsigned tiles = (unsigned)max_tiles, n = (unsigned)count;
-        switch (epilogue) {
-            case EPI_STORE: launch_split_batched<EPI_STORE>(s, b, tiles, n); break;
-            case EPI_GELU: launch_split_batched<EPI_GELU>(s, b, tiles, n); break;
-            case EPI_TANH: launch_split_batched<EPI_TANH>(s, b, tiles, n); break;
-            case EPI_RESIDUAL: launch_split_batched<EPI_RESIDUAL>(s, b, tiles, n); break;
-            case EPI_GEGLU: launch_split_batched<EPI_GEGLU>(s, b, tiles, n); break;
-            default: set_error("unknown GEMM epilogue %d", epilogue); return false;
-        }
-        if (!sync_debug(s, "gemm_split_batched_kernel")) return false;
-    }
-    return true;
-}
-
 bool split_weights(hipStream_t s, const float *W, int N, int K, int ldw, void *pieces) {
     if (N <= 0 || K <= 0 || K % GS_BK || ldw < K || split_bytes(N, K) / 6 > (size_t)INT32_MAX) {
         set_error("split_weights: bad shape N=%d K=%d ldw=%d (K a multiple of 16)", N, K, ldw);
@@ -466,6 +429,12 @@ bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int 
                   g.K, g.lda, epilogue, g.row_norm ? " row norm" : "", g.amax ? " amax" : "");
         return false;
     }
+    // every workgroup reads the bound as it starts, while tile 0 zeroes
+    // zero_slot and the epilogues raise amax: neither may be the bound
+    if (bound.dev && (g.zero_slot == bound.dev || g.amax == bound.dev)) {
+        set_error("gemm_h2: zero_slot and amax must not alias the A bound");
+        return false;
+    }
     const GemmDescH2 d = to_desc_h2(g);
     const H2Bound b{bound.dev, bound.value};
     const unsigned tiles = (unsigned)(((g.M + GS_BM - 1) / GS_BM) * ((g.N + GS_BN - 1) / GS_BN));
@@ -500,6 +469,12 @@ bool gemm_h2_batched(hipStream_t s, const std::vector<GemmArgsH2> &gs, const Ope
             if (!gemm_h2_ok(g, epilogue)) {
                 set_error("gemm_h2_batched: unsupported shape M=%lld N=%d K=%d lda=%d", (long long)g.M, g.N, g.K,
                           g.lda);
+                return false;
+            }
+            // the batched kernel splits fp32 A and has none of the single
+            // GEMM's modes
+            if (g.row_norm || g.a_h2 || g.kv_inner || g.zero_slot || g.amax) {
+                set_error("gemm_h2_batched: row_norm, a_h2, kv_inner, zero_slot and amax are not supported");
                 return false;
             }
             b.d[i] = to_desc_h2(g);
@@ -771,7 +746,7 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
 
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split, const float *bound,
-               bool out_h2, bool kv_scaled) {
+               bool out_h2, bool kv_scaled, bool device_choice) {
     if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
@@ -784,6 +759,11 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
         set_error("attention: prescaled k and v need the fp16 two-piece kernels (fp32 qkv and out, a bound)");
         return false;
     }
+    if (device_choice && (qkv_bf16 || !split || !bound || out_h2 || kv_scaled)) {
+        set_error("attention: the device-side range choice needs fp32 qkv, split and a bound, without h2 or "
+                  "prescaled operands");
+        return false;
+    }
     AttnArgs a;
     a.qkv = qkv; a.ld = ld; a.out = out; a.ld_out = ld_out;
     a.rope = rope;
@@ -793,23 +773,44 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     a.bound = split && !qkv_bf16 ? bound : nullptr;
     a.out_h2 = out_h2 ? 1 : 0;
     a.kv_scaled = kv_scaled ? 1 : 0;
+    a.guard = nullptr;
+    a.guard_h2 = 0;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
-    if (lay.L <= 64 && !qkv_bf16) {
-        // persistent: four workgroups per CU loop over the (sequence, head) tasks
-        static int cus = 0;
-        if (cus == 0 && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
-        const unsigned grid = (unsigned)std::min<int64_t>((int64_t)lay.S * heads, 4 * (int64_t)cus);
-        if (a.bound) {  // fp16 two-piece products
-            if (out_bf16) hipLaunchKernelGGL((attention_short_h2_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
-            else if (kv_scaled) hipLaunchKernelGGL((attention_short_h2_kernel<float, true>), dim3(grid), dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((attention_short_h2_kernel<float>), dim3(grid), dim3(256), 0, s, a);
-        } else if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((attention_short_kernel<float>), dim3(grid), dim3(256), 0, s, a);
-    } else if (lay.L <= 64)
-        launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16,
-                            split && !qkv_bf16);
-    else launch_attention<4>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 127) / 128)), out_bf16, qkv_bf16,
-                             split && !qkv_bf16);
+    auto launch = [&](const AttnArgs &a) {
+        if (lay.L <= 64 && !qkv_bf16) {
+            // persistent: four workgroups per CU loop over the (sequence, head) tasks
+            static int cus = 0;
+            if (cus == 0 && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess)
+                cus = 256;
+            const unsigned grid = (unsigned)std::min<int64_t>((int64_t)lay.S * heads, 4 * (int64_t)cus);
+            if (a.bound) {  // fp16 two-piece products
+                if (out_bf16) hipLaunchKernelGGL((attention_short_h2_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
+                else if (kv_scaled)
+                    hipLaunchKernelGGL((attention_short_h2_kernel<float, true>), dim3(grid), dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((attention_short_h2_kernel<float>), dim3(grid), dim3(256), 0, s, a);
+            } else if (out_bf16) hipLaunchKernelGGL((attention_short_kernel<bf16>), dim3(grid), dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((attention_short_kernel<float>), dim3(grid), dim3(256), 0, s, a);
+        } else if (lay.L <= 64)
+            launch_attention<2>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 63) / 64)), out_bf16, qkv_bf16,
+                                split && !qkv_bf16);
+        else launch_attention<4>(s, a, (unsigned)((int64_t)lay.S * heads * ((lay.L + 127) / 128)), out_bf16, qkv_bf16,
+                                 split && !qkv_bf16);
+    };
+    if (device_choice) {
+        // the two-piece kernel when the bound is in range, else the kernel
+        // without piece scales (three-piece bf16 for L > 64, fp32 MFMA below)
+        AttnArgs in = a, out_of = a;
+        in.guard = bound;
+        in.guard_h2 = 1;
+        out_of.bound = nullptr;
+        out_of.guard = bound;
+        out_of.guard_h2 = 0;
+        launch(in);
+        if (!sync_debug(s, "attention_kernel (bound in range)")) return false;
+        launch(out_of);
+    } else {
+        launch(a);
+    }
     return sync_debug(s, "attention_kernel");
 }
 
@@ -843,8 +844,8 @@ bool Dims::valid(char *why, size_t n) const {
 // ------------------------------------------------------------------ rotary
 void rope_table_host(int length, int dim_head, float *cos_t, float *sin_t, float *interleaved) {
     const int pairs = dim_head / 2;
-    float freq[512];
-    for (int i = 0; i < pairs && i < 512; i++) freq[i] = 1.0f / powf(10000.0f, (float)(2 * i) / (float)dim_head);
+    std::vector<float> freq(pairs > 0 ? pairs : 0);
+    for (int i = 0; i < pairs; i++) freq[i] = 1.0f / powf(10000.0f, (float)(2 * i) / (float)dim_head);
     for (int p = 0; p < length; p++)
         for (int k = 0; k < pairs; k++) {
             const float angle = (float)p * freq[k];

@@ -117,9 +117,6 @@ struct GemmArgsSplit {
 };
 bool gemm_split(hipStream_t s, const GemmArgsSplit &g, int epilogue, KernelTimer *t = nullptr,
                 const char *name = "gemm_split");
-// A ragged batch of split GEMMs (one launch per 64 problems).
-bool gemm_split_batched(hipStream_t s, const std::vector<GemmArgsSplit> &gs, int epilogue, KernelTimer *t = nullptr,
-                        const char *name = "gemm_split");
 // K granularity of gemm_split, and the bytes of W's pieces (N rounded up to
 // a multiple of 128).
 constexpr int SPLIT_K_MULTIPLE = 16;
@@ -219,9 +216,15 @@ struct AttnLayout {
 // rows scaled by 2^h2_exponent(*bound), for a gemm_h2 with a_h2 and that bound.
 // kv_scaled (with `bound`, fp32 qkv and out): the k and v columns arrive
 // times 2^ek and 2^ev, as a gemm_h2 with kv_inner and that bound writes them.
+// device_choice (with split and `bound`, neither out_h2 nor kv_scaled): the
+// bound may lie outside the two-piece kernels' scale range and is not read
+// back -- the two-piece kernel and the kernel without piece scales are both
+// launched, each returning at once unless the bound's range selects it
+// (AttnArgs::guard), so the call never synchronises.
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false,
-               bool split = false, const float *bound = nullptr, bool out_h2 = false, bool kv_scaled = false);
+               bool split = false, const float *bound = nullptr, bool out_h2 = false, bool kv_scaled = false,
+               bool device_choice = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {
@@ -280,17 +283,13 @@ int bounds_usable(hipStream_t s, const float *dev, int n, float *host = nullptr)
 // bf16 operands with fp32 accumulation (separately reported variant).
 enum Precision : int { PREC_FP32 = 0, PREC_BF16 = 1, PREC_FP32_MFMA = 2 };
 
-// Rotary cos/sin tables per sequence length, built on the host with the
-// reference's float expressions (native/vocalarc_separation.c:726-731,1312).
-// Rotary tables per sequence length, built on the host with the reference's
-// float expressions (native/vocalarc_separation.c:726-731): cos[L][Dh/2],
-// sin[L][Dh/2] and the same values interleaved as (cos, sin) pairs
-// [L][Dh/2][2], so one 16-byte load gives what four rotated dims need.
 // The rotary tables of positions 0..length-1 with base 10000, built on the
 // host with the reference's float expressions (native/vocalarc_separation.c:
-// 726-731) so they are bit-exact: cos_t/sin_t [length][dim_head/2] and
-// interleaved [length][dim_head/2][cos, sin]; null outputs are skipped.
-// dim_head <= 1024.
+// 726-731,1312) so they are bit-exact: cos_t/sin_t [length][dim_head/2] and
+// the same values interleaved as (cos, sin) pairs [length][dim_head/2][2], so
+// one 16-byte load gives what four rotated dims need; null outputs are
+// skipped.  An entry depends only on its position and pair, so the table of
+// a length is a prefix of every longer one's.
 void rope_table_host(int length, int dim_head, float *cos_t, float *sin_t, float *interleaved);
 
 struct RopeCache {

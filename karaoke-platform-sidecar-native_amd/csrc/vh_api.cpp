@@ -73,21 +73,22 @@ struct vh_model {
 // ------------------------------------------------- no-allocation scratch
 // Device scratch of vh_attention_noalloc: float 0 the operand bound,
 // [64, 64 + ABSMAX_PARTIALS) the absmax partials, then the interleaved rotary
-// table of up to VH_NOALLOC_MAX_LENGTH positions (1.05 MB in all).  Each
-// device holds its own copy for the life of the process.  Host code never
-// uses the array's name as an address: noalloc_scratch[device] holds the
-// device address from hipGetSymbolAddress, resolved by vh_create with the
-// device current.
+// table of VH_NOALLOC_MAX_LENGTH positions (1.05 MB in all).  Each device
+// holds its own copy for the life of the process.  Host code never uses the
+// array's name as an address: noalloc_scratch[device] holds the device
+// address from hipGetSymbolAddress, resolved by vh_create with the device
+// current, which also writes the rotary table there once: an entry depends
+// only on its position and pair, so every length's table is its prefix.
 constexpr size_t NOALLOC_ROPE_OFFSET = 64 + ABSMAX_PARTIALS;
 constexpr size_t NOALLOC_FLOATS = NOALLOC_ROPE_OFFSET + (size_t)VH_NOALLOC_MAX_LENGTH * 64;
 static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
 
 constexpr int NOALLOC_MAX_DEVICES = 64;
-static std::mutex noalloc_mutex;  // guards noalloc_scratch and noalloc_rope_host
+static std::mutex noalloc_mutex;  // guards noalloc_scratch
 static float *noalloc_scratch[NOALLOC_MAX_DEVICES] = {};
-static float noalloc_rope_host[(size_t)VH_NOALLOC_MAX_LENGTH * 64];
 
-// With `device` current: its scratch address (once per device).
+// With `device` current: its scratch address and rotary table (once per
+// device).
 static bool resolve_noalloc_scratch(int device) {
     if (device < 0 || device >= NOALLOC_MAX_DEVICES) {
         set_error("no-allocation scratch: device %d beyond %d", device, NOALLOC_MAX_DEVICES);
@@ -101,6 +102,12 @@ static bool resolve_noalloc_scratch(int device) {
         set_error("hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
         return false;
     }
+    std::vector<float> rope((size_t)VH_NOALLOC_MAX_LENGTH * 64);
+    rope_table_host(VH_NOALLOC_MAX_LENGTH, 64, nullptr, nullptr, rope.data());
+    if (!check(hipMemcpy(static_cast<float *>(p) + NOALLOC_ROPE_OFFSET, rope.data(), rope.size() * sizeof(float),
+                         hipMemcpyHostToDevice),
+               "hipMemcpy(no-allocation rotary table)"))
+        return false;
     noalloc_scratch[device] = static_cast<float *>(p);
     return true;
 }
@@ -336,32 +343,22 @@ extern "C" int vh_attention_noalloc(vh_context *ctx, int sequences, int length, 
         set_error("vh_attention_noalloc: scratch of device %d not resolved", ctx->device);
         return 0;
     }
-    const float *rt = nullptr;
-    if (apply_rotary) {
-        // the same host-built table as vh_attention's, copied into the scratch
-        std::lock_guard<std::mutex> lock(noalloc_mutex);
-        rope_table_host(length, 64, nullptr, nullptr, noalloc_rope_host);
-        if (!check(hipMemcpyAsync(scr + NOALLOC_ROPE_OFFSET, noalloc_rope_host, (size_t)length * 64 * sizeof(float),
-                                  hipMemcpyHostToDevice, ctx->stream),
-                   "hipMemcpy(rotary table)") ||
-            !check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(rotary table)"))
-            return 0;
-        rt = scr + NOALLOC_ROPE_OFFSET;
-    }
+    // the table vh_create wrote (bit for bit vh_attention's, whose length-L
+    // table is a prefix of it); no copy and no synchronisation here
+    const float *rt = apply_rotary ? scr + NOALLOC_ROPE_OFFSET : nullptr;
     const int inner = heads * 64;
     const bool h2 = (flags & VH_ATT_H2) && !(flags & VH_ATT_BF16);
-    bool h2_ok = false;
-    if (h2) {  // as vh_attention: the operands' own maximum, every partial written before it is read
+    if (h2) {
+        // as vh_attention: the operands' own maximum bounds them (every
+        // partial written before it is read); the kernels choose between the
+        // two-piece products and those without piece scales on the device
         if (!absmax(ctx->stream, static_cast<const float *>(qkv), (int64_t)sequences * length * 3 * inner, scr + 64,
                     scr))
             return 0;
-        float b = 0.0f;
-        if (bounds_usable(ctx->stream, scr, 1, &b) < 0) return 0;
-        h2_ok = h2_attention_bound_ok(b);
     }
     return attention(ctx->stream, qkv, 3 * inner, out, inner, rt, contiguous_layout(sequences, length), heads, -1,
                      nullptr, (flags & VH_ATT_OUT_BF16) != 0, (flags & VH_ATT_BF16) != 0,
-                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2_ok ? scr : nullptr)
+                     (flags & (VH_ATT_SPLIT | VH_ATT_H2)) != 0, h2 ? scr : nullptr, false, false, h2)
                ? 1
                : 0;
 }

@@ -64,8 +64,6 @@ ROLES = [
     (r"gemm_split_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via split bf16)"),
-    (r"gemm_split_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32 via split bf16)"),
-    (r"gemm_split_batched_kernel(<|ILi)0", "mask estimator layer 2, batched over bands (fp32 via split bf16)"),
     (r"split_weight_kernel", "weight split into bf16 pieces (model load)"),
     (r"gemm_f32_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32)"),
     (r"gemm_f32_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32)"),
@@ -154,17 +152,26 @@ def kernels(run_dir: str, jsonl: str, out: str, command: str) -> int:
     return 0
 
 
+XCDS = 8              # GRBM_GUI_ACTIVE is summed over the XCDs
+SIMDS_PER_SE = 32     # SQ_CYCLES is summed over the 32 shader engines, 32 SIMDs each
+PEAK_CLOCK_GHZ = 2.4  # the clock of the published dense MFMA peaks
+
+
 def counters(regex: str, out: str, command: str, *dirs: str) -> int:
     pat = re.compile(regex)
     vals: dict[str, list[float]] = {}
     names = set()
-    for d in dirs:
+    per_dispatch: dict[tuple[int, str], dict[str, float]] = {}
+    for i, d in enumerate(dirs):
         path = next(Path(d).rglob("*counter_collection.csv"))
         for r in csv.DictReader(open(path)):
             if not pat.search(r["Kernel_Name"]):
                 continue
             names.add(r["Kernel_Name"])
             vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+            rec = per_dispatch.setdefault((i, r["Dispatch_Id"]), {})
+            rec["ns"] = float(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+            rec[r["Counter_Name"]] = float(r["Counter_Value"])
     avg = {k: sum(v) / len(v) for k, v in vals.items()}
     lines = [f"# rocprofv3 counters of `{regex}`", "", "Commands (repository root, MI355X box; one pass per counter "
              "group):", "", "```", command.strip(), "```", "",
@@ -173,6 +180,27 @@ def counters(regex: str, out: str, command: str, *dirs: str) -> int:
              "| counter | value |", "|---|---:|"]
     for k in sorted(avg):
         lines.append(f"| `{k}` | {avg[k]:.4g} |")
+    # dispatches of the pass that read the clock and the matrix-core busy
+    # cycles: the clock each ran at (GRBM_GUI_ACTIVE per XCD over its
+    # duration), the matrix cores' busy share of the SIMD cycles, and their
+    # product with clock / peak clock -- the fraction of the dense MFMA peak
+    keys = ("GRBM_GUI_ACTIVE", "SQ_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES")
+    rows = [(k, v) for k, v in sorted(per_dispatch.items(), key=lambda kv: (kv[0][0], int(kv[0][1])))
+            if all(c in v for c in keys) and v["ns"] > 0]
+    if rows:
+        lines += ["", "Per dispatch (the pass with the clock and busy counters): clock = `GRBM_GUI_ACTIVE` / "
+                  f"{XCDS} XCDs / duration; busy = `SQ_VALU_MFMA_BUSY_CYCLES` / (`SQ_CYCLES` x {SIMDS_PER_SE}); "
+                  f"fraction of the MFMA peak = busy x clock / {PEAK_CLOCK_GHZ} GHz. Durations are the profiled "
+                  "dispatches' own (serialised, with pauses between them, so the clock ramps up over the first "
+                  "ones).", "",
+                  "| dispatch | ms | cycles per XCD | clock GHz | matrix cores busy | fraction of peak |",
+                  "|---:|---:|---:|---:|---:|---:|"]
+        for (_, did), v in rows:
+            cyc = v["GRBM_GUI_ACTIVE"] / XCDS
+            clk = cyc / v["ns"]
+            busy = v["SQ_VALU_MFMA_BUSY_CYCLES"] / (v["SQ_CYCLES"] * SIMDS_PER_SE)
+            lines.append(f"| {did} | {v['ns'] / 1e6:.3f} | {cyc:.4g} | {clk:.3f} | {busy:.3f} | "
+                         f"{busy * clk / PEAK_CLOCK_GHZ:.3f} |")
     Path(out).write_text("\n".join(lines) + "\n")
     print("\n".join(lines))
     return 0

@@ -169,6 +169,10 @@ class Context:
     def sync(self):
         _ok(lib().vh_synchronize(self.h), "vh_synchronize")
 
+    def set_stream(self, stream: int):
+        """Issue the context's work on the HIP stream handle `stream` (0: the null stream)."""
+        _ok(lib().vh_set_stream(self.h, stream), "vh_set_stream")
+
     # -- isolated kernels (device pointers) --
     def rmsnorm(self, x, gamma, y, rows: int, dim: int):
         _ok(lib().vh_rmsnorm(self.h, rows, dim, ptr(x), ptr(gamma), ptr(y)), "vh_rmsnorm")

@@ -7,10 +7,14 @@ C2  one axial layer on [801 frames, 62 bands, 384]: the time transformer
 C3  the DSP front and back end on 60 s of audio (hop 441, T = 6001):
     STFT, masked iSTFT, band split and mask estimator;
 C4  the depth-12 model: one whole 8 s window (fp32 and the bf16 variant),
-    and a 3-window chunked separation (8 s windows, 6 s step, zero-padded
-    tail) against the oracle's window forwards composed with the closed-form
-    cross-fade (the composition is pinned to the oracle's chunked separation
-    on the CPU, test_oracle_math.py).
+    a 3-window chunked separation (8 s windows, 6 s step, zero-padded tail),
+    and the benchmark's own launch shape -- a 50 s mix cut into 8 windows
+    that go through the device in ONE pass (time axis 496 sequences of 801,
+    band axis 6408 sequences of 62, 397,296 tokens per GEMM), one window
+    of digital silence among them -- each against the oracle's window
+    forwards composed with the closed-form cross-fade (the composition is
+    pinned to the oracle's chunked separation on the CPU,
+    test_oracle_math.py).
 C0  (the 10 s host path) runs in test_gpu_abi.py.
 
 Bars: fp32 waveforms per-sample max |delta| <= 1e-4 and SNR >= 80 dB; the
@@ -221,3 +225,51 @@ def test_c4_chunked_three_windows_depth12(c4, precision):
         _wave_bar(ref, out, "C4 chunked 3 windows, depth 12, fp32")
     else:
         _wave_bar(ref, out, "C4 chunked 3 windows, depth 12, bf16 variant", max_abs=np.inf, min_snr=40.0)
+
+
+@pytest.fixture(scope="module")
+def c4_pass(ctx):
+    """The benchmark's launch shape: a 50 s mix = 8 windows of 8 s every 6 s
+    (7 * 6 + 8 = 50, no padding), all 8 in one device pass; samples 18-26 s
+    are digital silence, so window 3 is all zeros (its band inputs take the
+    RMSNorm's epsilon path, native/vocalarc_separation.c:419-424, and its
+    features are the band-split biases alone) and windows 2 and 4 are
+    partly silent.  The oracle's forward of each window (depth 12)."""
+    d = CONFIG_DIMS
+    blob = pack.synthetic_pack(d, 406)
+    x = audio.sine_mix(50.0, 407)
+    x[:, 18 * RATE:26 * RATE] = 0.0
+    length = x.shape[1]
+    count = O.chunk_count(length, CHUNK, STEP)
+    assert count == 8 and (count - 1) * STEP + CHUNK == length
+    om = O.Model(d, blob)
+    outs = [om.forward(np.ascontiguousarray(x[:, k * STEP:k * STEP + CHUNK])) for k in range(count)]
+    assert not np.any(x[:, 3 * STEP:3 * STEP + CHUNK]) and np.all(np.isfinite(outs[3]))
+    dm = native.Model(ctx, d, blob)
+    yield d, dm, x, outs
+    dm.set_precision(native.PRECISION_FP32)
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_c4_eight_windows_one_pass_depth12(c4_pass, precision):
+    d, dm, x, outs = c4_pass
+    length = x.shape[1]
+    ref = compose_windows(outs, length, CHUNK, STEP)
+    dm.set_precision(native.PRECISION_FP32 if precision == "fp32" else native.PRECISION_BF16)
+    dx = to_dev(x)
+    dv, di = empty_dev(x.shape), empty_dev(x.shape)
+    dm.separate(dx, length, CHUNK, STEP, 8, dv, di)
+    out = from_dev(dv)
+    dm.set_precision(native.PRECISION_FP32)
+    assert np.array_equal(from_dev(di), x - out)
+    silent = slice(3 * STEP, 3 * STEP + CHUNK)
+    if precision == "fp32":
+        _wave_bar(ref, out, "C4 8 windows in one pass, depth 12, fp32")
+        # the silent window's span: the mix is zero there, so vocals come
+        # only from the edge frames of the overlapping windows 2 and 4
+        err = float(np.max(np.abs(out[:, silent].astype(np.float64) - ref[:, silent])))
+        print(f"silent span: max|ref| {float(np.max(np.abs(ref[:, silent]))):.3e}, max|d| {err:.3e}")
+        assert err <= 1e-4
+    else:
+        _wave_bar(ref, out, "C4 8 windows in one pass, depth 12, bf16 variant", max_abs=np.inf, min_snr=40.0)

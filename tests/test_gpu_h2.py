@@ -339,6 +339,14 @@ def test_gemm_h2_residual_amax(ctx, rng):
     with pytest.raises(native.NativeError):
         ctx.gemm_h2_ex(to_dev(x), planes, empty_dev((M, N)), M, N, K, dbound, epilogue=native.EPI_RESIDUAL,
                        row_norm=True)
+    # every workgroup reads the bound while tile 0 zeroes zero_slot and the
+    # epilogues raise amax: neither may be the bound itself (host-side check,
+    # nothing launched)
+    with pytest.raises(native.NativeError, match="alias"):
+        ctx.gemm_h2_ex(to_dev(x), planes, to_dev(c0), M, N, K, dbound, epilogue=native.EPI_RESIDUAL, amax=dbound)
+    with pytest.raises(native.NativeError, match="alias"):
+        ctx.gemm_h2_ex(to_dev(x), planes, empty_dev((M, N)), M, N, K, dbound, epilogue=native.EPI_STORE,
+                       zero_slot=dbound)
 
 
 @pytest.mark.parametrize("epi_name", ["store", "residual", "geglu"])
@@ -458,3 +466,4 @@ def test_rmsnorm_h2_rows_and_gemm(ctx, rng):
     assert torch.equal(c_rows, c_fp32)
     with pytest.raises(native.NativeError, match="bound"):
         ctx.gemm_h2(yh, planes, c_rows, rows, N, D, a_rows=True)  # rows need the bound they were split with
+
