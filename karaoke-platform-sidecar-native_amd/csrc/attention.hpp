@@ -56,6 +56,9 @@ struct AttnArgs {
     // attention once between them, with no read-back of the bound.
     const float *guard;
     int guard_h2;
+    // k and v arrive as the fused projection's fp16 pieces
+    // (GemmDescH2::kv_pieces; attention_h2_kvp_kernel)
+    int kv_pieces;
 };
 
 constexpr int ATT_DH = 64;
@@ -74,15 +77,22 @@ VH_DEVICE int attn_row(const AttnArgs &a, int s, int p) {
 
 // Rotate the two interleaved pairs of a float4 by t = (cos, sin) of each
 // pair; rope4_table reads t for the float4 at dimension d0 of position pos
-// from the table (one 16-byte load).
+// from the table (one 16-byte load).  Explicit fused forms, the same in every
+// kernel that rotates and symmetric in the pair: element e of a pair is
+// fma(x_e, cos, x_other * (e ? sin : -sin)) (the reference's
+// first*c - second*s, first*s + second*c, native/vocalarc_separation.c:
+// 705-706, with the product of the element itself fused), so a lane holding
+// one element and its partner's (rope_own) rounds as a lane holding both.
+VH_DEVICE float rope_own(float own, float other, float c, float s_signed) {
+    return __builtin_fmaf(own, c, other * s_signed);
+}
 VH_DEVICE floatx4 rope_pairs(floatx4 v, floatx4 t) {
     const float c0 = t[0], s0 = t[1], c1 = t[2], s1 = t[3];
     floatx4 r;
-    // explicit fused forms: the same rounding in every kernel that rotates
-    r[0] = __builtin_fmaf(v[0], c0, -(v[1] * s0));
-    r[1] = __builtin_fmaf(v[0], s0, v[1] * c0);
-    r[2] = __builtin_fmaf(v[2], c1, -(v[3] * s1));
-    r[3] = __builtin_fmaf(v[2], s1, v[3] * c1);
+    r[0] = rope_own(v[0], v[1], c0, -s0);
+    r[1] = rope_own(v[1], v[0], c0, s0);
+    r[2] = rope_own(v[2], v[3], c1, -s1);
+    r[3] = rope_own(v[3], v[2], c1, s1);
     return r;
 }
 VH_DEVICE floatx4 rope4_table(floatx4 v, const float *tab, int pos, int d0) {

@@ -363,6 +363,284 @@ __global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kernel(AttnArgs a)
         }
 }
 
+// attention_h2_kernel on k and v that the fused projection has already
+// written as fp16 pieces (GemmDescH2::kv_pieces: k rotated, both scaled by
+// their attention exponents; per head 256 bytes of the row's k and v regions,
+// 64 h then 64 m halves).  Nothing is computed while staging: a 32-key block
+// of K (or V) is 8 KB -- two pieces of 32 rows of 128 bytes -- copied global
+// -> LDS by eight 1 KB global_load_lds_dwordx4 (two per wave), with no
+// registers in between.  The 16-byte chunks of an LDS row are XOR-swizzled by
+// its key so the reads below touch distinct banks: K chunk c of key r at
+// slot c ^ ((r >> 1) & 7) (the QK^T operand reads: 16 lanes = 16 keys, one
+// chunk), V chunk c at c ^ (4 ((r >> 1) & 1)).  V stays key-major: the PV
+// product's V^T operand (32 dims x 8 keys per lane) comes from
+// ds_read_b64_tr_b16, which hands each lane of a 16-lane group one column of
+// the 4 x 16 block (4 keys x 16 dims) the group addresses -- two reads per
+// piece give the 8 keys of a lane's operand in the probabilities' key order.
+// The key blocks' pipeline, softmax and output are those of
+// attention_h2_kernel (same bits); only the time axis with 32-bit staging
+// offsets takes this path (OFF32).
+constexpr int KVP_ROW = 128;                 // bytes of one piece of one key (64 halves)
+constexpr int KVP_PIECE = ATT_KB * KVP_ROW;  // 4 KB: one piece of a 32-key block
+VH_DEVICE int kvp_swz_k(int r) { return (r >> 1) & 7; }
+VH_DEVICE int kvp_swz_v(int r) { return 4 * ((r >> 1) & 1); }
+
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 3) void attention_h2_kvp_kernel(AttnArgs a) {
+    static_assert(WAVES == 4, "two DMA loads per wave and operand");
+    __shared__ __attribute__((aligned(1024))) unsigned char Ks[2][2][KVP_PIECE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vs[2][2][KVP_PIECE];
+
+    const float *qkv = static_cast<const float *>(a.qkv);
+    const int qgroups = (a.L + 32 * WAVES - 1) / (32 * WAVES);
+    const int task = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);  // neighbouring tasks share K/V rows: same XCD
+    const int qg = task % qgroups;
+    const int sh = task / qgroups;
+    const int h = sh % a.H;
+    const int s = sh / a.H;
+
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int li = lane & 31, lh = lane >> 5;
+    const int q0 = (qg * WAVES + wave) * 32;
+
+    const float qs = a.scale * 1.4426950408889634f;
+    const float bnd = *a.bound;
+    int ek, eq, ev;
+    att_h2_exponents(bnd, qs, ek, eq, ev);
+    constexpr int EP = 5;
+    const float s_unscale = ldexpf(1.0f, -(ek + eq)), o_unscale = ldexpf(1.0f, -ev);
+
+    halfx8 qh[4], qm[4];
+    {
+        const int q = min(q0 + li, a.L - 1);
+        const float *qp = qkv + (size_t)attn_row(a, s, q) * a.ld + h * ATT_DH;
+        const float q_scale = qs * ldexpf(1.0f, eq);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int d0 = 16 * g + 8 * lh;
+            floatx4 lo = ld4(qp + d0), hi = ld4(qp + d0 + 4);
+            lo = rope4_table(lo, a.rope, q, d0);
+            hi = rope4_table(hi, a.rope, q, d0 + 4);
+            split8_h2(lo, hi, q_scale, qh[g], qm[g]);
+        }
+    }
+
+    // DMA staging.  Load i (0..7) of a block copies piece i / 4, keys
+    // 8 (i % 4) .. +7 of the block: lane l writes LDS bytes 16 l of the 1 KB,
+    // i.e. key 8 (i % 4) + l / 8, slot l % 8, and reads that key's chunk
+    // (l % 8) ^ swz from global memory.  Wave w issues loads w and w + 4 of K
+    // and of V.  Keys past L load the row of key L-1 (their scores are masked,
+    // their probabilities exactly 0).  32-bit offsets from the sequence's
+    // first row (the launcher checks they fit).
+    const char *seq_base = reinterpret_cast<const char *>(qkv) + (size_t)attn_row(a, s, 0) * a.ld * 4u;
+    const uint32_t pos_bytes = (uint32_t)a.pos_stride * (uint32_t)a.ld * 4u;
+    const int kr = 8 * (wave & 3) + (lane >> 3);  // the lane's key within the block (both of its loads)
+    const uint32_t k_off = 4u * (uint32_t)a.inner + 256u * (uint32_t)h + 16u * (uint32_t)((lane & 7) ^ kvp_swz_k(kr));
+    const uint32_t v_off = 8u * (uint32_t)a.inner + 256u * (uint32_t)h + 16u * (uint32_t)((lane & 7) ^ kvp_swz_v(kr));
+    const uint32_t ks_base = (uint32_t)(uintptr_t)&Ks[0][0][0], vs_base = (uint32_t)(uintptr_t)&Vs[0][0][0];
+    auto issue_k = [&](int kb) {
+        const uint32_t row = (uint32_t)min(kb * ATT_KB + kr, a.L - 1) * pos_bytes;
+#pragma unroll
+        for (int p = 0; p < 2; p++)
+            lds_dma16s(row + k_off + KVP_ROW * p, seq_base,
+                       ks_base + (uint32_t)(((kb & 1) * 2 + p) * KVP_PIECE + 1024 * (wave & 3)));
+    };
+    auto issue_v = [&](int kb) {
+        const uint32_t row = (uint32_t)min(kb * ATT_KB + kr, a.L - 1) * pos_bytes;
+#pragma unroll
+        for (int p = 0; p < 2; p++)
+            lds_dma16s(row + v_off + KVP_ROW * p, seq_base,
+                       vs_base + (uint32_t)(((kb & 1) * 2 + p) * KVP_PIECE + 1024 * (wave & 3)));
+    };
+
+    // S^T block from Ks[kbuf], still scaled by 2^(ek+eq)
+    auto qk = [&](int kbuf) {
+        floatx16 sc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[r] = 0.0f;
+        const unsigned char *kb0 = &Ks[kbuf][0][0] + li * KVP_ROW;
+        halfx8 kp[2][2];
+        auto read = [&](int g, halfx8 (&k)[2]) {
+            const int slot = (2 * g + lh) ^ kvp_swz_k(li);
+#pragma unroll
+            for (int p = 0; p < 2; p++) k[p] = *reinterpret_cast<const halfx8 *>(kb0 + p * KVP_PIECE + 16 * slot);
+        };
+        read(0, kp[0]);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            if (g < 3) read(g + 1, kp[(g + 1) & 1]);
+            const halfx8 &kh = kp[g & 1][0], &km = kp[g & 1][1];
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(km, qh[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qm[g], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[g], sc, 0, 0, 0);
+        }
+        return sc;
+    };
+
+    floatx16 o[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[t][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    auto soft_max = [&](floatx16 &sc, int kb) {
+        const int valid = a.L - kb * ATT_KB;
+        if (valid < ATT_KB) {
+            const int vl = valid - 4 * lh;
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                if (8 * (r >> 2) + (r & 3) >= vl) sc[r] = -INFINITY;
+        }
+        float mb = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) mb = fmaxf(mb, sc[r]);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
+            mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * s_unscale;
+        }
+        const bool grow = mb > m_run + 8.0f;
+        if (__ballot(grow)) {
+            const float m_new = grow ? mb : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+            o[0] *= alpha;
+            o[1] *= alpha;
+            m_run = m_new;
+        }
+    };
+    // V^T operand rows: lane (group g = lane / 16, j = lane % 16) addresses
+    // key 4 lh + j / 4 (+ 8 for the second read) of the step's 16 keys, dims
+    // 16 (g % 2) + 4 (j % 4) .. +3 of the 32 of tile t
+    typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+    const int tr_j = lane & 15, tr_dhalf = (lane >> 4) & 1;
+    auto soft_pv = [&](floatx16 &sc, int vbuf) {
+        float ls = 0.0f;
+        const float c = (float)EP - m_run;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], s_unscale, c));
+            ls += sc[r];
+        }
+        l_run += ls;
+        halfx8 pp[2][2];
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+            split8_h2_unit(floatx4{sc[8 * st], sc[8 * st + 1], sc[8 * st + 2], sc[8 * st + 3]},
+                           floatx4{sc[8 * st + 4], sc[8 * st + 5], sc[8 * st + 6], sc[8 * st + 7]}, pp[st][0],
+                           pp[st][1]);
+        halfx8 vp[2][2];
+        auto read = [&](int step, halfx8 (&v)[2]) {
+            const int st = step >> 1, t = step & 1;
+            const int key = 16 * st + 4 * lh + (tr_j >> 2);
+            const int chunk = 4 * t + 2 * tr_dhalf + ((tr_j & 3) >> 1);
+            const int byte = 8 * (tr_j & 1);
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const unsigned char *base = &Vs[vbuf][p][0];
+                const unsigned char *a0 = base + key * KVP_ROW + 16 * (chunk ^ kvp_swz_v(key)) + byte;
+                const unsigned char *a1 = base + (key + 8) * KVP_ROW + 16 * (chunk ^ kvp_swz_v(key + 8)) + byte;
+                const fp16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (__attribute__((address_space(3))) fp16x4 *)(a0));
+                const fp16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (__attribute__((address_space(3))) fp16x4 *)(a1));
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const u32x2 w0 = __builtin_bit_cast(u32x2, r0), w1 = __builtin_bit_cast(u32x2, r1);
+                v[p] = __builtin_bit_cast(halfx8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+            }
+        };
+        read(0, vp[0]);
+#pragma unroll
+        for (int step = 0; step < 4; step++) {
+            if (step < 3) read(step + 1, vp[(step + 1) & 1]);
+            const int st = step >> 1, t = step & 1;
+            const halfx8(&v)[2] = vp[step & 1];
+            const halfx8 &ph = pp[st][0], &pm = pp[st][1];
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v[1], ph, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v[0], pm, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v[0], ph, o[t], 0, 0, 0);
+        }
+    };
+
+    // Pipeline as attention_h2_kernel: entering iteration kb, Ks[(kb+1)%2]
+    // holds K(kb+1) and Vs[kb%2] holds V(kb); the iteration issues K(kb+2)
+    // into Ks[kb%2] (read last by block kb's scores, before the barrier that
+    // ended the previous iteration) and V(kb+1) into Vs[(kb+1)%2], computes
+    // block kb+1's scores and block kb's P V, and waits for its copies before
+    // the barrier that ends it.
+    const int nkb = (a.L + ATT_KB - 1) / ATT_KB;
+    issue_k(0);
+    issue_v(0);
+    issue_k(1);
+    wait_vmcnt<0>();
+    __syncthreads();
+    auto run = [&](auto active_c) {
+        constexpr bool ACTIVE = decltype(active_c)::value;
+        floatx16 s0, s1;
+        if constexpr (ACTIVE) {
+            s0 = qk(0);
+            soft_max(s0, 0);
+        }
+        __syncthreads();  // every wave has read K(0): iteration 0 copies K(2) there
+        auto iteration = [&](int kb, floatx16 &sc, floatx16 &sn) {
+            issue_k(kb + 2);
+            issue_v(kb + 1);
+            if constexpr (ACTIVE) {
+                sn = qk((kb + 1) & 1);
+                soft_pv(sc, kb & 1);
+            }
+            wait_vmcnt<0>();
+            __syncthreads();
+            if constexpr (ACTIVE) {
+                if (kb + 1 < nkb) soft_max(sn, kb + 1);
+            }
+        };
+        for (int kb = 0; kb < nkb; kb += 2) {
+            iteration(kb, s0, s1);
+            if (kb + 1 < nkb) iteration(kb + 1, s1, s0);
+        }
+    };
+    if (q0 < a.L) run(std::true_type());
+    else {
+        run(std::false_type());
+        return;
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const int q = q0 + li;
+    if (q >= a.L) return;
+    const float inv = (1.0f / l_tot) * o_unscale;
+    const int row = attn_row(a, s, q);
+    const float gate = a.gate_col >= 0 ? sigmoid_dev(qkv[(size_t)row * a.ld + a.gate_col + h]) : 1.0f;
+    float *op = static_cast<float *>(a.out) + (size_t)row * a.ld_out + h * ATT_DH;
+    if (a.out_h2) {
+        const float so = ldexpf(1.0f, h2_exponent(bnd));
+        unsigned char *rowp = reinterpret_cast<unsigned char *>(op);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            floatx4 lo, hi;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                lo[r] = (o[c >> 1][8 * (c & 1) + r] * inv) * gate;
+                hi[r] = (o[c >> 1][8 * (c & 1) + 4 + r] * inv) * gate;
+            }
+            store8_h2_half(rowp + 64 * c, lh, lo, hi, so);
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            floatx4 v;
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = (o[t][4 * rq + r] * inv) * gate;
+            st4(op + 32 * t + 8 * rq + 4 * lh, v);
+        }
+}
+
 // Short sequences (L <= 64: the band axis) in fp32 accuracy on the fp16
 // matrix cores: the persistent task loop, prefetch, query layout and
 // single-pass softmax of attention_short_kernel (attention.hpp), with every

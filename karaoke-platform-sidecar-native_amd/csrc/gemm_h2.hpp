@@ -42,6 +42,7 @@
 // and split.
 #pragma once
 
+#include "attention.hpp"
 #include "gemm_split.hpp"
 #include "h2.hpp"
 
@@ -65,7 +66,125 @@ struct GemmDescH2 {
     // the fp16 two-piece attention would otherwise apply as it stages them
     const float *kv_bound;
     int kv_inner;
+    // kv_pieces (with kv_inner): k, rotated, and v are written as the fp16
+    // pieces of those scaled values (kv_pieces_epilogue), the rotary position
+    // of row r being the frame (r / rope_period) % rope_len of rows ordered
+    // [chunk][frame][band] (rope_period bands per frame), its (cos, sin) at
+    // rope[(frame * 32 + pair) * 2]
+    int kv_pieces;
+    const float *rope;
+    int rope_period, rope_len;
 };
+
+// The fused projection's k or v column tile (32 x 128 per wave, n0 inside
+// [kv_inner, 3 kv_inner)) written as fp16 pieces instead of fp32: the head's
+// 64 columns of a row occupy its 256 bytes of the region -- 64 h halves, then
+// 64 m halves, dim order -- where h + m is the value y scaled by 2^ek (2^ev),
+// h = fp16(y), m = fp16(y - h) (exact difference): the pieces the two-piece
+// attention's staging forms, so the attention copies them into LDS as they
+// are.  k is rotated first (rope_own: each lane swaps its value with the
+// lane of the pair's other dimension), by the (cos, sin) of the row's frame;
+// a wave's 32 consecutive rows span at most two frames.  pre(r) is the fp32
+// value the plain epilogue would store for register r.
+template <typename PRE>
+VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li, int lh, PRE pre) {
+    const bool is_k = n0 < 2 * d.kv_inner;
+    const int region = is_k ? d.kv_inner : 2 * d.kv_inner;  // first column of the k (v) region
+    const int B = d.rope_period, T = d.rope_len;
+    const int f0 = (row0 / B) % T;
+    const int f1 = f0 + 1 == T ? 0 : f0 + 1;
+    const int off_b = B - row0 % B;  // first row (within the wave's 32) of frame f1
+    const bool even = (li & 1) == 0;
+    typedef __attribute__((address_space(1))) char gchar;
+    typedef __attribute__((address_space(1))) uint16_t gu16;
+    const uint32_t pitch = (uint32_t)d.ldc * 4u;
+    const gchar *const rbase = (const gchar *)(reinterpret_cast<char *>(d.C) + (size_t)row0 * (size_t)pitch);
+    // one straight-line body per (k or v, whole or ragged row tile, frame
+    // boundary inside the wave's rows or not)
+    auto body = [&](auto k_c, auto full_c, auto split_c) {
+        constexpr bool IS_K = decltype(k_c)::value, FULL = decltype(full_c)::value;
+        constexpr bool SPLIT = decltype(split_c)::value;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            // one column tile at a time: nothing of the next is hoisted into
+            // this one (the registers the K loop needs bound the epilogue's)
+            __builtin_amdgcn_sched_barrier(0);
+            const int kc = n0 + 32 * j + li - region;
+            const uint32_t off_h = 4u * (uint32_t)region + 256u * (uint32_t)(kc >> 6) + 2u * (uint32_t)(kc & 63) +
+                                   (uint32_t)(4 * lh) * pitch;
+            float c0 = 1.0f, s0 = 0.0f, c1 = 1.0f, s1 = 0.0f;
+            if constexpr (IS_K) {
+                const int pr = (kc & 63) >> 1;
+                const float *t0 = d.rope + 2 * (f0 * 32 + pr);
+                c0 = t0[0];
+                s0 = even ? -t0[1] : t0[1];
+                if constexpr (SPLIT) {
+                    const float *t1 = d.rope + 2 * (f1 * 32 + pr);
+                    c1 = t1[0];
+                    s1 = even ? -t1[1] : t1[1];
+                }
+            }
+            // rows in pairs (registers r, r + 1: consecutive rows of one
+            // column): one v_cvt_pk_f16_f32 makes both h, one v_fma_mix_f32
+            // per value and one v_cvt_pk_f16_f32 both m (m_pair_f16); the
+            // halves leave by 2-byte stores of each half of the packed dwords
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                float y[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    y[e] = pre(j, r + e);
+                    if constexpr (IS_K) {
+                        const float other =
+                            __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[e]), 0xB1, 0xF, 0xF, false));
+                        bool nxt = false;
+                        if constexpr (SPLIT) nxt = 8 * ((r + e) >> 2) + 4 * lh + ((r + e) & 3) >= off_b;
+                        y[e] = rope_own(y[e], other, nxt ? c1 : c0, nxt ? s1 : s0);
+                    }
+                }
+                const uint32_t hp = pack_f16x2(y[0], y[1]);
+                const uint32_t mp = m_pair_f16(y[0], y[1], opaque_one(), hp);
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint16_t hb = (uint16_t)(hp >> (16 * e)), mb = (uint16_t)(mp >> (16 * e));
+                    const int rr = 8 * ((r + e) >> 2) + ((r + e) & 3);  // the row of register r + e, less 4 lh
+                    if constexpr (FULL) {
+                        // wave-uniform row pointer (SGPRs) + the lane's 32-bit
+                        // offset; the high halves by the d16_hi form of the
+                        // same store, which the compiler would otherwise
+                        // address with a 64-bit VGPR pair per store
+                        const gchar *rp = rbase + (uint32_t)rr * pitch;
+                        asm("" : "+s"(rp));
+                        if (e == 0) {
+                            __builtin_nontemporal_store(hb, (gu16 *)(rp + off_h));
+                            __builtin_nontemporal_store(mb, (gu16 *)(rp + off_h + 128u));
+                        } else {
+                            asm volatile("global_store_short_d16_hi %0, %1, %2 nt\n\t"
+                                         "global_store_short_d16_hi %0, %3, %2 offset:128 nt"
+                                         :
+                                         : "v"(off_h), "v"(hp), "s"(rp), "v"(mp)
+                                         : "memory");
+                        }
+                    } else if (row0 + rr + 4 * lh < d.M) {
+                        char *rp = reinterpret_cast<char *>(d.C) + (size_t)(row0 + rr) * pitch + off_h;
+                        __builtin_nontemporal_store(hb, reinterpret_cast<uint16_t *>(rp));
+                        __builtin_nontemporal_store(mb, reinterpret_cast<uint16_t *>(rp + 128));
+                    }
+                }
+            }
+        }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    if (row0 + 32 <= d.M) {
+        if (!is_k) body(F_(), T_(), F_());
+        else if (off_b >= 32) body(T_(), T_(), F_());
+        else body(T_(), T_(), T_());
+    } else {
+        if (!is_k) body(F_(), F_(), F_());
+        else body(T_(), F_(), T_());
+    }
+}
 // Bound on |A|: *ptr when ptr is set (a device float), else value.
 struct H2Bound {
     const float *ptr;
@@ -86,7 +205,8 @@ constexpr int H2_WBLOCK = 2 * GS_BN * GS_BK;  // fp16 per (row tile, K chunk) bl
 // its 2 x 4 bytes per element of traffic go, and A is the residual stream
 // itself, bounded by the max |x| its producer's epilogue recorded.
 // KVS: the k and v columns scaled (GemmDescH2::kv_inner), compiled only into
-// the fused projection's instantiation.
+// the fused projection's instantiations, and with kv_pieces written as their
+// fp16 pieces (k rotated).
 template <int EPI, bool A_H2, int RING = 3, bool NORM = false, bool KVS = false>
 __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound, int tile) {
     static_assert(!(NORM && A_H2), "the row norm needs the fp32 rows");
@@ -265,6 +385,16 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
             const floatx4 r4 = *reinterpret_cast<const floatx4 *>(&rscale[wave][8 * q + 4 * lh]);
 #pragma unroll
             for (int e = 0; e < 4; e++) rs[4 * q + e] = r4[e];
+        }
+    }
+    if constexpr (KVS && NORM && EPI == EPI_STORE) {
+        if (d.kv_pieces && n0 >= d.kv_inner && n0 < 3 * d.kv_inner) {
+            // the plain epilogue's value of each element (bias and row norm in
+            // one fused multiply-add), formed in place first so the row
+            // scales and biases are dead before the rotation and the split
+            kv_pieces_epilogue(d, m0 + wave * 32, n0, li, lh,
+                               [&](int j, int r) { return fmaf(acc[0][j][r], rs[r], bpre[j]); });
+            return;
         }
     }
     GemmDescBF16 e{};

@@ -390,6 +390,9 @@ static bool gemm_h2_ok(const GemmArgsH2 &g, int epilogue) {
     if (g.amax && epilogue != EPI_RESIDUAL) return false;
     if (g.kv_inner && (g.kv_inner < 0 || g.kv_inner % 32 || !g.kv_bound || epilogue != EPI_STORE || !g.row_norm))
         return false;
+    if (g.kv_pieces && (!g.kv_inner || g.kv_inner % 128 || !g.rope || g.rope_period <= 0 || g.rope_len <= 0 ||
+                        3 * g.kv_inner > g.N))
+        return false;
     return true;
 }
 
@@ -400,6 +403,8 @@ static GemmDescH2 to_desc_h2(const GemmArgsH2 &g) {
     d.lda = g.lda; d.ldc = g.ldc;
     d.zero_slot = g.zero_slot; d.amax = g.amax;
     d.kv_bound = g.kv_bound; d.kv_inner = g.kv_inner;
+    d.kv_pieces = g.kv_pieces ? 1 : 0;
+    d.rope = g.rope; d.rope_period = g.rope_period; d.rope_len = g.rope_len;
     return d;
 }
 
@@ -700,6 +705,10 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
                                (last_row + 1) * a.ld * 4 <= (int64_t)UINT32_MAX &&
                                (int64_t)a.pos_stride * a.ld * 4 < (1 << 24);
             auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, dim3(grid), block, 0, s, a); };
+            if (a.kv_pieces) {  // attention() checked off32
+                go(attention_h2_kvp_kernel<WAVES>);
+                return;
+            }
             if (a.bound && a.kv_scaled) {  // fp16 two-piece products, k and v prescaled (fp32 out)
                 if (a.rope) off32 ? go(attention_h2_kernel<WAVES, float, true, true, true>)
                                   : go(attention_h2_kernel<WAVES, float, true, false, true>);
@@ -746,7 +755,7 @@ static void launch_attention(hipStream_t s, const AttnArgs &a, unsigned grid, bo
 
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t, bool out_bf16, bool qkv_bf16, bool split, const float *bound,
-               bool out_h2, bool kv_scaled, bool device_choice) {
+               bool out_h2, bool kv_scaled, bool device_choice, bool kv_pieces) {
     if (lay.S <= 0 || lay.L <= 0 || ld % (qkv_bf16 ? 8 : 4) || ld_out % 4 || ((uintptr_t)qkv & 15)) {
         set_error("attention: bad shape S=%d L=%d ld=%d", lay.S, lay.L, ld);
         return false;
@@ -758,6 +767,19 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     if (kv_scaled && (out_bf16 || qkv_bf16 || !split || !bound)) {
         set_error("attention: prescaled k and v need the fp16 two-piece kernels (fp32 qkv and out, a bound)");
         return false;
+    }
+    if (kv_pieces) {
+        // the DMA staging's 32-bit offsets from a sequence's first row
+        const int64_t last_row = (int64_t)((lay.S - 1) / lay.group) * lay.group_stride +
+                                 (int64_t)(std::min(lay.S, lay.group) - 1) * lay.seq_stride +
+                                 (int64_t)(lay.L - 1) * lay.pos_stride;
+        const bool off32 = lay.group_stride >= 0 && lay.seq_stride >= 0 && lay.pos_stride >= 0 &&
+                           (last_row + 1) * ld * 4 <= (int64_t)UINT32_MAX;
+        if (!kv_scaled || lay.L <= 64 || !rope || heads * ATT_DH % 128 || device_choice || out_bf16 || !off32) {
+            set_error("attention: k/v pieces need the prescaled two-piece kernel, L > 64, fp32 out, the rotary "
+                      "table and 32-bit staging offsets");
+            return false;
+        }
     }
     if (device_choice && (qkv_bf16 || !split || !bound || out_h2 || kv_scaled)) {
         set_error("attention: the device-side range choice needs fp32 qkv, split and a bound, without h2 or "
@@ -775,6 +797,7 @@ bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, co
     a.kv_scaled = kv_scaled ? 1 : 0;
     a.guard = nullptr;
     a.guard_h2 = 0;
+    a.kv_pieces = kv_pieces ? 1 : 0;
     Scope sc(t, s, lay.L > 64 ? "attention_long" : "attention_short");
     auto launch = [&](const AttnArgs &a) {
         if (lay.L <= 64 && !qkv_bf16) {
@@ -977,9 +1000,24 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
             gq.kv_bound = w.bounds + 1;
             gq.kv_inner = inner;
         }
+        // On the time axis of the [chunk][frame][band] token order, k (rotated)
+        // and v leave the QKV GEMM as the attention's fp16 pieces, which it
+        // copies into LDS without computing (attention_h2_kvp_kernel): the
+        // rotation and the split happen once per element instead of once per
+        // query group.  VOCALARC_KV_PIECES=0 keeps them fp32 (the same bits).
+        const char *kvp_env = getenv("VOCALARC_KV_PIECES");
+        const bool kv_pieces = kv_pre && lay.L > 64 && inner % 128 == 0 && lay.seq_stride == 1 &&
+                               lay.pos_stride == lay.group && lay.group_stride == lay.group * lay.L &&
+                               !(kvp_env && kvp_env[0] == '0');
+        if (kv_pieces) {
+            gq.kv_pieces = true;
+            gq.rope = rt;
+            gq.rope_period = lay.group;
+            gq.rope_len = lay.L;
+        }
         if (!gemm_h2(s, gq, OperandBound{xb->dev, 0.0f}, EPI_STORE, t, "gemm_qkv")) return false;
         if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, true,
-                       att_h2 ? w.bounds + 1 : nullptr, att_h2, kv_pre))
+                       att_h2 ? w.bounds + 1 : nullptr, att_h2, kv_pre, false, kv_pieces))
             return false;
         if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, att_h2, "gemm_out"))
             return false;

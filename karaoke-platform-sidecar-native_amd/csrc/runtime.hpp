@@ -147,6 +147,12 @@ struct GemmArgsH2 {
     // 2^ev of the attention bound *kv_bound (GemmDescH2::kv_inner)
     const float *kv_bound = nullptr;
     int kv_inner = 0;
+    // with kv_inner (a multiple of 128): k (rotated by the interleaved table
+    // rope of rope_len positions, row r at frame (r / rope_period) % rope_len)
+    // and v written as fp16 pieces for attention(kv_pieces) (GemmDescH2)
+    bool kv_pieces = false;
+    const float *rope = nullptr;
+    int rope_period = 0, rope_len = 0;
 };
 struct OperandBound {
     const float *dev = nullptr;
@@ -221,10 +227,12 @@ struct AttnLayout {
 // back -- the two-piece kernel and the kernel without piece scales are both
 // launched, each returning at once unless the bound's range selects it
 // (AttnArgs::guard), so the call never synchronises.
+// kv_pieces (with kv_scaled, L > 64): k and v arrive as the fp16 pieces a
+// gemm_h2 with kv_pieces writes (k rotated; rope must be the table it used).
 bool attention(hipStream_t s, const void *qkv, int ld, void *out, int ld_out, const float *rope, const AttnLayout &lay,
                int heads, int gate_col, KernelTimer *t = nullptr, bool out_bf16 = false, bool qkv_bf16 = false,
                bool split = false, const float *bound = nullptr, bool out_h2 = false, bool kv_scaled = false,
-               bool device_choice = false);
+               bool device_choice = false, bool kv_pieces = false);
 
 // ------------------------------------------------------------------- dims
 struct Dims {

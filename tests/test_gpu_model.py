@@ -79,6 +79,38 @@ def test_transformer_block_kv_prescale_bit_identical(cfg2_models, rng, monkeypat
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("windows", [1, 3])
+def test_kv_pieces_bit_identical(cfg2_models, monkeypatch, windows):
+    """On the pipeline's time axis (L > 64, [chunk][frame][band] rows) the
+    fused QKV GEMM writes k, rotated, and v as the attention's fp16 pieces
+    and the attention copies them into LDS by DMA, reading V^T through the
+    transpose load; VOCALARC_KV_PIECES=0 keeps the fp32 projection and the
+    attention's own rotation and splits.  Both must give the same bits: one
+    2 s window (T = 201: ragged query and key blocks) and three 2 s windows
+    in one pass (M = 37386 rows: a ragged last row tile, waves whose 32 rows
+    straddle two frames, and frames that wrap to the next window)."""
+    om, dm = cfg2_models
+    chunk, step = 88200, 66150
+    x = audio.sine_mix(2.0 if windows == 1 else 5.0, 15)
+    length = x.shape[1]
+    assert O.chunk_count(length, chunk, step) == windows
+    outs = []
+    for env in (None, "0"):
+        if env is None:
+            monkeypatch.delenv("VOCALARC_KV_PIECES", raising=False)
+        else:
+            monkeypatch.setenv("VOCALARC_KV_PIECES", env)
+        dv = empty_dev(x.shape)
+        if windows == 1:
+            dm.forward(to_dev(x), length, dv)
+        else:
+            dm.separate(to_dev(x), length, chunk, step, windows, dv)
+        outs.append(from_dev(dv))
+    monkeypatch.delenv("VOCALARC_KV_PIECES", raising=False)
+    assert np.all(np.isfinite(outs[0]))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("axis,S,L", [(0, 90, 23), (1, 23, 90)])
 def test_transformer_block_reference_shape(ref_models, rng, axis, S, L):
     om, dm = ref_models
