@@ -86,8 +86,10 @@ struct GemmDescH2 {
 // lane of the pair's other dimension), by the (cos, sin) of the row's frame;
 // a wave's 32 consecutive rows span at most two frames.  pre(r) is the fp32
 // value the plain epilogue would store for register r.
+// tv: the rotary table entry (cos, sin) of frame f0 (lanes 0-31) or f1
+// (lanes 32-63) and pair lane % 32, loaded before the K loop (k tiles only).
 template <typename PRE>
-VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li, int lh, PRE pre) {
+VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li, int lh, float2 tv, PRE pre) {
     const bool is_k = n0 < 2 * d.kv_inner;
     const int region = is_k ? d.kv_inner : 2 * d.kv_inner;  // first column of the k (v) region
     const int B = d.rope_period, T = d.rope_len;
@@ -114,14 +116,15 @@ VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li,
                                    (uint32_t)(4 * lh) * pitch;
             float c0 = 1.0f, s0 = 0.0f, c1 = 1.0f, s1 = 0.0f;
             if constexpr (IS_K) {
+                // the lane's pair: its entries from the lanes holding them
                 const int pr = (kc & 63) >> 1;
-                const float *t0 = d.rope + 2 * (f0 * 32 + pr);
-                c0 = t0[0];
-                s0 = even ? -t0[1] : t0[1];
+                c0 = __shfl(tv.x, pr, 64);
+                s0 = __shfl(tv.y, pr, 64);
+                if (even) s0 = -s0;
                 if constexpr (SPLIT) {
-                    const float *t1 = d.rope + 2 * (f1 * 32 + pr);
-                    c1 = t1[0];
-                    s1 = even ? -t1[1] : t1[1];
+                    c1 = __shfl(tv.x, 32 + pr, 64);
+                    s1 = __shfl(tv.y, 32 + pr, 64);
+                    if (even) s1 = -s1;
                 }
             }
             // rows in pairs (registers r, r + 1: consecutive rows of one
@@ -290,6 +293,17 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[0][j][r] = 0.0f;
 
+    // k/v pieces: the rotary table entries the epilogue of a k tile needs,
+    // loaded now so that their latency is spent in the K loop (two registers)
+    float2 tv = make_float2(1.0f, 0.0f);
+    if constexpr (KVS && NORM && EPI == EPI_STORE) {
+        if (d.kv_pieces && n0 >= d.kv_inner && n0 < 2 * d.kv_inner) {
+            const int row0 = m0 + wave * 32;
+            const int f0 = (row0 / d.rope_period) % d.rope_len;
+            const int f = lane < 32 ? f0 : (f0 + 1 == d.rope_len ? 0 : f0 + 1);
+            tv = *reinterpret_cast<const float2 *>(d.rope + 2 * (f * 32 + (lane & 31)));
+        }
+    }
     const int nk = d.K / GS_BK;
     float ss = 0.0f;  // NORM: sum of squares of this lane's half of row wave*32 + li
 #pragma unroll
@@ -392,7 +406,7 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
             // the plain epilogue's value of each element (bias and row norm in
             // one fused multiply-add), formed in place first so the row
             // scales and biases are dead before the rotation and the split
-            kv_pieces_epilogue(d, m0 + wave * 32, n0, li, lh,
+            kv_pieces_epilogue(d, m0 + wave * 32, n0, li, lh, tv,
                                [&](int j, int r) { return fmaf(acc[0][j][r], rs[r], bpre[j]); });
             return;
         }

@@ -48,7 +48,8 @@ ROLES = [
      "FFN down-projection + residual, raising the stream's bound (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<0, false, true[,>]|ILi0ELb0ELb1E)",
-     "fused QKV + gate projection with the attention's pre-norm inside (fp32 via two-piece fp16)"),
+     "fused QKV + gate projection with the attention's pre-norm inside; on the time axis k (rotated) and v written "
+     "as the attention's fp16 pieces (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via two-piece fp16)"),
     (r"gemm_h2_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32 via two-piece fp16)"),
     (r"gemm_h2_batched_kernel(<|ILi)0", "mask estimator layer 2, batched over bands (fp32 via two-piece fp16)"),
@@ -58,6 +59,8 @@ ROLES = [
     (r"absmax_kernel", "maxima: of a weight for its fp16 pieces (model load), of the residual stream (once per pass)"),
     (r"absmax_partial_kernel", "residual stream maximum, partial (once per pass)"),
     (r"operand_bounds_kernel", "operand bounds of the fp16 two-piece GEMMs (model load)"),
+    (r"attention_h2_kvp_kernel", "time-axis attention, L = 801, on the fused projection's k/v pieces (fp32 via "
+     "two-piece fp16)"),
     (r"attention_h2_kernel", "time-axis attention, L = 801 (fp32 via two-piece fp16)"),
     (r"attention_short_h2_kernel", "band-axis attention, L = 62 (fp32 via two-piece fp16)"),
     (r"rmsnorm_h2_kernel", "FFN pre-norm, written as fp16 pieces for the FFN-up GEMM"),
@@ -158,15 +161,24 @@ PEAK_CLOCK_GHZ = 2.4  # the clock of the published dense MFMA peaks
 
 
 def counters(regex: str, out: str, command: str, *dirs: str) -> int:
+    """Summary of a kernel's counters over the dispatches whose name matches
+    regex; with a regex ending in "#largest", only the dispatches of the
+    largest grid (the full 8-window passes of a separation run)."""
+    largest = regex.endswith("#largest")
+    regex = regex[:-len("#largest")] if largest else regex
     pat = re.compile(regex)
     vals: dict[str, list[float]] = {}
     names = set()
     per_dispatch: dict[tuple[int, str], dict[str, float]] = {}
+    rows_all = []
     for i, d in enumerate(dirs):
         path = next(Path(d).rglob("*counter_collection.csv"))
-        for r in csv.DictReader(open(path)):
-            if not pat.search(r["Kernel_Name"]):
-                continue
+        rows_all += [(i, r) for r in csv.DictReader(open(path)) if pat.search(r["Kernel_Name"])]
+    grid_max = max((int(r["Grid_Size"]) for _, r in rows_all), default=0)
+    for i, r in rows_all:
+        if largest and int(r["Grid_Size"]) != grid_max:
+            continue
+        if True:
             names.add(r["Kernel_Name"])
             vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
             rec = per_dispatch.setdefault((i, r["Dispatch_Id"]), {})
@@ -175,7 +187,8 @@ def counters(regex: str, out: str, command: str, *dirs: str) -> int:
     avg = {k: sum(v) / len(v) for k, v in vals.items()}
     lines = [f"# rocprofv3 counters of `{regex}`", "", "Commands (repository root, MI355X box; one pass per counter "
              "group):", "", "```", command.strip(), "```", "",
-             "Kernels matched: " + ", ".join(f"`{n[:120]}`" for n in sorted(names)), "",
+             "Kernels matched: " + ", ".join(f"`{n[:120]}`" for n in sorted(names)) +
+             (f" (only the dispatches of the largest grid, {grid_max} work-items)" if largest else ""), "",
              "Per-dispatch averages (totals over the device as rocprofv3 reports them):", "",
              "| counter | value |", "|---|---:|"]
     for k in sorted(avg):
@@ -188,6 +201,14 @@ def counters(regex: str, out: str, command: str, *dirs: str) -> int:
     rows = [(k, v) for k, v in sorted(per_dispatch.items(), key=lambda kv: (kv[0][0], int(kv[0][1])))
             if all(c in v for c in keys) and v["ns"] > 0]
     if rows:
+        shown = rows[-12:]
+        busy_all = [v["SQ_VALU_MFMA_BUSY_CYCLES"] / (v["SQ_CYCLES"] * SIMDS_PER_SE) for _, v in rows]
+        clk_all = sorted(v["GRBM_GUI_ACTIVE"] / XCDS / v["ns"] for _, v in rows)
+        lines += ["", f"Over the {len(rows)} dispatches of that pass: matrix cores busy {min(busy_all):.3f}-"
+                  f"{max(busy_all):.3f} (mean {sum(busy_all) / len(busy_all):.3f}), clock median "
+                  f"{clk_all[len(clk_all) // 2]:.3f} GHz" + (f"; the last {len(shown)} below" if len(shown) < len(rows)
+                                                             else "") + "."]
+        rows = shown
         lines += ["", "Per dispatch (the pass with the clock and busy counters): clock = `GRBM_GUI_ACTIVE` / "
                   f"{XCDS} XCDs / duration; busy = `SQ_VALU_MFMA_BUSY_CYCLES` / (`SQ_CYCLES` x {SIMDS_PER_SE}); "
                   f"fraction of the MFMA peak = busy x clock / {PEAK_CLOCK_GHZ} GHz. Durations are the profiled "
