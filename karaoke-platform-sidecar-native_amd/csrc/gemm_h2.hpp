@@ -84,12 +84,13 @@ struct GemmDescH2 {
 // attention's staging forms, so the attention copies them into LDS as they
 // are.  k is rotated first (rope_own: each lane swaps its value with the
 // lane of the pair's other dimension), by the (cos, sin) of the row's frame;
-// a wave's 32 consecutive rows span at most two frames.  pre(r) is the fp32
-// value the plain epilogue would store for register r.
+// a wave's 32 consecutive rows span at most two frames.  Each value is first
+// formed as the plain epilogue forms it: acc times the row's norm scale plus
+// the bias in one fused multiply-add.
 // tv: the rotary table entry (cos, sin) of frame f0 (lanes 0-31) or f1
 // (lanes 32-63) and pair lane % 32, loaded before the K loop (k tiles only).
-template <typename PRE>
-VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li, int lh, float2 tv, PRE pre) {
+VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li, int lh, float2 tv,
+                                  const floatx16 (&acc)[1][4], floatx16 rs, floatx4 bpre) {
     const bool is_k = n0 < 2 * d.kv_inner;
     const int region = is_k ? d.kv_inner : 2 * d.kv_inner;  // first column of the k (v) region
     const int B = d.rope_period, T = d.rope_len;
@@ -136,7 +137,7 @@ VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li,
                 float y[2];
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    y[e] = pre(j, r + e);
+                    y[e] = fmaf(acc[0][j][r + e], rs[r + e], bpre[j]);
                     if constexpr (IS_K) {
                         const float other =
                             __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[e]), 0xB1, 0xF, 0xF, false));
@@ -406,8 +407,13 @@ __device__ __forceinline__ void gemm_h2_body(const GemmDescH2 &d, float a_bound,
             // the plain epilogue's value of each element (bias and row norm in
             // one fused multiply-add), formed in place first so the row
             // scales and biases are dead before the rotation and the split
-            kv_pieces_epilogue(d, m0 + wave * 32, n0, li, lh, tv,
-                               [&](int j, int r) { return fmaf(acc[0][j][r], rs[r], bpre[j]); });
+            // the row scales and biases as vector values (not arrays), which
+            // keeps them in registers across the epilogue's variants
+            floatx16 rsv;
+#pragma unroll
+            for (int r = 0; r < 16; r++) rsv[r] = rs[r];
+            kv_pieces_epilogue(d, m0 + wave * 32, n0, li, lh, tv, acc, rsv,
+                               floatx4{bpre[0], bpre[1], bpre[2], bpre[3]});
             return;
         }
     }
