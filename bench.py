@@ -57,7 +57,7 @@ HBM_PEAK_GBS = 8000.0
 HOST_SECONDS = 10.0
 DOMINANT = "gemm_ff1"
 KERNEL_CLASSES = ("stft", "band_gather", "gemm_band_split", "rmsnorm", "gemm_qkv", "attention_long",
-                  "attention_short", "gemm_out", "gemm_ff1", "gemm_ff2", "gemm_mask1", "gemm_mask2", "mask_glu",
+                  "attention_short", "band_attention", "gemm_out", "gemm_ff1", "gemm_ff2", "gemm_mask1", "gemm_mask2", "mask_glu",
                   "istft", "crossfade")
 
 

@@ -1,0 +1,429 @@
+// The band-axis attention fused with its projection.  On the band axis a
+// sequence is one frame's L <= 64 band tokens, consecutive rows of the
+// residual stream, so one workgroup can hold everything an attention head of
+// two sequences needs: it computes the pre-norm fused projection's q, k and v
+// columns of one head for 2 x 64 rows (the RMSNorm inside, as the QKV GEMM
+// with row_norm does) and the gate logit of that head by fp32 dot products,
+// keeps them in LDS, and runs the attention of both sequences on them
+// (attention_short_h2_kernel's products and softmax), writing only the
+// attention output -- the out projection's h2 rows.  q, k, v and the gate
+// logits never reach HBM: the separate kernels wrote them (3 x inner + 32
+// floats per token) and read them back.
+//
+// Projection.  Tile rows 0-63 are the positions of sequence s0 (rows past L
+// repeat position L - 1, sequences past S repeat the last one), rows 64-127
+// those of s0 + 1; columns are the head's 64 q, 64 k and 64 v columns of the
+// fused matrix (three 64-row halves of its 128-row piece tiles).  K chunks of
+// 16 go global -> LDS by DMA in a 3-chunk ring (8 KB of fp32 rows, 12 KB of
+// weight pieces); 8 waves, wave w holding rows 32 (w % 4) .. +31 and columns
+// 96 (w / 4) .. +95 (three 32x32 accumulators, 9 v_mfma_f32_32x32x16_f16 per
+// chunk).  Each wave splits its A rows as gemm_h2_body does, sums their
+// squares for the row norm, and the waves of columns 0-95 also accumulate the
+// row's dot product with the head's gate row (fp32 FMAs; the gain folded in
+// as in the pieces).  The epilogue forms each value as the QKV GEMM's does --
+// acc 2^-(ea+ew) (times 2^ek for k, 2^ev for v) times the row's norm scale
+// plus the bias, one fused multiply-add -- so q, k and v are the bits that
+// GEMM would have written; the gate logit is the fp32 dot product times the
+// norm scale plus the gate's bias.
+//
+// Attention (rotary: the table is required).  q goes through LDS as fp32
+// (dim-major), is rotated and split by
+// the wave that owns the query (attention_short_h2_kernel's expressions); k
+// is rotated in the epilogue (rope_own with the partner dimension from the
+// neighbouring lane, the table entry of each row's position) and split, v
+// split, both written as the short kernel's LDS operands.  Wave w then takes
+// 16 queries (16 (w % 4) ..) of sequence w / 4: three v_mfma_f32_16x16x32_f16
+// per product, single-pass softmax, the gate, and the output written as h2
+// rows scaled by 2^h2_exponent(bound).
+#pragma once
+
+#include "attention_h2.hpp"
+
+namespace vh {
+
+struct BandAttnArgs {
+    const float *x;  // residual stream [S * L][lda] fp32, sequence s at rows s L .. s L + L - 1
+    int lda, K;      // K: the model dim (a multiple of 16, at most BA_MAX_K)
+    // the fused q|k|v|gates projection's pieces (split_weight_h2_kernel) of
+    // the matrix with the RMSNorm gain folded in, H * 64 rows per q, k, v
+    const void *W;
+    const float *bias;     // [3 H 64 (+ gates)] or null
+    const float *gate_w;   // [H][K] the gain-folded gate rows (fp32); null: no gates
+    const float *gate_b;   // [H] the gates' biases, or null
+    const float *x_bound;  // device float: max |x| (the projection's A scale)
+    const float *bound;    // device float bounding |q|, |k|, |v| (the attention's piece scales)
+    const float *rope;     // [L][32][2] (cos, sin) pairs
+    float *out;            // [S * L][ld_out]: head h's 64 values at column 64 h, as h2 rows
+    int ld_out;
+    int S, L, H;
+    float scale;  // softmax scale
+};
+
+constexpr int BA_THREADS = 512;
+constexpr int BA_ROWS = 128;                       // two sequences at 64 tile rows each
+constexpr int BA_MAX_K = 512;                      // gate row staged in LDS
+constexpr int BA_A_BYTES = BA_ROWS * GS_BK * 4;    // 8 KB: fp32 rows of 64 B
+constexpr int BA_B_BYTES = 12 * 1024;              // q, k, v x two planes x 64 rows of 32 B
+constexpr int BA_STAGE = BA_A_BYTES + BA_B_BYTES;  // 20 KB
+constexpr int BA_RING = 3;
+constexpr int BA_PITCH = ATT_DH + 8;       // halves per LDS row of a K or V^T piece
+constexpr int BA_PIECE = 64 * BA_PITCH * 2;  // bytes of one piece of one sequence's K (or V^T)
+constexpr int BA_V_OFF = 4 * BA_PIECE;       // the V^T pieces follow the K pieces
+constexpr int BA_QPITCH = BA_ROWS + 4;       // floats per dim of the dim-major q staging
+constexpr int BA_REGION = 8 * BA_PIECE;      // 72 KB: the ring, then q, then the K and V^T pieces
+static_assert(BA_RING * BA_STAGE <= BA_REGION && ATT_DH * BA_QPITCH * 4 <= BA_V_OFF, "LDS region");
+
+// position of dimension d (of a K row) or key d (of a V^T row) within the
+// 64 halves of an attention operand row (attention_short_h2_kernel's order)
+VH_DEVICE int ba_slot(int d) { return 8 * (4 * (d >> 5) + ((d >> 2) & 3)) + 4 * ((d >> 4) & 1) + (d & 3); }
+
+__global__ __launch_bounds__(BA_THREADS, 2) __attribute__((amdgpu_waves_per_eu(4, 4))) void band_attention_fused_kernel(
+    BandAttnArgs a) {
+    __shared__ __attribute__((aligned(1024))) unsigned char region[BA_REGION];
+    __shared__ __attribute__((aligned(16))) float rsc[BA_ROWS];
+    __shared__ __attribute__((aligned(16))) float glog[BA_ROWS];
+    __shared__ __attribute__((aligned(16))) float gw[BA_MAX_K];
+
+    const int task = xcd_swizzle((int)blockIdx.x, (int)gridDim.x);  // the 8 heads of a tile: same XCD
+    const int h = task % a.H;
+    const int s0 = 2 * (task / a.H);
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, lh = lane >> 5;
+    const int rb = wave & 3, ch = wave >> 2;
+    const int inner = a.H * ATT_DH;
+    const bool gated = a.gate_w != nullptr;
+    const int row_base = s0 * a.L;
+    auto grow = [&](int r) { return min(s0 + (r >> 6), a.S - 1) * a.L + min(r & 63, a.L - 1); };
+
+    const int ea = h2_exponent(*a.x_bound);
+    const int ew = h2_exponent(*static_cast<const float *>(a.W));
+    const float a_scale = ldexpf(1.0f, ea);
+    const float bnd = *a.bound;
+    const float qs = a.scale * 1.4426950408889634f;
+    int ek, eq, ev;
+    att_h2_exponents(bnd, qs, ek, eq, ev);
+
+    // column block j of the wave: 32-column block cb = 3 ch + j of the 192,
+    // i.e. q, k or v (t = cb / 2), dims 32 (cb % 2) ..; its bias and extra
+    // power of two (k: 2^ek, v: 2^ev), loaded before the K loop
+    const float gbias = a.gate_w && a.gate_b ? a.gate_b[h] : 0.0f;
+    float bpre[3];
+    int eblk[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int cb = 3 * ch + j, t = cb >> 1;
+        const int col = t * inner + h * ATT_DH + 32 * (cb & 1) + li;
+        bpre[j] = a.bias ? a.bias[col] : 0.0f;
+        eblk[j] = t == 1 ? ek : (t == 2 ? ev : 0);
+    }
+
+    // DMA.  A: wave w copies tile rows 16 w .. 16 w + 15 of each chunk (lane:
+    // row 16 w + lane / 4, 16-byte slot lane % 4, swizzled as gemm_h2_body's).
+    // W: the chunk's 12 KB are twelve 1 KB pieces i = 4 t + 2 plane + half
+    // (t: q, k, v; the head's 64 rows of a 128-row piece tile are 2 KB per
+    // plane); wave w copies piece w and, when w < 4, piece w + 8.  The gate
+    // row (at most 2 KB) goes to gw by waves 0 and 1 ahead of the ring.
+    auto swz_a = [](int r) { return (r >> 2) & 3; };
+    auto swz_w = [](int r) { return (r >> 3) & 1; };
+    const uint32_t ring_base = (uint32_t)(uintptr_t)region;
+    const int ar = 16 * wave + (lane >> 2);
+    const uint32_t a_voff =
+        (uint32_t)(grow(ar) - row_base) * (uint32_t)a.lda * 4u + 16u * (uint32_t)((lane & 3) ^ swz_a(ar));
+    const float *a_base = a.x + (size_t)row_base * a.lda;
+    const int nkc = a.K / GS_BK;
+    const char *w_planes = static_cast<const char *>(a.W) + H2_HEADER;
+    auto piece_src = [&](int i) {
+        const int t = i >> 2, plane = (i >> 1) & 1, half = i & 1;
+        const int tile = (t * inner + h * ATT_DH) / GS_BN;
+        return w_planes + (size_t)tile * nkc * (H2_WBLOCK * 2) + plane * (GS_BN * GS_BK * 2) +
+               (h & 1) * (64 * GS_BK * 2) + half * 1024;
+    };
+    const bool two_b = wave < 4;
+    const char *wsrc0 = piece_src(wave);
+    const char *wsrc1 = piece_src(two_b ? wave + 8 : wave);
+    const uint32_t w_voff = 16u * (uint32_t)lane;
+    if (gated && wave < 2) {
+        const uint32_t off = 1024u * (uint32_t)wave + 16u * (uint32_t)lane;
+        if (off < 4u * (uint32_t)a.K)
+            lds_dma16s(off, a.gate_w + (size_t)h * a.K, (uint32_t)(uintptr_t)gw + 1024u * (uint32_t)wave);
+    }
+    auto issue = [&](int kt) {
+        const uint32_t sb = ring_base + (uint32_t)((kt % BA_RING) * BA_STAGE);
+        lds_dma16s(a_voff, a_base + kt * GS_BK, sb + wave * 1024);
+        lds_dma16s(w_voff, wsrc0 + (size_t)kt * (H2_WBLOCK * 2), sb + BA_A_BYTES + wave * 1024);
+        if (two_b) lds_dma16s(w_voff, wsrc1 + (size_t)kt * (H2_WBLOCK * 2), sb + BA_A_BYTES + (wave + 8) * 1024);
+    };
+    // chunk kt + 1 has landed once at most the loads of chunk kt + 2 (2 or 3
+    // per wave) are in flight
+    auto wait_next = [&](bool more) {
+        if (!more) wait_vmcnt<0>();
+        else if (two_b) wait_vmcnt<3>();
+        else wait_vmcnt<2>();
+    };
+
+    floatx16 acc[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+    float ss = 0.0f, gdot = 0.0f;
+
+    issue(0);
+    if (nkc > 1) issue(1);
+    wait_next(nkc > 1);
+    __syncthreads();
+    for (int kt = 0; kt < nkc; kt++) {
+        // chunk kt + 2 goes to the slot chunk kt - 1 used: every wave finished
+        // reading it before the barrier that ended the previous iteration
+        if (kt + 2 < nkc) issue(kt + 2);
+        const unsigned char *sbuf = region + (kt % BA_RING) * BA_STAGE;
+        const int r = 32 * rb + li;
+        const unsigned char *arow = sbuf + r * 64;
+        const floatx4 lo = *reinterpret_cast<const floatx4 *>(arow + 16 * (lh ^ swz_a(r)));
+        const floatx4 hi = *reinterpret_cast<const floatx4 *>(arow + 16 * ((2 + lh) ^ swz_a(r)));
+        halfx8 ah, am;
+        split8_h2(lo, hi, a_scale, ah, am);
+#pragma unroll
+        for (int e = 0; e < 4; e++) ss = fmaf(hi[e], hi[e], fmaf(lo[e], lo[e], ss));
+        if (gated && ch == 0) {
+            // the lane's k: 16 kt + 4 lh .. +3 (lo) and 16 kt + 8 + 4 lh .. +3 (hi)
+            const floatx4 g0 = *reinterpret_cast<const floatx4 *>(&gw[16 * kt + 4 * lh]);
+            const floatx4 g1 = *reinterpret_cast<const floatx4 *>(&gw[16 * kt + 8 + 4 * lh]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) gdot = fmaf(lo[e], g0[e], gdot);
+#pragma unroll
+            for (int e = 0; e < 4; e++) gdot = fmaf(hi[e], g1[e], gdot);
+        }
+        halfx8 wh[3], wm[3];
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int cb = 3 * ch + j;
+            const int rw = 32 * (cb & 1) + li;
+            const unsigned char *wp = sbuf + BA_A_BYTES + (cb >> 1) * 4096 + rw * 32 + 16 * (lh ^ swz_w(rw));
+            wh[j] = *reinterpret_cast<const halfx8 *>(wp);
+            wm[j] = *reinterpret_cast<const halfx8 *>(wp + 2048);
+        }
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, wh[j], acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wm[j], acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, wh[j], acc[j], 0, 0, 0);
+        wait_next(kt + 2 < nkc);
+        __syncthreads();
+    }
+
+    // the row norm's scales (lanes li and li + 32 summed the two halves of
+    // row 32 rb + li; both waves of a row block hold the same sums) and the
+    // gate logits
+    {
+        const float tot = ss + __shfl_xor(ss, 32, 64);
+        const float gd = gdot + __shfl_xor(gdot, 32, 64);
+        const float rs = sqrtf((float)a.K) / sqrtf(tot + 1.0e-12f);
+        if (ch == 0 && lh == 0) {
+            rsc[32 * rb + li] = rs;
+            glog[32 * rb + li] = gated ? fmaf(gd, rs, gbias) : 0.0f;
+        }
+    }
+    __syncthreads();
+    // the wave's queries (below): 16 (wave % 4) + n of sequence wave / 4;
+    // their rotary table entries are loaded here, used after the next barrier
+    const int n = lane & 15, g = lane >> 4;
+    const int sq = wave >> 2;
+    const int q = 16 * (wave & 3) + n;
+    const int qc = min(q, a.L - 1);
+    const int tq = 64 * sq + qc;
+    floatx4 qtab[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) qtab[j] = ld4(a.rope + qc * ATT_DH + 16 * j + 4 * g);
+    // every value as the QKV GEMM's epilogue forms it; register 4 q4 + e of a
+    // lane is row 32 rb + 8 q4 + 4 lh + e, column li of its block
+    {
+        const int eu = -(ea + ew);
+        floatx16 rsv;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const floatx4 r4 = *reinterpret_cast<const floatx4 *>(&rsc[32 * rb + 8 * q4 + 4 * lh]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) rsv[4 * q4 + e] = r4[e];
+        }
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const float b = ldexpf(bpre[j], eblk[j]);
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[j][r] = fmaf(ldexpf(acc[j][r], eu + eblk[j]), rsv[r], b);
+        }
+    }
+    // LDS layout from here: the q staging (dim-major fp32, 33 KB) and the K
+    // pieces share the region's first 36 KB (K piece p of sequence s at
+    // (2 s + p) BA_PIECE, row = key); the V^T pieces (piece p of sequence s at
+    // BA_V_OFF + (2 s + p) BA_PIECE, row = dim) lie beyond it, so v is written
+    // together with q and k after q has been read
+    const int seq = rb >> 1;
+    const int key0 = 32 * (rb & 1) + 4 * lh;  // key of register r: key0 + 8 (r / 4) + r % 4
+    const float one = opaque_one();
+    float *Qs = reinterpret_cast<float *>(region);
+    if (ch == 0) {
+        // q: blocks 0 and 1 of the waves of columns 0-95
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+                *reinterpret_cast<floatx4 *>(&Qs[(32 * j + li) * BA_QPITCH + 32 * rb + 8 * q4 + 4 * lh]) =
+                    floatx4{acc[j][4 * q4], acc[j][4 * q4 + 1], acc[j][4 * q4 + 2], acc[j][4 * q4 + 3]};
+    } else {
+        // v: blocks 1 and 2 of the waves of columns 96-191, split
+        auto write_v = [&](const floatx16 &y, int d) {
+            unsigned char *vh = region + BA_V_OFF + (2 * seq) * BA_PIECE + d * BA_PITCH * 2;
+            unsigned char *vm = vh + BA_PIECE;
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                const int key = key0 + 8 * q4;  // keys key .. key + 3: consecutive slots
+                const uint32_t h01 = pack_f16x2(y[4 * q4], y[4 * q4 + 1]);
+                const uint32_t h23 = pack_f16x2(y[4 * q4 + 2], y[4 * q4 + 3]);
+                const uint32_t m01 = m_pair_f16(y[4 * q4], y[4 * q4 + 1], one, h01);
+                const uint32_t m23 = m_pair_f16(y[4 * q4 + 2], y[4 * q4 + 3], one, h23);
+                *reinterpret_cast<u32x2 *>(vh + 2 * ba_slot(key)) = u32x2{h01, h23};
+                *reinterpret_cast<u32x2 *>(vm + 2 * ba_slot(key)) = u32x2{m01, m23};
+            }
+        };
+        write_v(acc[1], li);
+        write_v(acc[2], 32 + li);
+    }
+    // the rotary table entries of the wave's k block (dims 32 ch + li: pair
+    // (32 ch + li) / 2 at the 16 positions of the lane's rows), loaded here so
+    // that their latency passes in the q step
+    float2 ktab[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int key = key0 + 8 * (r >> 2) + (r & 3);
+        ktab[r] = *reinterpret_cast<const float2 *>(a.rope + min(key, a.L - 1) * ATT_DH + 2 * ((32 * ch + li) >> 1));
+    }
+    __syncthreads();
+
+    // the wave's queries rotated, scaled and split (attention_short_h2_kernel's
+    // expressions)
+    halfx8 qh[2], qm[2];
+    {
+        floatx4 qpre[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) qpre[j][e] = Qs[(16 * j + 4 * g + e) * BA_QPITCH + tq];
+        const float q_scale = qs * ldexpf(1.0f, eq);
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+            split8_h2(rope_pairs(qpre[2 * st], qtab[2 * st]), rope_pairs(qpre[2 * st + 1], qtab[2 * st + 1]), q_scale,
+                      qh[st], qm[st]);
+    }
+    const float gate_logit = glog[tq];
+    __syncthreads();  // the q staging is overwritten below
+
+    // k, rotated and split (blocks 2 of the waves of columns 0-95, 0 of the others)
+    {
+        auto write_k = [&](const floatx16 &y, int d) {
+            _Float16 *kh = reinterpret_cast<_Float16 *>(region + (2 * seq) * BA_PIECE) + ba_slot(d);
+            _Float16 *km = reinterpret_cast<_Float16 *>(region + (2 * seq + 1) * BA_PIECE) + ba_slot(d);
+            const bool even = (d & 1) == 0;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                float v[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    // the pair's other dimension from the neighbouring lane
+                    const float other =
+                        __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[r + e]), 0xB1, 0xF, 0xF, false));
+                    const float2 cs = ktab[r + e];
+                    v[e] = rope_own(y[r + e], other, cs.x, even ? -cs.y : cs.y);
+                }
+                const uint32_t hp = pack_f16x2(v[0], v[1]);
+                const uint32_t mp = m_pair_f16(v[0], v[1], one, hp);
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const int key = key0 + 8 * ((r + e) >> 2) + ((r + e) & 3);
+                    kh[key * BA_PITCH] = __builtin_bit_cast(_Float16, (uint16_t)(hp >> (16 * e)));
+                    km[key * BA_PITCH] = __builtin_bit_cast(_Float16, (uint16_t)(mp >> (16 * e)));
+                }
+            }
+        };
+        if (ch == 0) write_k(acc[2], li);
+        else write_k(acc[0], 32 + li);
+    }
+    __syncthreads();
+
+    // attention of the wave's 16 queries over the sequence's keys
+    constexpr int EP = 13;  // probabilities <= 1: 2^13 < 2^14
+    const float s_unscale = ldexpf(1.0f, -(ek + eq)), o_unscale = ldexpf(1.0f, -(ev + EP));
+    const float p_scale = ldexpf(1.0f, EP);
+    typedef _Float16 Row[BA_PITCH];
+    const Row *Kh = reinterpret_cast<const Row *>(region + (2 * sq) * BA_PIECE);
+    const Row *Km = reinterpret_cast<const Row *>(region + (2 * sq + 1) * BA_PIECE);
+    const Row *Vh = reinterpret_cast<const Row *>(region + BA_V_OFF + (2 * sq) * BA_PIECE);
+    const Row *Vm = reinterpret_cast<const Row *>(region + BA_V_OFF + (2 * sq + 1) * BA_PIECE);
+    floatx4 sc[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+        sc[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            const halfx8 kh = *reinterpret_cast<const halfx8 *>(&Kh[16 * kt + n][8 * (4 * st + g)]);
+            const halfx8 km = *reinterpret_cast<const halfx8 *>(&Km[16 * kt + n][8 * (4 * st + g)]);
+            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(km, qh[st], sc[kt], 0, 0, 0);
+            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qm[st], sc[kt], 0, 0, 0);
+            sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[st], sc[kt], 0, 0, 0);
+        }
+        sc[kt] = sc[kt] * s_unscale;  // exact: a power of two
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            if (16 * kt + 4 * g + r >= a.L) sc[kt][r] = -INFINITY;
+            m = fmaxf(m, sc[kt][r]);
+        }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float l = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            sc[kt][r] = __builtin_amdgcn_exp2f(sc[kt][r] - m);
+            l += sc[kt][r];
+        }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+
+    floatx4 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        halfx8 ph, pm;
+        split8_h2(sc[2 * u], sc[2 * u + 1], p_scale, ph, pm);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const halfx8 vh = *reinterpret_cast<const halfx8 *>(&Vh[n + 16 * dt][8 * (4 * u + g)]);
+            const halfx8 vm = *reinterpret_cast<const halfx8 *>(&Vm[n + 16 * dt][8 * (4 * u + g)]);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vm, ph, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pm, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, o[dt], 0, 0, 0);
+        }
+    }
+
+    if (q < a.L && s0 + sq < a.S) {
+        const float f = (1.0f / l) * (gated ? sigmoid_dev(gate_logit) : 1.0f) * o_unscale;
+        // dims 16 dt + 4 g .. +3: group g of chunk dt, whose group g ^ 2 lies
+        // in lane ^ 32 (the same query)
+        const float so = ldexpf(1.0f, h2_exponent(bnd));
+        unsigned char *rowp =
+            reinterpret_cast<unsigned char *>(a.out + (size_t)((s0 + sq) * a.L + q) * a.ld_out + h * ATT_DH);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) store4_h2_swap<32>(rowp + 64 * dt, g, o[dt] * f, so);
+    }
+}
+
+}  // namespace vh

@@ -13,6 +13,7 @@
 #include "attention_bf16.hpp"
 #include "attention_split.hpp"
 #include "attention_h2.hpp"
+#include "band_attention.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
 #include "gemm_bf16.hpp"
@@ -453,6 +454,32 @@ bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int 
         default: set_error("unknown GEMM epilogue %d", epilogue); return false;
     }
     return sync_debug(s, "gemm_h2_kernel");
+}
+
+bool band_attention(hipStream_t s, const BandAttention &b, KernelTimer *t) {
+    const int inner = b.heads * ATT_DH;
+    // a tile's rows (two sequences) lie within 2^32 bytes of its first row
+    const bool ok = b.x && b.W && b.out && b.x_bound && b.bound && b.rope && b.S > 0 && b.L > 0 && b.L <= 64 && b.heads > 0 &&
+                    b.K >= GS_BK && b.K % GS_BK == 0 && b.K <= BA_MAX_K && b.lda >= b.K && b.lda % 4 == 0 &&
+                    b.lda <= (1 << 21) && inner % GS_BN == 0 && b.ld_out >= inner && b.ld_out % 4 == 0 &&
+                    (int64_t)b.S * b.L <= INT32_MAX / 2 && !(((uintptr_t)b.x | (uintptr_t)b.W | (uintptr_t)b.out) & 15) &&
+                    !((uintptr_t)b.gate_w & 15);
+    if (!ok) {
+        set_error("band_attention: unsupported shape S=%d L=%d heads=%d K=%d lda=%d ld_out=%d", b.S, b.L, b.heads, b.K,
+                  b.lda, b.ld_out);
+        return false;
+    }
+    BandAttnArgs a;
+    a.x = b.x; a.lda = b.lda; a.K = b.K;
+    a.W = b.W; a.bias = b.bias; a.gate_w = b.gate_w; a.gate_b = b.gate_b;
+    a.x_bound = b.x_bound; a.bound = b.bound; a.rope = b.rope;
+    a.out = b.out; a.ld_out = b.ld_out;
+    a.S = b.S; a.L = b.L; a.H = b.heads;
+    a.scale = 0.125f;
+    const unsigned grid = (unsigned)(((int64_t)b.S + 1) / 2 * b.heads);
+    Scope sc(t, s, "band_attention");
+    hipLaunchKernelGGL(band_attention_fused_kernel, dim3(grid), dim3(BA_THREADS), 0, s, a);
+    return sync_debug(s, "band_attention_fused_kernel");
 }
 
 template <int EPI>
@@ -1015,10 +1042,26 @@ bool transformer_block(hipStream_t s, const Dims &d, const LayerWeights &w, floa
             gq.rope_period = lay.group;
             gq.rope_len = lay.L;
         }
-        if (!gemm_h2(s, gq, OperandBound{xb->dev, 0.0f}, EPI_STORE, t, "gemm_qkv")) return false;
-        if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, true,
-                       att_h2 ? w.bounds + 1 : nullptr, att_h2, kv_pre, false, kv_pieces))
-            return false;
+        // On the band axis (sequences of L <= 64 consecutive rows) the
+        // projection and the attention run as one kernel (band_attention.hpp):
+        // q, k, v and the gate logits stay on chip.  VOCALARC_BAND_FUSED=0
+        // keeps the two kernels.
+        const char *bf_env = getenv("VOCALARC_BAND_FUSED");
+        const bool band_fused = kv_pre && lay.L <= 64 && lay.group == 1 && lay.seq_stride == 0 &&
+                                lay.pos_stride == 1 && lay.group_stride == lay.L && tokens == (int64_t)lay.S * lay.L &&
+                                D <= BA_MAX_K && inner % GS_BN == 0 && (!d.gated || w.wgate_g) && rt &&
+                                !(bf_env && bf_env[0] == '0');
+        if (band_fused) {
+            BandAttention ba{x, D, D, w.wqkvg_pg, w.bqkvg, d.gated ? w.wgate_g : nullptr,
+                             d.gated && w.bqkvg ? w.bqkvg + d.qkv_dim() : nullptr, xb->dev, w.bounds + 1, rt,
+                             attn, inner, lay.S, lay.L, d.heads};
+            if (!band_attention(s, ba, t)) return false;
+        } else {
+            if (!gemm_h2(s, gq, OperandBound{xb->dev, 0.0f}, EPI_STORE, t, "gemm_qkv")) return false;
+            if (!attention(s, qkvg, nq, attn, inner, rt, lay, d.heads, gate, t, false, false, true,
+                           att_h2 ? w.bounds + 1 : nullptr, att_h2, kv_pre, false, kv_pieces))
+                return false;
+        }
         if (!lin(attn, inner, w.wout, w.wout_p, 1, nullptr, x, D, D, inner, EPI_RESIDUAL, att_h2, "gemm_out"))
             return false;
         if (!rmsnorm_h2(s, x, D, w.ff_gamma, normed, D, tokens, D, w.bounds + 2, t)) return false;

@@ -163,6 +163,27 @@ bool gemm_h2(hipStream_t s, const GemmArgsH2 &g, const OperandBound &bound, int 
 // A ragged batch of fp16 two-piece GEMMs with one A bound (one launch per 64 problems).
 bool gemm_h2_batched(hipStream_t s, const std::vector<GemmArgsH2> &gs, const OperandBound &bound, int epilogue,
                      KernelTimer *t = nullptr, const char *name = "gemm_h2");
+// The band-axis attention fused with its pre-norm projection
+// (band_attention.hpp): for S sequences of L <= 64 consecutive rows of the
+// residual stream x, the q, k, v and gate columns of the gain-folded fused
+// projection (W: its pieces, rows q|k|v of heads * 64 each, then the gates;
+// gate_w: the gate rows in fp32 with the gain folded, null for none), the
+// rotary attention with the fp16 two-piece products, and out written as h2
+// rows scaled by 2^h2_exponent(*bound) (the out projection's A).  x_bound:
+// max |x| (device float); bound: the fused projection's bound (device float,
+// within the two-piece attention's range); rope: the interleaved rotary table
+// of at least L positions (required).  K a multiple of 16 and at most
+// 512; heads * 64 a multiple of 128.
+struct BandAttention {
+    const float *x; int lda, K;
+    const void *W;
+    const float *bias;
+    const float *gate_w, *gate_b;
+    const float *x_bound, *bound, *rope;
+    float *out; int ld_out;
+    int S, L, heads;
+};
+bool band_attention(hipStream_t s, const BandAttention &b, KernelTimer *t = nullptr);
 // Bytes of W's fp16 pieces: a 256-byte header (max|W|) and two planes (N
 // rounded up to a multiple of 128).
 inline size_t h2_bytes(int N, int K) { return 256 + (size_t)(N + 127) / 128 * 128 * K * 4; }
@@ -267,6 +288,9 @@ struct LayerWeights {
     // (fold_gain_split_h2), for blocks whose attention pre-norm runs inside
     // that GEMM (XBound); null: the RMSNorm kernel runs
     void *wqkvg_pg = nullptr;
+    // the gate rows of that gain-folded matrix in fp32 ([heads][D]), for the
+    // band-axis attention fused with its projection; null: not fused
+    float *wgate_g = nullptr;
     float *bounds = nullptr;
     // the fused projection's bound (bounds[1], which also bounds q, k and v)
     // lies in the fp16 two-piece attention's range (h2_attention_bound_ok);

@@ -594,8 +594,10 @@ bool prepare_split(vh_model *m) {
     auto bytes = [](int N, int K) { return K % SPLIT_K_MULTIPLE ? 0 : (h2_bytes(N, K) + 255) & ~(size_t)255; };
     // per layer: the four matrices, and the QKV one again with its RMSNorm
     // gain folded in (the attention's pre-norm fused into the QKV GEMM)
-    const size_t per_layer =
-        2 * bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) + bytes(D, d.ff_dim);
+    // (and that matrix's gate rows in fp32 for the fused band-axis attention)
+    const size_t gate_bytes = d.gated ? ((size_t)d.heads * D * sizeof(float) + 255) & ~(size_t)255 : 0;
+    const size_t per_layer = 2 * bytes(d.qkvg_dim(), D) + bytes(D, d.inner()) + bytes(d.ff1_out(), D) +
+                             bytes(D, d.ff_dim) + gate_bytes;
     size_t total = per_layer * m->layers.size();
     for (int b = 0; b < d.bands; b++) total += bytes(Hm, D) + bytes(2 * d.in_dim(b), Hm);
     m->mask_w1_s.assign(d.bands, nullptr);
@@ -635,6 +637,15 @@ bool prepare_split(vh_model *m) {
         if (ok == 0) w.bounds = nullptr;  // weights beyond the scale range: this layer's linears on fp32 MFMA
         w.att_h2 = w.bounds && h2_attention_bound_ok(hb[1]);
         if (w.bounds && !split_folded(w.wqkvg, d.qkvg_dim(), w.gamma, &w.wqkvg_pg)) return false;
+        if (w.wqkvg_pg && gate_bytes) {
+            // fold_tmp still holds the gain-folded matrix (stream order)
+            w.wgate_g = reinterpret_cast<float *>(cur);
+            cur += gate_bytes;
+            if (!check(hipMemcpyAsync(w.wgate_g, fold_tmp.f() + (size_t)d.qkv_dim() * D,
+                                      (size_t)d.heads * D * sizeof(float), hipMemcpyDeviceToDevice, s),
+                       "hipMemcpy(gate rows)"))
+                return false;
+        }
     }
     for (int b = 0; b < d.bands && mask_ok; b++)  // no pieces: the mask estimator stays on fp32 MFMA
         if (!split(m->mask_w1[b], Hm, D, &m->mask_w1_s[b]) || !split(m->mask_w2[b], 2 * d.in_dim(b), Hm, &m->mask_w2_s[b]))

@@ -48,8 +48,8 @@ ROLES = [
      "FFN down-projection + residual, raising the stream's bound (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<0, false, true[,>]|ILi0ELb0ELb1E)",
-     "fused QKV + gate projection with the attention's pre-norm inside; on the time axis k (rotated) and v written "
-     "as the attention's fp16 pieces (fp32 via two-piece fp16)"),
+     "time-axis fused QKV + gate projection with the attention's pre-norm inside, k (rotated) and v written as the "
+     "attention's fp16 pieces (fp32 via two-piece fp16)"),
     (r"gemm_h2_kernel(<|ILi)0", "fused QKV + gate projection (fp32 via two-piece fp16)"),
     (r"gemm_h2_batched_kernel(<|ILi)2", "mask estimator layer 1 + tanh, batched over bands (fp32 via two-piece fp16)"),
     (r"gemm_h2_batched_kernel(<|ILi)0", "mask estimator layer 2, batched over bands (fp32 via two-piece fp16)"),
@@ -63,6 +63,8 @@ ROLES = [
      "two-piece fp16)"),
     (r"attention_h2_kernel", "time-axis attention, L = 801 (fp32 via two-piece fp16)"),
     (r"attention_short_h2_kernel", "band-axis attention, L = 62 (fp32 via two-piece fp16)"),
+    (r"band_attention_fused_kernel", "band-axis pre-norm q, k, v and gate projection with the attention, L = 62, "
+     "one kernel (fp32 via two-piece fp16)"),
     (r"rmsnorm_h2_kernel", "FFN pre-norm, written as fp16 pieces for the FFN-up GEMM"),
     (r"gemm_split_kernel(<|ILi)4", "FFN up-projection + GELU-GLU (fp32 via split bf16)"),
     (r"gemm_split_kernel(<|ILi)3", "out projection / FFN down-projection + residual (fp32 via split bf16)"),

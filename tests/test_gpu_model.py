@@ -63,9 +63,12 @@ def test_transformer_block_kv_prescale_bit_identical(cfg2_models, rng, monkeypat
     attention stages them unscaled; VOCALARC_KV_PRESCALE=0 keeps the
     unscaled projection and the scaling multiplies in the attention.  Both
     must give the same bits (powers of two commute with the rotation and the
-    splits), on both axes and on a ragged length."""
+    splits), on both axes and on a ragged length.  The band axis runs its
+    projection and attention as the two kernels here (VOCALARC_BAND_FUSED=0:
+    the fused kernel always scales k and v in its epilogue)."""
     om, dm = cfg2_models
     x = rng.standard_normal((S, L, om.d.dim), dtype=np.float32)
+    monkeypatch.setenv("VOCALARC_BAND_FUSED", "0")
     outs = []
     for env in (None, "0"):
         if env is None:
@@ -76,7 +79,37 @@ def test_transformer_block_kv_prescale_bit_identical(cfg2_models, rng, monkeypat
         dm.transformer(1, axis, dx, S, L)
         outs.append(from_dev(dx))
     monkeypatch.delenv("VOCALARC_KV_PRESCALE", raising=False)
+    monkeypatch.delenv("VOCALARC_BAND_FUSED", raising=False)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("S,L", [(4, 62), (23, 62), (5, 64), (7, 17), (3, 1)])
+def test_band_attention_fused(cfg2_models, rng, monkeypatch, S, L):
+    """The band axis's pre-norm projection and attention in one kernel
+    (sequences of L <= 64 consecutive rows; q, k, v and the gate logits stay
+    on chip), against the oracle and against the two kernels it replaces
+    (VOCALARC_BAND_FUSED=0).  q, k and v are formed by the same expressions
+    as the QKV GEMM's; the gate logit is an fp32 dot product instead of the
+    split GEMM's column, so the two paths agree to a few fp32 roundings of the
+    gate, not bit for bit.  Odd S leaves a tile with one sequence, L = 64
+    fills a tile's 64 positions, L = 1 is a single key."""
+    om, dm = cfg2_models
+    x = rng.standard_normal((S, L, om.d.dim), dtype=np.float32)
+    outs = []
+    for env in (None, "0"):
+        if env is None:
+            monkeypatch.delenv("VOCALARC_BAND_FUSED", raising=False)
+        else:
+            monkeypatch.setenv("VOCALARC_BAND_FUSED", env)
+        dx = to_dev(x)
+        dm.transformer(1, 1, dx, S, L)
+        outs.append(from_dev(dx))
+    monkeypatch.delenv("VOCALARC_BAND_FUSED", raising=False)
+    ref = om.transformer(1, 1, x, S, L)
+    assert_close(ref, outs[0], rtol=1e-4, atol=1e-4, min_snr=100, what="fused band attention (oracle)")
+    scale = float(np.max(np.abs(outs[1])))
+    assert float(np.max(np.abs(outs[0] - outs[1]))) <= 1e-5 * scale
+    assert snr_db(outs[1], outs[0]) >= 120.0
 
 
 @pytest.mark.parametrize("windows", [1, 3])
