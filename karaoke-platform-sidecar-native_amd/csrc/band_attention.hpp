@@ -80,7 +80,7 @@ VH_DEVICE int ba_slot(int d) { return 8 * (4 * (d >> 5) + ((d >> 2) & 3)) + 4 * 
 __global__ __launch_bounds__(BA_THREADS, 2) __attribute__((amdgpu_waves_per_eu(4, 4))) void band_attention_fused_kernel(
     BandAttnArgs a) {
     __shared__ __attribute__((aligned(1024))) unsigned char region[BA_REGION];
-    __shared__ __attribute__((aligned(16))) float rsc[BA_ROWS];
+    __shared__ __attribute__((aligned(16))) float rsw[BA_THREADS / 64][32];
     __shared__ __attribute__((aligned(16))) float glog[BA_ROWS];
     __shared__ __attribute__((aligned(16))) float gw[BA_MAX_K];
 
@@ -214,21 +214,18 @@ __global__ __launch_bounds__(BA_THREADS, 2) __attribute__((amdgpu_waves_per_eu(4
         __syncthreads();
     }
 
-    // the row norm's scales (lanes li and li + 32 summed the two halves of
-    // row 32 rb + li; both waves of a row block hold the same sums) and the
-    // gate logits
+    // the row norm's scale of row 32 rb + li (lanes li and li + 32 summed the
+    // row's two halves; both waves of a row block hold the same sums), and the
+    // gate logits (read by the query waves after the barrier below)
     {
         const float tot = ss + __shfl_xor(ss, 32, 64);
         const float gd = gdot + __shfl_xor(gdot, 32, 64);
         const float rs = sqrtf((float)a.K) / sqrtf(tot + 1.0e-12f);
-        if (ch == 0 && lh == 0) {
-            rsc[32 * rb + li] = rs;
-            glog[32 * rb + li] = gated ? fmaf(gd, rs, gbias) : 0.0f;
-        }
+        if (lh == 0) rsw[wave][li] = rs;  // read back below by this wave only
+        if (ch == 0 && lh == 0) glog[32 * rb + li] = gated ? fmaf(gd, rs, gbias) : 0.0f;
     }
-    __syncthreads();
     // the wave's queries (below): 16 (wave % 4) + n of sequence wave / 4;
-    // their rotary table entries are loaded here, used after the next barrier
+    // their rotary table entries are loaded here, used after the barrier below
     const int n = lane & 15, g = lane >> 4;
     const int sq = wave >> 2;
     const int q = 16 * (wave & 3) + n;
@@ -241,10 +238,13 @@ __global__ __launch_bounds__(BA_THREADS, 2) __attribute__((amdgpu_waves_per_eu(4
     // lane is row 32 rb + 8 q4 + 4 lh + e, column li of its block
     {
         const int eu = -(ea + ew);
+        // each accumulator row's scale, as the wave wrote it above (LDS
+        // operations of one wave complete in order: no workgroup barrier)
+        __builtin_amdgcn_wave_barrier();
         floatx16 rsv;
 #pragma unroll
         for (int q4 = 0; q4 < 4; q4++) {
-            const floatx4 r4 = *reinterpret_cast<const floatx4 *>(&rsc[32 * rb + 8 * q4 + 4 * lh]);
+            const floatx4 r4 = *reinterpret_cast<const floatx4 *>(&rsw[wave][8 * q4 + 4 * lh]);
 #pragma unroll
             for (int e = 0; e < 4; e++) rsv[4 * q4 + e] = r4[e];
         }
@@ -378,12 +378,15 @@ __global__ __launch_bounds__(BA_THREADS, 2) __attribute__((amdgpu_waves_per_eu(4
     }
     float m = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++)
+    for (int kt = 0; kt < 4; kt++) {
+        if (16 * kt + 16 > a.L) {  // key tiles that reach past L (wave-uniform)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            if (16 * kt + 4 * g + r >= a.L) sc[kt][r] = -INFINITY;
-            m = fmaxf(m, sc[kt][r]);
+            for (int r = 0; r < 4; r++)
+                if (16 * kt + 4 * g + r >= a.L) sc[kt][r] = -INFINITY;
         }
+#pragma unroll
+        for (int r = 0; r < 4; r++) m = fmaxf(m, sc[kt][r]);
+    }
     m = fmaxf(m, __shfl_xor(m, 16, 64));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
     float l = 0.0f;
