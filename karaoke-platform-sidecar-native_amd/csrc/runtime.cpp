@@ -469,6 +469,13 @@ bool band_attention(hipStream_t s, const BandAttention &b, KernelTimer *t) {
                   b.lda, b.ld_out);
         return false;
     }
+    // every workgroup reads x while others write out: the two must not overlap
+    const uintptr_t x0 = (uintptr_t)b.x, x1 = x0 + (uintptr_t)((int64_t)b.S * b.L * b.lda * sizeof(float));
+    const uintptr_t o0 = (uintptr_t)b.out, o1 = o0 + (uintptr_t)((int64_t)b.S * b.L * b.ld_out * sizeof(float));
+    if (o0 < x1 && x0 < o1) {
+        set_error("band_attention: out overlaps x");
+        return false;
+    }
     BandAttnArgs a;
     a.x = b.x; a.lda = b.lda; a.K = b.K;
     a.W = b.W; a.bias = b.bias; a.gate_w = b.gate_w; a.gate_b = b.gate_b;

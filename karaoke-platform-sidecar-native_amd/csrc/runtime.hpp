@@ -173,7 +173,7 @@ bool gemm_h2_batched(hipStream_t s, const std::vector<GemmArgsH2> &gs, const Ope
 // max |x| (device float); bound: the fused projection's bound (device float,
 // within the two-piece attention's range); rope: the interleaved rotary table
 // of at least L positions (required).  K a multiple of 16 and at most
-// 512; heads * 64 a multiple of 128.
+// 512; heads * 64 a multiple of 128; out must not overlap x.
 struct BandAttention {
     const float *x; int lda, K;
     const void *W;
