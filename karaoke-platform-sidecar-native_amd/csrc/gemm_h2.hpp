@@ -93,10 +93,10 @@ VH_DEVICE void kv_pieces_epilogue(const GemmDescH2 &d, int row0, int n0, int li,
                                   const floatx16 (&acc)[1][4], floatx16 rs, floatx4 bpre) {
     const bool is_k = n0 < 2 * d.kv_inner;
     const int region = is_k ? d.kv_inner : 2 * d.kv_inner;  // first column of the k (v) region
-    const int B = d.rope_period, T = d.rope_len;
-    const int f0 = (row0 / B) % T;
-    const int f1 = f0 + 1 == T ? 0 : f0 + 1;
-    const int off_b = B - row0 % B;  // first row (within the wave's 32) of frame f1
+    const int B = d.rope_period;
+    // first row (within the wave's 32) of the second frame the rows span: its
+    // table entries are those tv holds in lanes 32-63
+    const int off_b = B - row0 % B;
     const bool even = (li & 1) == 0;
     typedef __attribute__((address_space(1))) char gchar;
     typedef __attribute__((address_space(1))) uint16_t gu16;
