@@ -374,8 +374,9 @@ __global__ __launch_bounds__(BA_THREADS, 2) __attribute__((amdgpu_waves_per_eu(4
             sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qm[st], sc[kt], 0, 0, 0);
             sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[st], sc[kt], 0, 0, 0);
         }
-        sc[kt] = sc[kt] * s_unscale;  // exact: a power of two
     }
+    // the scores stay scaled by 2^(ek+eq) until the exponent's fused multiply-add
+    // (the same values as unscaling them first: a power of two, exactly)
     float m = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
@@ -388,13 +389,13 @@ __global__ __launch_bounds__(BA_THREADS, 2) __attribute__((amdgpu_waves_per_eu(4
         for (int r = 0; r < 4; r++) m = fmaxf(m, sc[kt][r]);
     }
     m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64)) * s_unscale;
     float l = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            sc[kt][r] = __builtin_amdgcn_exp2f(sc[kt][r] - m);
+            sc[kt][r] = __builtin_amdgcn_exp2f(fmaf(sc[kt][r], s_unscale, -m));
             l += sc[kt][r];
         }
     l += __shfl_xor(l, 16, 64);
