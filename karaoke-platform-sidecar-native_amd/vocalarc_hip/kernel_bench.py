@@ -336,6 +336,20 @@ def main() -> int:
                 _emit("attention_short_h2", t, gbytes=S * L * 4 * 512 * 4 / 1e9, shape=f"S={S} L={L} H=8", reps=r,
                       device=r"attention_short_h2_kernel", extra={"algorithmic_GFLOP": round(gf, 2)})
             del qkv, o
+        # the default path's band axis: the pre-norm q, k, v and gate projection
+        # and the attention in one kernel, driven through a one-layer block at
+        # the pass's band-axis shape (live ms: the whole block; rocprof ms: the
+        # fused kernel alone)
+        d1 = CONFIG_DIMS.with_depth(1)
+        bmodel = native.Model(ctx, d1, pack.synthetic_pack(d1, 3))
+        S, L = 8 * 801, 62
+        xb = torch.randn(S * L, d1.dim, device=dev, generator=g)
+        gf = (2.0 * S * L * d1.dim * 3 * 512 + 4.0 * S * 8 * L * L * 64) / 1e9
+        _emit("band_attention_fused", _event_time(lambda: bmodel.transformer(0, 1, xb, S, L), r), gflop=gf,
+              shape=f"S={S} L={L} H=8, dim {d1.dim}", peak_tflops=FP16_TFLOPS, mc_products=3,
+              device=r"band_attention_fused_kernel", reps=r)
+        del xb
+        bmodel.close()
 
     if "c2" in groups or "c3" in groups:
         d = CONFIG_DIMS.with_depth(1)
