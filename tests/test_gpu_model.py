@@ -239,6 +239,30 @@ def test_forward_config_shape(cfg2_models):
     assert np.array_equal(from_dev(di), x - out)
 
 
+def test_forward_band_unfused(cfg2_models, monkeypatch):
+    """The whole forward with the band axis on the two separate kernels
+    (VOCALARC_BAND_FUSED=0: the QKV GEMM, then attention_short_h2_kernel)
+    against the oracle and against the default, fused path: the path the
+    pipeline no longer takes by default stays at the parity bar."""
+    om, dm = cfg2_models
+    x = audio.sine_mix(0.5, 13)
+    ref = om.forward(x)
+    outs = []
+    for env in ("0", None):
+        if env is None:
+            monkeypatch.delenv("VOCALARC_BAND_FUSED", raising=False)
+        else:
+            monkeypatch.setenv("VOCALARC_BAND_FUSED", env)
+        dv = empty_dev(x.shape)
+        dm.forward(to_dev(x), x.shape[1], dv)
+        outs.append(from_dev(dv))
+    monkeypatch.delenv("VOCALARC_BAND_FUSED", raising=False)
+    for out in outs:
+        assert float(np.max(np.abs(out.astype(np.float64) - ref))) <= 1e-4
+        assert snr_db(ref, out) >= 80
+    assert snr_db(outs[0], outs[1]) >= 110
+
+
 def test_forward_reference_shape(ref_models):
     om, dm = ref_models
     x = audio.sine_mix(0.2, 12)
